@@ -1,0 +1,184 @@
+"""ctypes binding for the CPU checker.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and by
+bench.py's cpu_baseline leg.  The product package (tailorquantkernel_amd) never
+imports it.
+
+* ``Oracle``  — liboracle.so, the C restatement of the reference's scalar Q8
+  attention path (oracle/tq_oracle.c).
+* ``Ref``     — oracle/_ref/libtqref{,_scalar}.so, the reference's own C sources
+  compiled by oracle/Makefile plus oracle/ref_driver.c.  Present only where it
+  was built; ``Ref.available()`` says whether it is.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+QK = 32
+BLOCK_Q8 = np.dtype([("d", "<f4"), ("q", "i1", (QK,))])
+assert BLOCK_Q8.itemsize == 36
+
+_f32p = C.POINTER(C.c_float)
+_vp = C.c_void_p
+_i = C.c_int
+_f = C.c_float
+_sz = C.c_size_t
+
+
+def ptr(a: np.ndarray | None):
+    """Data pointer of a C-contiguous array (None -> NULL)."""
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "arrays passed to C must be contiguous"
+    return a.ctypes.data
+
+
+def f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def blocks(n: int) -> np.ndarray:
+    return np.zeros(n, dtype=BLOCK_Q8)
+
+
+def dequant(b: np.ndarray) -> np.ndarray:
+    """block_q8 rows -> fp32 values (d * q), shape (..., nb*32)."""
+    vals = b["q"].astype(np.float32) * b["d"][..., None]
+    return vals.reshape(*b.shape[:-1], b.shape[-1] * QK) if b.ndim > 1 else vals.reshape(-1)
+
+
+def _load(path: str) -> C.CDLL:
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built (run `make -C oracle` / `make -C oracle ref`)")
+    return C.CDLL(path)
+
+
+class Oracle:
+    """The C restatement (liboracle.so)."""
+
+    def __init__(self, path: str | None = None):
+        self.lib = _load(path or os.path.join(HERE, "liboracle.so"))
+        L = self.lib
+        L.oracle_quantize_row_q8.argtypes = [_vp, _vp, _i]
+        L.oracle_rope_table.argtypes = [_vp, _vp, _i, _i, _f]
+        L.oracle_rope_apply.argtypes = [_vp, _i, _vp, _vp]
+        L.oracle_softmax.argtypes = [_vp, _i]
+        L.oracle_attn_scores_q8.argtypes = [_vp, _i, _vp, _i, _i, _f, _vp, _sz]
+        L.oracle_attn_accum_q8.argtypes = [_vp, _sz, _i, _vp, _i, _i, _vp, _sz]
+        L.oracle_attention_head_q8.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _vp, _vp]
+        L.oracle_store_kv_q8.argtypes = [_vp, _vp, _i, _i, _i, _i, _vp, _vp]
+        L.oracle_store_kv_q8.restype = _i
+        L.oracle_attend_q8.argtypes = [_vp, _vp, _i, _i, _i, _i, _vp, _i, _vp, _vp]
+        L.oracle_attend_q8.restype = _i
+        L.oracle_attention_qkv.argtypes = [_vp, _vp, _i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp, _vp]
+        L.oracle_attention_qkv.restype = _i
+        L.oracle_prefill_qkv.argtypes = [_vp, _vp, _i, _i, _i, _i, _f, _i, _i, _vp, _vp, _vp, _vp, _vp]
+        L.oracle_prefill_qkv.restype = _i
+
+    # --- element ops -------------------------------------------------------
+    def quantize_row_q8(self, x) -> np.ndarray:
+        x = f32(x).reshape(-1)
+        out = blocks(x.size // QK)
+        self.lib.oracle_quantize_row_q8(ptr(x), ptr(out), x.size)
+        return out
+
+    def rope_table(self, head_dim: int, pos: int, theta: float):
+        c = np.zeros(head_dim // 2, np.float32)
+        s = np.zeros(head_dim // 2, np.float32)
+        self.lib.oracle_rope_table(ptr(c), ptr(s), head_dim, pos, theta)
+        return c, s
+
+    def rope_apply(self, x, cos_t, sin_t) -> np.ndarray:
+        x = f32(x).copy()
+        self.lib.oracle_rope_apply(ptr(x), x.size, ptr(f32(cos_t)), ptr(f32(sin_t)))
+        return x
+
+    def softmax(self, x) -> np.ndarray:
+        x = f32(x).copy()
+        self.lib.oracle_softmax(ptr(x), x.size)
+        return x
+
+    def attn_scores_q8(self, q, g, k, n, nb, scale, scores, stride):
+        self.lib.oracle_attn_scores_q8(ptr(q), g, ptr(k), n, nb, scale, ptr(scores), stride)
+
+    def attn_accum_q8(self, w, w_stride, g, v, n, nb, out, out_stride):
+        self.lib.oracle_attn_accum_q8(ptr(w), w_stride, g, ptr(v), n, nb, ptr(out), out_stride)
+
+    def attention_head_q8(self, q, k, v, n, head_dim):
+        q = f32(q)
+        qq = blocks(head_dim // QK)
+        scores = np.zeros(max(n, 1), np.float32)
+        out = np.zeros(head_dim, np.float32)
+        self.lib.oracle_attention_head_q8(ptr(q), ptr(qq), ptr(k), ptr(v), n, head_dim,
+                                          ptr(scores), ptr(out))
+        return out, qq, scores
+
+    # --- layer-level -------------------------------------------------------
+    def attention_qkv(self, kc, vc, nq, nkv, hd, max_tokens, theta, pos, q, k, v):
+        """RoPE + store_kv + attend_q8 on flat caches (modified in place)."""
+        q = f32(q).copy()
+        k = f32(k).copy()
+        v = f32(v)
+        scores = np.zeros(nq * max_tokens, np.float32)
+        out = np.zeros(nq * hd, np.float32)
+        rc = self.lib.oracle_attention_qkv(ptr(kc), ptr(vc), nq, nkv, hd, max_tokens, theta, pos,
+                                           ptr(q), ptr(k), ptr(v), ptr(scores), ptr(out))
+        return rc, out
+
+    def prefill_qkv(self, kc, vc, nq, nkv, hd, max_tokens, theta, pos0, n, q, k, v):
+        q = f32(q).copy()
+        k = f32(k).copy()
+        v = f32(v)
+        scores = np.zeros(nq * max_tokens, np.float32)
+        out = np.zeros((max(n, 0), nq * hd), np.float32)
+        rc = self.lib.oracle_prefill_qkv(ptr(kc), ptr(vc), nq, nkv, hd, max_tokens, theta, pos0, n,
+                                         ptr(q), ptr(k), ptr(v), ptr(scores), ptr(out))
+        return rc, out
+
+    def attend_q8(self, kc, vc, nq, nkv, hd, max_tokens, q, pos):
+        scores = np.zeros(nq * max_tokens, np.float32)
+        out = np.zeros(nq * hd, np.float32)
+        rc = self.lib.oracle_attend_q8(ptr(kc), ptr(vc), nq, nkv, hd, max_tokens, ptr(f32(q)), pos,
+                                       ptr(scores), ptr(out))
+        return rc, out
+
+
+class Ref:
+    """The reference compiled from its own sources (oracle/_ref)."""
+
+    def __init__(self, scalar: bool = False):
+        name = "libtqref_scalar.so" if scalar else "libtqref.so"
+        self.lib = _load(os.path.join(HERE, "_ref", name))
+        L = self.lib
+        L.quantize_row_q8.argtypes = [_vp, _vp, _i]
+        L.rope_table.argtypes = [_vp, _vp, _i, _i, _f]
+        L.rope_apply.argtypes = [_vp, _i, _vp, _vp]
+        L.softmax.argtypes = [_vp, _i]
+        L.attn_scores_q8_scalar.argtypes = [_vp, _i, _vp, _i, _i, _f, _vp, _sz]
+        L.attn_accum_q8_scalar.argtypes = [_vp, _sz, _i, _vp, _i, _i, _vp, _sz]
+        L.attn_scores_q8.argtypes = [_vp, _i, _vp, _i, _i, _f, _vp, _sz]
+        L.attn_accum_q8.argtypes = [_vp, _sz, _i, _vp, _i, _i, _vp, _sz]
+        L.attention_head_q8.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _vp, _vp]
+        L.tqref_layer_run.argtypes = [_i, _i, _i, _i, _f, _f] + [_vp] * 6 + [_vp, _vp, _i, _i, _vp, _vp, _vp]
+        L.tqref_layer_run.restype = _i
+        L.tqref_layer_batch_run.argtypes = [_i, _i, _i, _i, _f, _f] + [_vp] * 6 + [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]
+        L.tqref_layer_batch_run.restype = _i
+        L.tqref_project_qkv.argtypes = [_i, _i, _i, _i, _f] + [_vp] * 5 + [_vp, _vp, _vp, _vp]
+        L.tqref_project_qkv.restype = _i
+        L.tqref_project_out.argtypes = [_i, _i, _i, _vp, _vp, _vp]
+        L.tqref_project_out.restype = _i
+        L.tqref_attention_qkv.argtypes = [_i, _i, _i, _i, _f, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]
+        L.tqref_attention_qkv.restype = _i
+        L.tqref_isa.restype = C.c_char_p
+
+    @staticmethod
+    def available(scalar: bool = False) -> bool:
+        name = "libtqref_scalar.so" if scalar else "libtqref.so"
+        return os.path.exists(os.path.join(HERE, "_ref", name))
+
+    def isa(self) -> str:
+        return self.lib.tqref_isa().decode()

@@ -1,0 +1,218 @@
+/* tq_oracle.c — CPU restatement of the reference's scalar Q8 attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker): loaded by tests/, by
+ * __graft_entry__.smoke() and by bench.py's cpu_baseline leg, never by the
+ * product libraries.  Built with gcc -O2 -ffp-contract=off (see Makefile) so
+ * that every a*b+c below is a rounded multiply followed by a rounded add, the
+ * same operation sequence the reference's scalar code executes on x86-64
+ * without -mfma.
+ *
+ * Pinning (tests/test_oracle.py): every function here is checked bit for bit
+ * against the compiled reference (oracle/_ref, when built) and against the
+ * committed golden vectors in tests/golden/ made from it, and also against
+ * closed forms: fp64 brute force for scores/accum/softmax/attention, RoPE
+ * identities, and quantizer invariants (max|q| = 127, ties to even).
+ */
+#include "tq_oracle.h"
+
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+/* kernel/quant_x.c:5-10.  Adding 1.5*2^23 moves v into the binade where the
+ * fp32 ulp is 1, so the add itself rounds v to the nearest integer with ties
+ * to even; the low mantissa bits then hold that integer (two's complement
+ * relative to the constant's bit pattern).  The int8 result is the low byte
+ * of the difference, which is also what a NaN or out-of-range input yields. */
+static int8_t rne_code(float v) {
+    const float shifted = v + 12582912.0f;
+    uint32_t bits;
+    memcpy(&bits, &shifted, sizeof bits);
+    return (int8_t)(uint8_t)((bits - 0x4B400000u) & 0xFFu);
+}
+
+/* kernel/quant_x.c:12-33: per 32 values, scale = amax/127, inverse 0 for an
+ * all-zero block, codes = RNE(x * inverse). */
+void oracle_quantize_row_q8(const float *x, block_q8 *out, int n) {
+    const int nblocks = n / QK;
+    for (int b = 0; b < nblocks; b++) {
+        const float *xb = x + (size_t)b * QK;
+        float amax = 0.0f;
+        for (int j = 0; j < QK; j++) {
+            float a = xb[j];
+            if (a < 0) a = -a;
+            if (a > amax) amax = a;
+        }
+        const float d = amax / 127.0f;
+        const float inv = (d != 0.0f) ? 1.0f / d : 0.0f;
+        out[b].d = d;
+        for (int j = 0; j < QK; j++) out[b].q[j] = rne_code(xb[j] * inv);
+    }
+}
+
+/* model/rope.c:4-12: freq_i = theta^(-2 i / hd), angle = pos * freq_i, with
+ * the exponent evaluated as (-2.0f * i) * (1.0f / hd) in fp32. */
+void oracle_rope_table(float *cos_t, float *sin_t, int head_dim, int pos, float theta) {
+    const float inv_hd = 1.0f / (float)head_dim;
+    for (int i = 0; i < head_dim / 2; i++) {
+        const float e = (-2.0f * (float)i) * inv_hd;
+        const float freq = powf(theta, e);
+        const float angle = (float)pos * freq;
+        cos_t[i] = cosf(angle);
+        sin_t[i] = sinf(angle);
+    }
+}
+
+/* model/rope.c:14-22: rotate-half pairing of i with i + hd/2. */
+void oracle_rope_apply(float *x, int head_dim, const float *cos_t, const float *sin_t) {
+    const int half = head_dim / 2;
+    for (int i = 0; i < half; i++) {
+        const float a = x[i], b = x[i + half];
+        x[i] = a * cos_t[i] - b * sin_t[i];
+        x[i + half] = a * sin_t[i] + b * cos_t[i];
+    }
+}
+
+/* model/softmax.c:4-23: max-subtracted expf, serial sum, scale by 1/sum. */
+void oracle_softmax(float *x, int n) {
+    if (n <= 0) return;
+    float m = x[0];
+    for (int i = 1; i < n; i++)
+        if (x[i] > m) m = x[i];
+    float total = 0.0f;
+    for (int i = 0; i < n; i++) {
+        x[i] = expf(x[i] - m);
+        total += x[i];
+    }
+    const float r = 1.0f / total;
+    for (int i = 0; i < n; i++) x[i] *= r;
+}
+
+/* model/attn_q8.c:17-34: per (token, head) an exact int32 dot per block,
+ * scaled by (qd * kd) and summed over blocks in order in fp32, times scale. */
+void oracle_attn_scores_q8(const block_q8 *q, int g, const block_q8 *k, int n, int nb,
+                           float scale, float *scores, size_t stride) {
+    for (int t = 0; t < n; t++) {
+        const block_q8 *krow = k + (size_t)t * nb;
+        for (int h = 0; h < g; h++) {
+            const block_q8 *qrow = q + (size_t)h * nb;
+            float acc = 0.0f;
+            for (int b = 0; b < nb; b++) {
+                int32_t dot = 0;
+                for (int j = 0; j < QK; j++)
+                    dot += (int32_t)qrow[b].q[j] * (int32_t)krow[b].q[j];
+                const float dd = qrow[b].d * krow[b].d;
+                acc += (float)dot * dd;
+            }
+            scores[(size_t)h * stride + t] = acc * scale;
+        }
+    }
+}
+
+/* model/attn_q8.c:36-54: out[h][j] = sum_t (w[h][t] * vd[t][b]) * code[t][j],
+ * zeroed first, tokens in order. */
+void oracle_attn_accum_q8(const float *w, size_t w_stride, int g, const block_q8 *v,
+                          int n, int nb, float *out, size_t out_stride) {
+    const int hd = nb * QK;
+    for (int h = 0; h < g; h++) {
+        float *o = out + (size_t)h * out_stride;
+        for (int j = 0; j < hd; j++) o[j] = 0.0f;
+        for (int t = 0; t < n; t++) {
+            const float wt = w[(size_t)h * w_stride + t];
+            const block_q8 *vrow = v + (size_t)t * nb;
+            for (int b = 0; b < nb; b++) {
+                const float a = wt * vrow[b].d;
+                for (int j = 0; j < QK; j++) o[b * QK + j] += a * (float)vrow[b].q[j];
+            }
+        }
+    }
+}
+
+/* model/attn_q8.c:78-90: one head (g = 1); q_q8 is an output. */
+void oracle_attention_head_q8(const float *q, block_q8 *q_q8, const block_q8 *k_cache,
+                              const block_q8 *v_cache, int n, int head_dim,
+                              float *scores, float *out) {
+    const int nb = head_dim / QK;
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    oracle_quantize_row_q8(q, q_q8, head_dim);
+    oracle_attn_scores_q8(q_q8, 1, k_cache, n, nb, scale, scores, (size_t)n);
+    oracle_softmax(scores, n);
+    oracle_attn_accum_q8(scores, (size_t)n, 1, v_cache, n, nb, out, (size_t)head_dim);
+}
+
+/* model/attention_layer.c:62-64 */
+static size_t slot_of(int max_tokens, int h, int pos) {
+    return (size_t)h * (size_t)max_tokens + (size_t)pos;
+}
+
+/* model/attention_layer.c:66-90, Q8 branch. */
+int oracle_store_kv_q8(block_q8 *k_cache, block_q8 *v_cache, int n_kv_heads, int head_dim,
+                       int max_tokens, int pos, const float *k, const float *v) {
+    if (pos < 0 || pos >= max_tokens) return -1;
+    const int nb = head_dim / QK;
+    for (int h = 0; h < n_kv_heads; h++) {
+        const size_t base = slot_of(max_tokens, h, pos) * (size_t)nb;
+        oracle_quantize_row_q8(k + (size_t)h * head_dim, k_cache + base, head_dim);
+        oracle_quantize_row_q8(v + (size_t)h * head_dim, v_cache + base, head_dim);
+    }
+    return 0;
+}
+
+/* model/attention_layer.c:125-150.  The group's q rows are quantized, scored
+ * against tokens 0..pos of their kv head, softmaxed per head and accumulated
+ * against V.  q head h reads kv head h / (n_q_heads / n_kv_heads). */
+int oracle_attend_q8(const block_q8 *k_cache, const block_q8 *v_cache, int n_q_heads,
+                     int n_kv_heads, int head_dim, int max_tokens, const float *q, int pos,
+                     float *scores, float *out) {
+    if (pos < 0 || pos >= max_tokens) return -1;
+    const int nb = head_dim / QK;
+    const int n = pos + 1;
+    const int group = n_q_heads / n_kv_heads;
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    const size_t stride = (size_t)max_tokens;
+    block_q8 qq[group * nb];
+
+    for (int kvh = 0; kvh < n_kv_heads; kvh++) {
+        const float *qg = q + (size_t)kvh * group * head_dim;
+        float *og = out + (size_t)kvh * group * head_dim;
+        float *sg = scores + (size_t)kvh * group * stride;
+        const size_t base = slot_of(max_tokens, kvh, 0) * (size_t)nb;
+        for (int h = 0; h < group; h++)
+            oracle_quantize_row_q8(qg + (size_t)h * head_dim, qq + (size_t)h * nb, head_dim);
+        oracle_attn_scores_q8(qq, group, k_cache + base, n, nb, scale, sg, stride);
+        for (int h = 0; h < group; h++) oracle_softmax(sg + (size_t)h * stride, n);
+        oracle_attn_accum_q8(sg, stride, group, v_cache + base, n, nb, og, (size_t)head_dim);
+    }
+    return 0;
+}
+
+int oracle_attention_qkv(block_q8 *k_cache, block_q8 *v_cache, int n_q_heads, int n_kv_heads,
+                         int head_dim, int max_tokens, float rope_theta, int pos,
+                         float *q, float *k, const float *v, float *scores, float *out) {
+    if (pos < 0 || pos >= max_tokens) return -1;
+    float cos_t[head_dim / 2], sin_t[head_dim / 2];
+    oracle_rope_table(cos_t, sin_t, head_dim, pos, rope_theta);
+    for (int h = 0; h < n_q_heads; h++)
+        oracle_rope_apply(q + (size_t)h * head_dim, head_dim, cos_t, sin_t);
+    for (int h = 0; h < n_kv_heads; h++)
+        oracle_rope_apply(k + (size_t)h * head_dim, head_dim, cos_t, sin_t);
+    oracle_store_kv_q8(k_cache, v_cache, n_kv_heads, head_dim, max_tokens, pos, k, v);
+    return oracle_attend_q8(k_cache, v_cache, n_q_heads, n_kv_heads, head_dim, max_tokens,
+                            q, pos, scores, out);
+}
+
+int oracle_prefill_qkv(block_q8 *k_cache, block_q8 *v_cache, int n_q_heads, int n_kv_heads,
+                       int head_dim, int max_tokens, float rope_theta, int pos0, int n,
+                       float *q, float *k, const float *v, float *scores, float *out) {
+    if (n <= 0) return -1;
+    if (pos0 < 0 || pos0 + n > max_tokens) return -1;
+    const size_t qdim = (size_t)n_q_heads * head_dim;
+    const size_t kvdim = (size_t)n_kv_heads * head_dim;
+    for (int i = 0; i < n; i++) {
+        int rc = oracle_attention_qkv(k_cache, v_cache, n_q_heads, n_kv_heads, head_dim,
+                                      max_tokens, rope_theta, pos0 + i, q + i * qdim,
+                                      k + i * kvdim, v + i * kvdim, scores, out + i * qdim);
+        if (rc != 0) return rc;
+    }
+    return 0;
+}

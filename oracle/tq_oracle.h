@@ -1,0 +1,76 @@
+/* tq_oracle.h — CPU restatement of the reference's scalar Q8 attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP path is
+ * compared against.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it; the product (libtqhip.so, libtqattn.so) never
+ * links, loads or calls it.
+ *
+ * Every function restates one reference function (cited file:line) from its
+ * arithmetic, in the same floating-point operation order, and is compiled
+ * without FMA contraction (-ffp-contract=off), as the reference's scalar
+ * sources are (no -mfma for them).  Cache layout is the reference's flat one:
+ * [n_kv_heads][max_tokens][head_dim/32] block_q8 for K and for V, with
+ * slot(h, pos) = h*max_tokens + pos (model/attention_layer.c:62-64).
+ */
+#ifndef TQ_ORACLE_H
+#define TQ_ORACLE_H
+
+#include <stddef.h>
+#include "../include/tq/block_q8.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* kernel/quant_x.c:12-33 */
+void oracle_quantize_row_q8(const float *x, block_q8 *out, int n);
+
+/* model/rope.c:4-12 and :14-22 */
+void oracle_rope_table(float *cos_t, float *sin_t, int head_dim, int pos, float theta);
+void oracle_rope_apply(float *x, int head_dim, const float *cos_t, const float *sin_t);
+
+/* model/softmax.c:4-23 */
+void oracle_softmax(float *x, int n);
+
+/* model/attn_q8.c:17-34 */
+void oracle_attn_scores_q8(const block_q8 *q, int g, const block_q8 *k, int n, int nb,
+                           float scale, float *scores, size_t stride);
+
+/* model/attn_q8.c:36-54 */
+void oracle_attn_accum_q8(const float *w, size_t w_stride, int g, const block_q8 *v,
+                          int n, int nb, float *out, size_t out_stride);
+
+/* model/attn_q8.c:78-90 */
+void oracle_attention_head_q8(const float *q, block_q8 *q_q8, const block_q8 *k_cache,
+                              const block_q8 *v_cache, int n, int head_dim,
+                              float *scores, float *out);
+
+/* model/attention_layer.c:66-90, TQ_KV_Q8 branch: k is post-RoPE. */
+int oracle_store_kv_q8(block_q8 *k_cache, block_q8 *v_cache, int n_kv_heads, int head_dim,
+                       int max_tokens, int pos, const float *k, const float *v);
+
+/* model/attention_layer.c:125-150 (attend_q8), serial over kv heads.
+ * scores: n_q_heads * max_tokens floats, as the reference's ctx->scores. */
+int oracle_attend_q8(const block_q8 *k_cache, const block_q8 *v_cache, int n_q_heads,
+                     int n_kv_heads, int head_dim, int max_tokens, const float *q, int pos,
+                     float *scores, float *out);
+
+/* The attention core of attention_layer (model/attention_layer.c:172,186-191):
+ * pos range check, rope_table(pos), RoPE on q and k, store_kv, attend_q8.
+ * q and k are post-norm and pre-RoPE; q is rotated in place.  Returns -1 for a
+ * bad pos before any write, else 0. */
+int oracle_attention_qkv(block_q8 *k_cache, block_q8 *v_cache, int n_q_heads, int n_kv_heads,
+                         int head_dim, int max_tokens, float rope_theta, int pos,
+                         float *q, float *k, const float *v, float *scores, float *out);
+
+/* The attention loop of attention_layer_batch (model/attention_layer.c:203-204,
+ * 221-236): n tokens at pos0..pos0+n-1, token-major q/k/v/out. */
+int oracle_prefill_qkv(block_q8 *k_cache, block_q8 *v_cache, int n_q_heads, int n_kv_heads,
+                       int head_dim, int max_tokens, float rope_theta, int pos0, int n,
+                       float *q, float *k, const float *v, float *scores, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TQ_ORACLE_H */
