@@ -1,0 +1,178 @@
+/* tq_hip.h — C-ABI of libtqhip.so, the MI355X (gfx950) Q8 GQA attention path.
+ *
+ * Plain pointers and sizes only.  Every call returns 0 on success or a
+ * negative code (TQ_HIP_E*); HIP runtime errors come back as
+ * TQ_HIP_EHIP_BASE - hipError_t.  No call aborts the process.
+ *
+ * Two kinds of entry point:
+ *   - synchronous ones take HOST buffers, copy them in, run, copy results out
+ *     and return with the results valid (the boundary of attention_layer);
+ *   - *_async ones take DEVICE buffers and a stream (hipStream_t as void*,
+ *     NULL = the cache's own stream) and only enqueue work.
+ *
+ * KV storage is an HBM-resident paged cache.  A page holds TQ_HIP_PAGE_TOKENS
+ * consecutive positions of one sequence for every kv head, K then V:
+ *   page[kvh][0=K,1=V][16 tokens][head_dim/32] block_q8
+ * so one (page, kv head) is a contiguous 2 * 16 * head_dim/32 * 36 byte run
+ * (4,608 B at head_dim 128).  Each sequence owns a page table (logical page ->
+ * physical page).  Within a token row the bytes are exactly the reference's
+ * block_q8 row (model/attention_layer.c:62-64, packer/packer.h:7-11).
+ */
+#ifndef TQ_HIP_H
+#define TQ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "block_q8.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TQ_HIP_PAGE_TOKENS 16
+
+#define TQ_HIP_OK 0
+#define TQ_HIP_EINVAL (-1)     /* argument out of range: pos, n, seq, shape     */
+#define TQ_HIP_ENOMEM (-2)     /* device or host allocation failed              */
+#define TQ_HIP_ETYPE (-3)      /* unsupported head_dim / group size             */
+#define TQ_HIP_ENODEV (-4)     /* no usable gfx950 device                        */
+#define TQ_HIP_ENOTREADY (-5)  /* sequence has no page for a requested position  */
+#define TQ_HIP_EHIP_BASE (-1000)
+
+/* ---- device and plumbing ------------------------------------------------ */
+
+/* Select the device for this thread and check it is gfx950.  Idempotent. */
+int tq_hip_init(int device);
+const char *tq_hip_strerror(int code);
+/* Name of the current device's architecture (e.g. "gfx950:sramecc+:xnack-"). */
+int tq_hip_device_arch(char *buf, size_t len);
+
+int tq_hip_malloc(void **ptr, size_t bytes);
+int tq_hip_free(void *ptr);
+/* stream NULL: synchronous copy. */
+int tq_hip_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
+int tq_hip_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
+int tq_hip_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream);
+int tq_hip_stream_synchronize(void *stream);
+int tq_hip_device_synchronize(void);
+
+/* ---- kernel-level ops on flat block_q8 arrays (device pointers) --------- */
+
+/* kernel/quant_x.c:12-33 quantize_row_q8: x[n] -> out[n/32], bit-exact. */
+int tq_hip_quantize_row_q8(const float *x, block_q8 *out, int n, void *stream);
+
+/* model/rope.c:14-22 rope_apply on n_heads consecutive heads of x, in place,
+ * with a host-computed cos/sin table of head_dim/2 entries (bit-exact). */
+int tq_hip_rope_apply(float *x, int n_heads, int head_dim, const float *cos_t,
+                      const float *sin_t, void *stream);
+
+/* model/attn_q8.c:17-34 attn_scores_q8(_scalar): scores[gi*stride + t] for
+ * t < n, gi < g; nothing at or past n is written.  Bit-exact vs the scalar. */
+int tq_hip_attn_scores_q8(const block_q8 *q, int g, const block_q8 *k, int n, int nb,
+                          float scale, float *scores, size_t stride, void *stream);
+
+/* model/attn_q8.c:36-54 attn_accum_q8(_scalar): out[gi*out_stride + j], j < nb*32,
+ * zeroed first; nothing past nb*32 is written.  Bit-exact vs the scalar. */
+int tq_hip_attn_accum_q8(const float *w, size_t w_stride, int g, const block_q8 *v, int n,
+                         int nb, float *out, size_t out_stride, void *stream);
+
+/* model/softmax.c:4-23 softmax on `rows` rows of n values, row r at x + r*stride. */
+int tq_hip_softmax(float *x, int n, int rows, size_t stride, void *stream);
+
+/* model/attn_q8.c:78-90 attention_head_q8: writes q_q8 (head_dim/32 blocks),
+ * scores[n] (the softmax weights) and out[head_dim]. */
+int tq_hip_attention_head_q8(const float *q, block_q8 *q_q8, const block_q8 *k_cache,
+                             const block_q8 *v_cache, int n, int head_dim, float *scores,
+                             float *out, void *stream);
+
+/* ---- paged KV cache -------------------------------------------------------
+ * Replaces tq_kv_cache_init / tq_kv_cache_free (model/kv_cache.c:17-48) for a
+ * device-resident Q8 cache; the reference's flat layout becomes one sequence
+ * whose page table is the identity. */
+
+typedef struct tq_hip_kv tq_hip_kv;
+
+typedef struct {
+    int n_q_heads;          /* query heads (sizes decode scratch)        */
+    int n_kv_heads;
+    int head_dim;           /* 32, 64, 128 or 256                        */
+    int n_pages;            /* physical pages in the pool                */
+    int max_seqs;           /* sequences (page tables)                   */
+    int max_pages_per_seq;  /* logical pages per sequence                */
+} tq_hip_kv_desc;
+
+/* Allocate the pool (zero-filled), page tables (all -1) and a stream on the
+ * current device.  Returns TQ_HIP_EINVAL for a bad shape (same conditions as
+ * tq_attn_validate: model/attention_layer.c:11,16-17), TQ_HIP_ETYPE for a
+ * head_dim or group size the kernels do not cover, TQ_HIP_ENOMEM on OOM. */
+int tq_hip_kv_create(tq_hip_kv **kv, const tq_hip_kv_desc *desc);
+/* Idempotent; NULL is fine. */
+void tq_hip_kv_destroy(tq_hip_kv *kv);
+/* Map logical pages 0..n_pages-1 of `seq` to the given physical pages (host
+ * array); entries of -1 unmap.  Pages past n_pages are unmapped. */
+int tq_hip_kv_set_pages(tq_hip_kv *kv, int seq, const int32_t *pages, int n_pages);
+/* Tokens addressable in `seq` (mapped logical pages * 16), or < 0. */
+int tq_hip_kv_capacity(const tq_hip_kv *kv, int seq);
+void *tq_hip_kv_stream(tq_hip_kv *kv);
+/* Device base and size of the pool; device pointer of the page tables
+ * ([max_seqs][max_pages_per_seq] int32). */
+int tq_hip_kv_pool(tq_hip_kv *kv, void **base, size_t *bytes, int32_t **page_table);
+
+/* Copy rows [pos0, pos0+n) of `seq` between the cache and host block_q8
+ * arrays laid out [n_kv_heads][n][head_dim/32] (the reference's flat layout
+ * when pos0 = 0 and n = max_tokens).  Either of k/v may be NULL. */
+int tq_hip_kv_write(tq_hip_kv *kv, int seq, int pos0, int n, const block_q8 *k, const block_q8 *v);
+int tq_hip_kv_read(tq_hip_kv *kv, int seq, int pos0, int n, block_q8 *k, block_q8 *v);
+
+/* ---- append: store_kv, Q8 branch (model/attention_layer.c:66-90) fused with
+ * rope_heads on k (:188).  k, v: [n_kv_heads * head_dim] fp32; with cos/sin
+ * (head_dim/2 each) k is post-norm and pre-RoPE, with NULL it is already
+ * rotated.  K and V codes and scales are bit-exact with quantize_row_q8. */
+int tq_hip_kv_append(tq_hip_kv *kv, int seq, int pos, const float *k, const float *v,
+                     const float *cos_t, const float *sin_t);
+/* Device form for n_rows rows: row r goes to sequence d_seq[r] at position
+ * d_pos[r]; k/v rows at r * n_kv_heads * head_dim; cos/sin rows at r *
+ * head_dim/2 (or NULL).  Rows whose position has no mapped page are skipped. */
+int tq_hip_kv_append_async(tq_hip_kv *kv, int n_rows, const int32_t *d_seq,
+                           const int32_t *d_pos, const float *d_k, const float *d_v,
+                           const float *d_cos, const float *d_sin, void *stream);
+
+/* ---- decode: attend_q8 (model/attention_layer.c:125-150) -----------------
+ * For query i: q heads at q + i*n_q_heads*head_dim (post-RoPE, or pre-RoPE
+ * with a cos/sin row), quantized with quantize_row_q8; q head h attends kv
+ * head h / (n_q_heads/n_kv_heads) over tokens [0, len) of its sequence;
+ * out[i][h][head_dim] fp32.  Split-K over the context with an online softmax;
+ * partials are combined in a fixed order, so results do not depend on timing. */
+int tq_hip_attend(tq_hip_kv *kv, int seq, int pos, const float *q, const float *cos_t,
+                  const float *sin_t, float *out);
+/* max_len: an upper bound of every d_len[i] (sizes the grid). */
+int tq_hip_decode_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_len,
+                        int max_len, const float *d_q, const float *d_cos, const float *d_sin,
+                        float *d_out, void *stream);
+
+/* ---- decode step: the attention core of attention_layer
+ * (model/attention_layer.c:186-191): RoPE on q and k, store_kv of token
+ * d_pos[i] of sequence d_seq[i], then attend over [0, d_pos[i]].  The new
+ * token's K/V are quantized once, written to the cache and used by the same
+ * launch.  max_pos: an upper bound of every d_pos[i]. */
+int tq_hip_decode_step_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq,
+                             const int32_t *d_pos, int max_pos, const float *d_q,
+                             const float *d_k, const float *d_v, const float *d_cos,
+                             const float *d_sin, float *d_out, void *stream);
+
+/* ---- prefill: the attention loop of attention_layer_batch
+ * (model/attention_layer.c:203-204,221-236): tokens pos0..pos0+n-1 of `seq`,
+ * each stored then attending causally to [0, pos0+i].  q [n][nq*hd], k/v
+ * [n][nkv*hd] (k pre-RoPE), cos/sin [n][hd/2], out [n][nq*hd]. */
+int tq_hip_prefill(tq_hip_kv *kv, int seq, int pos0, int n, const float *q, const float *k,
+                   const float *v, const float *cos_t, const float *sin_t, float *out);
+int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d_q,
+                         const float *d_k, const float *d_v, const float *d_cos,
+                         const float *d_sin, float *d_out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TQ_HIP_H */

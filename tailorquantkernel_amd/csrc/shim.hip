@@ -1,0 +1,565 @@
+// shim.hip — the extern "C" boundary of libtqhip.so (declared in
+// include/tq/tq_hip.h): device selection, error mapping, the paged KV cache
+// object, split-K planning, synchronous host-buffer entry points and async
+// device-buffer entry points.  No entry point aborts; HIP errors come back as
+// TQ_HIP_EHIP_BASE - hipError_t.
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "tq_common.hpp"
+
+struct tq_hip_kv {
+    tq_hip_kv_desc desc;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    unsigned char *pool = nullptr;
+    size_t pool_bytes = 0;
+    int32_t *d_page_table = nullptr;
+    std::vector<int32_t> h_page_table;
+    tq::PagedView view{};
+    float *partials = nullptr;      // split-K scratch, grown on demand
+    size_t partials_bytes = 0;
+    unsigned char *stage = nullptr; // device staging for the synchronous calls
+    size_t stage_bytes = 0;
+};
+
+namespace {
+
+int herr(hipError_t e) { return e == hipSuccess ? TQ_HIP_OK : TQ_HIP_EHIP_BASE - (int)e; }
+
+#define TQ_TRY(expr)                          \
+    do {                                      \
+        const hipError_t e_ = (expr);         \
+        if (e_ != hipSuccess) return herr(e_); \
+    } while (0)
+
+hipStream_t pick(tq_hip_kv *kv, void *stream) {
+    return stream ? static_cast<hipStream_t>(stream) : kv->stream;
+}
+
+// Work-groups the decode aims for: several per CU of the 256-CU MI355X so
+// that each CU streams from a few splits at once.  Overridable for sweeps.
+int decode_wg_target() {
+    static int v = [] {
+        const char *s = getenv("TQ_HIP_DECODE_WG_TARGET");
+        const int x = s ? atoi(s) : 0;
+        return x > 0 ? x : 1024;
+    }();
+    return v;
+}
+
+int decode_max_splits() {
+    static int v = [] {
+        const char *s = getenv("TQ_HIP_DECODE_MAX_SPLITS");
+        const int x = s ? atoi(s) : 0;
+        return x > 0 ? x : 64;
+    }();
+    return v;
+}
+
+// Split the context of every query into n_splits ranges of split_tokens
+// (a multiple of the kernel's sub-chunk) for n_q queries of up to max_len.
+void plan_splits(const tq_hip_kv *kv, int n_q, int max_len, int *split_tokens, int *n_splits) {
+    const int tsub = tq_decode_tsub(kv->desc.head_dim);
+    const int chunks = std::max(1, (max_len + tsub - 1) / tsub);
+    const long pairs = (long)n_q * kv->desc.n_kv_heads;
+    long want = (decode_wg_target() + pairs - 1) / pairs;
+    want = std::max(1L, std::min<long>(want, decode_max_splits()));
+    want = std::min<long>(want, chunks);
+    const int per = (int)((chunks + want - 1) / want);
+    *split_tokens = per * tsub;
+    *n_splits = (chunks + per - 1) / per;
+}
+
+int ensure_partials(tq_hip_kv *kv, size_t bytes) {
+    if (bytes <= kv->partials_bytes) return TQ_HIP_OK;
+    if (kv->partials) {
+        TQ_TRY(hipStreamSynchronize(kv->stream));
+        TQ_TRY(hipFree(kv->partials));
+        kv->partials = nullptr;
+        kv->partials_bytes = 0;
+    }
+    if (hipMalloc(&kv->partials, bytes) != hipSuccess) {
+        kv->partials = nullptr;
+        return TQ_HIP_ENOMEM;
+    }
+    kv->partials_bytes = bytes;
+    return TQ_HIP_OK;
+}
+
+int ensure_stage(tq_hip_kv *kv, size_t bytes) {
+    if (bytes <= kv->stage_bytes) return TQ_HIP_OK;
+    if (kv->stage) {
+        TQ_TRY(hipStreamSynchronize(kv->stream));
+        TQ_TRY(hipFree(kv->stage));
+        kv->stage = nullptr;
+        kv->stage_bytes = 0;
+    }
+    if (hipMalloc(&kv->stage, bytes) != hipSuccess) {
+        kv->stage = nullptr;
+        return TQ_HIP_ENOMEM;
+    }
+    kv->stage_bytes = bytes;
+    return TQ_HIP_OK;
+}
+
+// Bump allocator over the staging buffer (256-byte aligned pieces).
+struct Stage {
+    size_t used = 0;
+    size_t take(size_t bytes) {
+        const size_t at = used;
+        used += (bytes + 255) & ~(size_t)255;
+        return at;
+    }
+};
+
+int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_len, int len_plus,
+                  int seq_const, int pos0, int max_len, const float *d_q, const float *d_cos,
+                  const float *d_sin, const float *d_k, const float *d_v, float *d_out,
+                  hipStream_t s) {
+    if (n_q <= 0) return TQ_HIP_OK;
+    // queries and kv heads are grid dimensions y/z (at most 65535 each)
+    if (n_q > 65535 || kv->desc.n_kv_heads > 65535) return TQ_HIP_EINVAL;
+    if (max_len <= 0 || !d_q || !d_out) return TQ_HIP_EINVAL;
+    if ((d_cos == nullptr) != (d_sin == nullptr)) return TQ_HIP_EINVAL;
+    const tq_hip_kv_desc &D = kv->desc;
+    TqDecodeArgs a{};
+    a.view = kv->view;
+    a.seq_of = d_seq;
+    a.len_of = d_len;
+    a.len_plus = len_plus;
+    a.seq_const = seq_const;
+    a.pos0 = pos0;
+    a.q = d_q;
+    a.cos_t = d_cos;
+    a.sin_t = d_sin;
+    a.k_new = d_k;
+    a.v_new = d_v;
+    a.out = d_out;
+    a.n_q = n_q;
+    a.n_q_heads = D.n_q_heads;
+    a.n_kv_heads = D.n_kv_heads;
+    a.head_dim = D.head_dim;
+    a.scale = 1.0f / sqrtf((float)D.head_dim);  // model/attention_layer.c:131
+    plan_splits(kv, n_q, max_len, &a.split_tokens, &a.n_splits);
+    if (a.n_splits > 1) {
+        const int g = D.n_q_heads / D.n_kv_heads;
+        const size_t bytes = (size_t)n_q * D.n_kv_heads * a.n_splits * g * (D.head_dim + 2) * sizeof(float);
+        const int rc = ensure_partials(kv, bytes);
+        if (rc != TQ_HIP_OK) return rc;
+        a.partials = kv->partials;
+    }
+    return herr(tq_launch_decode(a, s));
+}
+
+bool seq_ok(const tq_hip_kv *kv, int seq) { return kv && seq >= 0 && seq < kv->desc.max_seqs; }
+
+int capacity_of(const tq_hip_kv *kv, int seq) {
+    int mapped = 0;
+    const int32_t *row = kv->h_page_table.data() + (size_t)seq * kv->desc.max_pages_per_seq;
+    while (mapped < kv->desc.max_pages_per_seq && row[mapped] >= 0) mapped++;
+    return mapped * TQ_HIP_PAGE_TOKENS;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tq_hip_init(int device) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return TQ_HIP_ENODEV;
+    if (device < 0 || device >= n) return TQ_HIP_EINVAL;
+    TQ_TRY(hipSetDevice(device));
+    hipDeviceProp_t p;
+    TQ_TRY(hipGetDeviceProperties(&p, device));
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0) return TQ_HIP_ENODEV;
+    return TQ_HIP_OK;
+}
+
+const char *tq_hip_strerror(int code) {
+    switch (code) {
+        case TQ_HIP_OK: return "ok";
+        case TQ_HIP_EINVAL: return "argument out of range";
+        case TQ_HIP_ENOMEM: return "out of memory";
+        case TQ_HIP_ETYPE: return "unsupported head_dim or group size";
+        case TQ_HIP_ENODEV: return "no gfx950 device";
+        case TQ_HIP_ENOTREADY: return "position has no mapped page";
+        default: break;
+    }
+    if (code <= TQ_HIP_EHIP_BASE) return hipGetErrorString((hipError_t)(TQ_HIP_EHIP_BASE - code));
+    return "unknown error";
+}
+
+int tq_hip_device_arch(char *buf, size_t len) {
+    if (!buf || len == 0) return TQ_HIP_EINVAL;
+    int dev = 0;
+    TQ_TRY(hipGetDevice(&dev));
+    hipDeviceProp_t p;
+    TQ_TRY(hipGetDeviceProperties(&p, dev));
+    strncpy(buf, p.gcnArchName, len - 1);
+    buf[len - 1] = 0;
+    return TQ_HIP_OK;
+}
+
+int tq_hip_malloc(void **ptr, size_t bytes) {
+    if (!ptr) return TQ_HIP_EINVAL;
+    *ptr = nullptr;
+    if (bytes == 0) return TQ_HIP_OK;
+    const hipError_t e = hipMalloc(ptr, bytes);
+    if (e == hipErrorOutOfMemory) return TQ_HIP_ENOMEM;
+    return herr(e);
+}
+
+int tq_hip_free(void *ptr) { return ptr ? herr(hipFree(ptr)) : TQ_HIP_OK; }
+
+int tq_hip_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream) {
+    if (bytes == 0) return TQ_HIP_OK;
+    if (!dst || !src) return TQ_HIP_EINVAL;
+    if (!stream) return herr(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return herr(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
+}
+
+int tq_hip_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream) {
+    if (bytes == 0) return TQ_HIP_OK;
+    if (!dst || !src) return TQ_HIP_EINVAL;
+    if (!stream) return herr(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return herr(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream));
+}
+
+int tq_hip_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream) {
+    if (bytes == 0) return TQ_HIP_OK;
+    if (!dst || !src) return TQ_HIP_EINVAL;
+    if (!stream) return herr(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+    return herr(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+}
+
+int tq_hip_stream_synchronize(void *stream) { return herr(hipStreamSynchronize((hipStream_t)stream)); }
+int tq_hip_device_synchronize(void) { return herr(hipDeviceSynchronize()); }
+
+// ---- kernel-level ops ------------------------------------------------------
+
+int tq_hip_quantize_row_q8(const float *x, block_q8 *out, int n, void *stream) {
+    if (n < 0 || (n > 0 && (!x || !out))) return TQ_HIP_EINVAL;
+    return herr(tq_launch_quantize(x, out, n, (hipStream_t)stream));
+}
+
+int tq_hip_rope_apply(float *x, int n_heads, int head_dim, const float *cos_t, const float *sin_t,
+                      void *stream) {
+    if (n_heads < 0 || head_dim < 2 || (head_dim & 1) || !x || !cos_t || !sin_t) return TQ_HIP_EINVAL;
+    return herr(tq_launch_rope(x, n_heads, head_dim, cos_t, sin_t, (hipStream_t)stream));
+}
+
+int tq_hip_attn_scores_q8(const block_q8 *q, int g, const block_q8 *k, int n, int nb, float scale,
+                          float *scores, size_t stride, void *stream) {
+    if (g <= 0 || n < 0 || nb <= 0 || stride < (size_t)n || !q || (n > 0 && (!k || !scores)))
+        return TQ_HIP_EINVAL;
+    return herr(tq_launch_scores(q, g, k, n, nb, scale, scores, stride, (hipStream_t)stream));
+}
+
+int tq_hip_attn_accum_q8(const float *w, size_t w_stride, int g, const block_q8 *v, int n, int nb,
+                         float *out, size_t out_stride, void *stream) {
+    if (g <= 0 || n < 0 || nb <= 0 || out_stride < (size_t)nb * QK || w_stride < (size_t)n || !out ||
+        (n > 0 && (!w || !v)))
+        return TQ_HIP_EINVAL;
+    return herr(tq_launch_accum(w, w_stride, g, v, n, nb, out, out_stride, (hipStream_t)stream));
+}
+
+int tq_hip_softmax(float *x, int n, int rows, size_t stride, void *stream) {
+    if (n < 0 || rows < 0 || (rows > 1 && stride < (size_t)n) || (n > 0 && rows > 0 && !x))
+        return TQ_HIP_EINVAL;
+    return herr(tq_launch_softmax(x, n, rows, stride, (hipStream_t)stream));
+}
+
+int tq_hip_attention_head_q8(const float *q, block_q8 *q_q8, const block_q8 *k_cache,
+                             const block_q8 *v_cache, int n, int head_dim, float *scores, float *out,
+                             void *stream) {
+    if (head_dim <= 0 || head_dim % QK || n <= 0 || !q || !q_q8 || !k_cache || !v_cache || !scores || !out)
+        return TQ_HIP_EINVAL;
+    const hipStream_t s = (hipStream_t)stream;
+    const int nb = head_dim / QK;
+    const float scale = 1.0f / sqrtf((float)head_dim);  // model/attn_q8.c:83
+    TQ_TRY(tq_launch_quantize(q, q_q8, head_dim, s));
+    TQ_TRY(tq_launch_scores(q_q8, 1, k_cache, n, nb, scale, scores, (size_t)n, s));
+    TQ_TRY(tq_launch_softmax(scores, n, 1, (size_t)n, s));
+    return herr(tq_launch_accum(scores, (size_t)n, 1, v_cache, n, nb, out, (size_t)head_dim, s));
+}
+
+// ---- paged cache -------------------------------------------------------------
+
+int tq_hip_kv_create(tq_hip_kv **out, const tq_hip_kv_desc *desc) {
+    if (!out) return TQ_HIP_EINVAL;
+    *out = nullptr;
+    if (!desc) return TQ_HIP_EINVAL;
+    const tq_hip_kv_desc D = *desc;
+    // model/attention_layer.c:11,16-17 (tq_attn_validate -8, -5, -6)
+    if (D.n_q_heads <= 0 || D.n_kv_heads <= 0 || D.head_dim <= 0) return TQ_HIP_EINVAL;
+    if (D.n_q_heads % D.n_kv_heads != 0 || D.head_dim % QK != 0) return TQ_HIP_EINVAL;
+    if (D.n_pages <= 0 || D.max_seqs <= 0 || D.max_pages_per_seq <= 0) return TQ_HIP_EINVAL;
+    if (!tq_decode_supported(D.head_dim, D.n_q_heads / D.n_kv_heads)) return TQ_HIP_ETYPE;
+
+    tq_hip_kv *kv = new (std::nothrow) tq_hip_kv();
+    if (!kv) return TQ_HIP_ENOMEM;
+    kv->desc = D;
+    int rc = herr(hipGetDevice(&kv->device));
+    const int nb = D.head_dim / QK;
+    tq::PagedView &v = kv->view;
+    v.nb = nb;
+    v.row_bytes = (size_t)nb * sizeof(block_q8);
+    v.kv_chunk = (size_t)TQ_HIP_PAGE_TOKENS * v.row_bytes;
+    v.head_run = 2 * v.kv_chunk;
+    v.page_bytes = (size_t)D.n_kv_heads * v.head_run;
+    v.n_pages = D.n_pages;
+    v.max_seqs = D.max_seqs;
+    v.max_pages = D.max_pages_per_seq;
+    v.n_kv_heads = D.n_kv_heads;
+    kv->pool_bytes = (size_t)D.n_pages * v.page_bytes;
+    const size_t pt_entries = (size_t)D.max_seqs * D.max_pages_per_seq;
+    try {
+        kv->h_page_table.assign(pt_entries, -1);
+    } catch (...) {
+        delete kv;
+        return TQ_HIP_ENOMEM;
+    }
+    if (rc == TQ_HIP_OK) rc = herr(hipStreamCreateWithFlags(&kv->stream, hipStreamNonBlocking));
+    if (rc == TQ_HIP_OK && hipMalloc(&kv->pool, kv->pool_bytes) != hipSuccess) {
+        kv->pool = nullptr;
+        rc = TQ_HIP_ENOMEM;
+    }
+    if (rc == TQ_HIP_OK && hipMalloc(&kv->d_page_table, pt_entries * sizeof(int32_t)) != hipSuccess) {
+        kv->d_page_table = nullptr;
+        rc = TQ_HIP_ENOMEM;
+    }
+    if (rc == TQ_HIP_OK) rc = herr(hipMemsetAsync(kv->pool, 0, kv->pool_bytes, kv->stream));
+    if (rc == TQ_HIP_OK)
+        rc = herr(hipMemsetAsync(kv->d_page_table, 0xFF, pt_entries * sizeof(int32_t), kv->stream));
+    if (rc == TQ_HIP_OK) rc = herr(hipStreamSynchronize(kv->stream));
+    if (rc != TQ_HIP_OK) {
+        tq_hip_kv_destroy(kv);
+        return rc;
+    }
+    v.pool = kv->pool;
+    v.page_table = kv->d_page_table;
+    *out = kv;
+    return TQ_HIP_OK;
+}
+
+void tq_hip_kv_destroy(tq_hip_kv *kv) {
+    if (!kv) return;
+    if (kv->stream) (void)hipStreamSynchronize(kv->stream);
+    if (kv->pool) (void)hipFree(kv->pool);
+    if (kv->d_page_table) (void)hipFree(kv->d_page_table);
+    if (kv->partials) (void)hipFree(kv->partials);
+    if (kv->stage) (void)hipFree(kv->stage);
+    if (kv->stream) (void)hipStreamDestroy(kv->stream);
+    delete kv;
+}
+
+int tq_hip_kv_set_pages(tq_hip_kv *kv, int seq, const int32_t *pages, int n_pages) {
+    if (!seq_ok(kv, seq) || n_pages < 0 || n_pages > kv->desc.max_pages_per_seq) return TQ_HIP_EINVAL;
+    if (n_pages > 0 && !pages) return TQ_HIP_EINVAL;
+    for (int i = 0; i < n_pages; i++)
+        if (pages[i] < -1 || pages[i] >= kv->desc.n_pages) return TQ_HIP_EINVAL;
+    int32_t *row = kv->h_page_table.data() + (size_t)seq * kv->desc.max_pages_per_seq;
+    for (int i = 0; i < kv->desc.max_pages_per_seq; i++) row[i] = i < n_pages ? pages[i] : -1;
+    TQ_TRY(hipMemcpyAsync(kv->d_page_table + (size_t)seq * kv->desc.max_pages_per_seq, row,
+                          (size_t)kv->desc.max_pages_per_seq * sizeof(int32_t), hipMemcpyHostToDevice,
+                          kv->stream));
+    return herr(hipStreamSynchronize(kv->stream));
+}
+
+int tq_hip_kv_capacity(const tq_hip_kv *kv, int seq) {
+    if (!seq_ok(kv, seq)) return TQ_HIP_EINVAL;
+    return capacity_of(kv, seq);
+}
+
+void *tq_hip_kv_stream(tq_hip_kv *kv) { return kv ? (void *)kv->stream : nullptr; }
+
+int tq_hip_kv_pool(tq_hip_kv *kv, void **base, size_t *bytes, int32_t **page_table) {
+    if (!kv) return TQ_HIP_EINVAL;
+    if (base) *base = kv->pool;
+    if (bytes) *bytes = kv->pool_bytes;
+    if (page_table) *page_table = kv->d_page_table;
+    return TQ_HIP_OK;
+}
+
+// Copy rows [pos0, pos0+n) page by page; `to_device` patches rows into
+// the pages (read-modify-write of each touched page run).
+static int kv_rows(tq_hip_kv *kv, int seq, int pos0, int n, block_q8 *k, block_q8 *v, bool to_device) {
+    if (!seq_ok(kv, seq) || pos0 < 0 || n < 0) return TQ_HIP_EINVAL;
+    if (n == 0) return TQ_HIP_OK;
+    if (pos0 + n > capacity_of(kv, seq)) return TQ_HIP_EINVAL;
+    const tq::PagedView &V = kv->view;
+    const int nkv = kv->desc.n_kv_heads, nb = V.nb;
+    std::vector<unsigned char> run(V.head_run);
+    const int32_t *pt = kv->h_page_table.data() + (size_t)seq * kv->desc.max_pages_per_seq;
+    for (int lp = pos0 / TQ_HIP_PAGE_TOKENS; lp * TQ_HIP_PAGE_TOKENS < pos0 + n; lp++) {
+        const int phys = pt[lp];
+        for (int h = 0; h < nkv; h++) {
+            unsigned char *dev = kv->pool + (size_t)phys * V.page_bytes + (size_t)h * V.head_run;
+            TQ_TRY(hipMemcpy(run.data(), dev, V.head_run, hipMemcpyDeviceToHost));
+            for (int r = 0; r < TQ_HIP_PAGE_TOKENS; r++) {
+                const int pos = lp * TQ_HIP_PAGE_TOKENS + r;
+                if (pos < pos0 || pos >= pos0 + n) continue;
+                const size_t hoff = ((size_t)h * n + (pos - pos0)) * nb;
+                unsigned char *kr = run.data() + (size_t)r * V.row_bytes;
+                unsigned char *vr = kr + V.kv_chunk;
+                if (to_device) {
+                    if (k) memcpy(kr, k + hoff, V.row_bytes);
+                    if (v) memcpy(vr, v + hoff, V.row_bytes);
+                } else {
+                    if (k) memcpy(k + hoff, kr, V.row_bytes);
+                    if (v) memcpy(v + hoff, vr, V.row_bytes);
+                }
+            }
+            if (to_device) TQ_TRY(hipMemcpy(dev, run.data(), V.head_run, hipMemcpyHostToDevice));
+        }
+    }
+    return TQ_HIP_OK;
+}
+
+int tq_hip_kv_write(tq_hip_kv *kv, int seq, int pos0, int n, const block_q8 *k, const block_q8 *v) {
+    if (kv) TQ_TRY(hipStreamSynchronize(kv->stream));
+    return kv_rows(kv, seq, pos0, n, const_cast<block_q8 *>(k), const_cast<block_q8 *>(v), true);
+}
+
+int tq_hip_kv_read(tq_hip_kv *kv, int seq, int pos0, int n, block_q8 *k, block_q8 *v) {
+    if (kv) TQ_TRY(hipStreamSynchronize(kv->stream));
+    return kv_rows(kv, seq, pos0, n, k, v, false);
+}
+
+// ---- append --------------------------------------------------------------------
+
+int tq_hip_kv_append_async(tq_hip_kv *kv, int n_rows, const int32_t *d_seq, const int32_t *d_pos,
+                           const float *d_k, const float *d_v, const float *d_cos, const float *d_sin,
+                           void *stream) {
+    if (!kv || n_rows < 0) return TQ_HIP_EINVAL;
+    if (n_rows == 0) return TQ_HIP_OK;
+    if (!d_seq || !d_pos || !d_k || !d_v || ((d_cos == nullptr) != (d_sin == nullptr))) return TQ_HIP_EINVAL;
+    return herr(tq_launch_append(kv->view, n_rows, d_seq, d_pos, 0, 0, d_k, d_v, d_cos, d_sin,
+                                 kv->desc.head_dim, pick(kv, stream)));
+}
+
+int tq_hip_kv_append(tq_hip_kv *kv, int seq, int pos, const float *k, const float *v, const float *cos_t,
+                     const float *sin_t) {
+    if (!seq_ok(kv, seq) || !k || !v || ((cos_t == nullptr) != (sin_t == nullptr))) return TQ_HIP_EINVAL;
+    if (pos < 0 || pos >= capacity_of(kv, seq)) return TQ_HIP_EINVAL;  // model/attention_layer.c:68,172
+    const tq_hip_kv_desc &D = kv->desc;
+    const size_t kvb = (size_t)D.n_kv_heads * D.head_dim * sizeof(float);
+    const size_t tb = (size_t)(D.head_dim / 2) * sizeof(float);
+    Stage st;
+    const size_t ok_ = st.take(kvb), ov = st.take(kvb), oc = st.take(tb), os = st.take(tb);
+    int rc = ensure_stage(kv, st.used);
+    if (rc != TQ_HIP_OK) return rc;
+    const hipStream_t s = kv->stream;
+    unsigned char *S = kv->stage;
+    TQ_TRY(hipMemcpyAsync(S + ok_, k, kvb, hipMemcpyHostToDevice, s));
+    TQ_TRY(hipMemcpyAsync(S + ov, v, kvb, hipMemcpyHostToDevice, s));
+    if (cos_t) {
+        TQ_TRY(hipMemcpyAsync(S + oc, cos_t, tb, hipMemcpyHostToDevice, s));
+        TQ_TRY(hipMemcpyAsync(S + os, sin_t, tb, hipMemcpyHostToDevice, s));
+    }
+    TQ_TRY(tq_launch_append(kv->view, 1, nullptr, nullptr, seq, pos, (const float *)(S + ok_),
+                            (const float *)(S + ov), cos_t ? (const float *)(S + oc) : nullptr,
+                            cos_t ? (const float *)(S + os) : nullptr, D.head_dim, s));
+    return herr(hipStreamSynchronize(s));
+}
+
+// ---- decode ----------------------------------------------------------------------
+
+int tq_hip_decode_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_len, int max_len,
+                        const float *d_q, const float *d_cos, const float *d_sin, float *d_out,
+                        void *stream) {
+    if (!kv || n_q < 0) return TQ_HIP_EINVAL;
+    if (n_q > 0 && (!d_seq || !d_len)) return TQ_HIP_EINVAL;
+    return decode_common(kv, n_q, d_seq, d_len, 0, 0, 0, max_len, d_q, d_cos, d_sin, nullptr, nullptr,
+                         d_out, pick(kv, stream));
+}
+
+int tq_hip_decode_step_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_pos,
+                             int max_pos, const float *d_q, const float *d_k, const float *d_v,
+                             const float *d_cos, const float *d_sin, float *d_out, void *stream) {
+    if (!kv || n_q < 0 || max_pos < 0) return TQ_HIP_EINVAL;
+    if (n_q > 0 && (!d_seq || !d_pos || !d_k || !d_v)) return TQ_HIP_EINVAL;
+    return decode_common(kv, n_q, d_seq, d_pos, 1, 0, 0, max_pos + 1, d_q, d_cos, d_sin, d_k, d_v, d_out,
+                         pick(kv, stream));
+}
+
+int tq_hip_attend(tq_hip_kv *kv, int seq, int pos, const float *q, const float *cos_t, const float *sin_t,
+                  float *out) {
+    if (!seq_ok(kv, seq) || !q || !out || ((cos_t == nullptr) != (sin_t == nullptr))) return TQ_HIP_EINVAL;
+    if (pos < 0 || pos >= capacity_of(kv, seq)) return TQ_HIP_EINVAL;
+    const tq_hip_kv_desc &D = kv->desc;
+    const size_t qb = (size_t)D.n_q_heads * D.head_dim * sizeof(float);
+    const size_t tb = (size_t)(D.head_dim / 2) * sizeof(float);
+    Stage st;
+    const size_t oq = st.take(qb), oc = st.take(tb), os = st.take(tb), oo = st.take(qb);
+    int rc = ensure_stage(kv, st.used);
+    if (rc != TQ_HIP_OK) return rc;
+    const hipStream_t s = kv->stream;
+    unsigned char *S = kv->stage;
+    TQ_TRY(hipMemcpyAsync(S + oq, q, qb, hipMemcpyHostToDevice, s));
+    if (cos_t) {
+        TQ_TRY(hipMemcpyAsync(S + oc, cos_t, tb, hipMemcpyHostToDevice, s));
+        TQ_TRY(hipMemcpyAsync(S + os, sin_t, tb, hipMemcpyHostToDevice, s));
+    }
+    rc = decode_common(kv, 1, nullptr, nullptr, 0, seq, pos, pos + 1, (const float *)(S + oq),
+                       cos_t ? (const float *)(S + oc) : nullptr, cos_t ? (const float *)(S + os) : nullptr,
+                       nullptr, nullptr, (float *)(S + oo), s);
+    if (rc != TQ_HIP_OK) return rc;
+    TQ_TRY(hipMemcpyAsync(out, S + oo, qb, hipMemcpyDeviceToHost, s));
+    return herr(hipStreamSynchronize(s));
+}
+
+// ---- prefill ---------------------------------------------------------------------
+
+int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d_q, const float *d_k,
+                         const float *d_v, const float *d_cos, const float *d_sin, float *d_out,
+                         void *stream) {
+    if (!seq_ok(kv, seq) || !d_q || !d_k || !d_v || !d_out || ((d_cos == nullptr) != (d_sin == nullptr)))
+        return TQ_HIP_EINVAL;
+    // model/attention_layer.c:203-204
+    if (n <= 0 || pos0 < 0 || pos0 + n > capacity_of(kv, seq)) return TQ_HIP_EINVAL;
+    const hipStream_t s = pick(kv, stream);
+    TQ_TRY(tq_launch_append(kv->view, n, nullptr, nullptr, seq, pos0, d_k, d_v, d_cos, d_sin,
+                            kv->desc.head_dim, s));
+    return decode_common(kv, n, nullptr, nullptr, 0, seq, pos0, pos0 + n, d_q, d_cos, d_sin, nullptr, nullptr,
+                         d_out, s);
+}
+
+int tq_hip_prefill(tq_hip_kv *kv, int seq, int pos0, int n, const float *q, const float *k, const float *v,
+                   const float *cos_t, const float *sin_t, float *out) {
+    if (!seq_ok(kv, seq) || !q || !k || !v || !out || ((cos_t == nullptr) != (sin_t == nullptr)))
+        return TQ_HIP_EINVAL;
+    if (n <= 0 || pos0 < 0 || pos0 + n > capacity_of(kv, seq)) return TQ_HIP_EINVAL;
+    const tq_hip_kv_desc &D = kv->desc;
+    const size_t qb = (size_t)n * D.n_q_heads * D.head_dim * sizeof(float);
+    const size_t kvb = (size_t)n * D.n_kv_heads * D.head_dim * sizeof(float);
+    const size_t tb = (size_t)n * (D.head_dim / 2) * sizeof(float);
+    Stage st;
+    const size_t oq = st.take(qb), ok_ = st.take(kvb), ov = st.take(kvb), oc = st.take(tb), os = st.take(tb),
+                 oo = st.take(qb);
+    int rc = ensure_stage(kv, st.used);
+    if (rc != TQ_HIP_OK) return rc;
+    const hipStream_t s = kv->stream;
+    unsigned char *S = kv->stage;
+    TQ_TRY(hipMemcpyAsync(S + oq, q, qb, hipMemcpyHostToDevice, s));
+    TQ_TRY(hipMemcpyAsync(S + ok_, k, kvb, hipMemcpyHostToDevice, s));
+    TQ_TRY(hipMemcpyAsync(S + ov, v, kvb, hipMemcpyHostToDevice, s));
+    if (cos_t) {
+        TQ_TRY(hipMemcpyAsync(S + oc, cos_t, tb, hipMemcpyHostToDevice, s));
+        TQ_TRY(hipMemcpyAsync(S + os, sin_t, tb, hipMemcpyHostToDevice, s));
+    }
+    rc = tq_hip_prefill_async(kv, seq, pos0, n, (const float *)(S + oq), (const float *)(S + ok_),
+                              (const float *)(S + ov), cos_t ? (const float *)(S + oc) : nullptr,
+                              cos_t ? (const float *)(S + os) : nullptr, (float *)(S + oo), s);
+    if (rc != TQ_HIP_OK) return rc;
+    TQ_TRY(hipMemcpyAsync(out, S + oo, qb, hipMemcpyDeviceToHost, s));
+    return herr(hipStreamSynchronize(s));
+}
+
+}  // extern "C"

@@ -1,0 +1,178 @@
+// tq_common.hpp — shared device helpers and launch interfaces of libtqhip.so.
+//
+// Exactness rules (the quantized KV codes and scales must equal the
+// reference's quantize_row_q8 bit for bit, kernel/quant_x.c:12-33):
+//   * every helper that reproduces a reference expression disables FP
+//   contraction for its body, so a*b+c stays a rounded multiply followed by a
+//   rounded add, as on the reference's x86 build without -mfma;
+//   * fp32 division uses hipcc's default correctly rounded division (no
+//   fast-math anywhere in this library).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/tq/tq_hip.h"
+
+namespace tq {
+
+constexpr int kQK = 32;           // values per block
+constexpr int kBlockBytes = 36;   // sizeof(block_q8)
+constexpr int kPage = TQ_HIP_PAGE_TOKENS;
+constexpr int kThreads = 256;     // work-group size of the attention kernels
+
+// 16-byte vector as a native clang vector, which stays in registers where
+// HIP's struct-wrapped uint4 can end up in scratch.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Quantization of one 32-value block spread one value per lane over 32
+// consecutive lanes of a wave (lanes 0-31 or 32-63).
+
+// max(0, |x_j|) over the 32 lanes with the reference's strict "val > max"
+// update (kernel/quant_x.c:18-22): NaN never wins, -0 counts as 0.  max is
+// exact, so the butterfly gives the same value as the serial scan.
+__device__ __forceinline__ float block_amax32(float x) {
+    float a = x < 0.0f ? -x : x;
+    float m = a > 0.0f ? a : 0.0f;
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) {
+        float o = __shfl_xor(m, off, 32);
+        m = o > m ? o : m;
+    }
+    return m;
+}
+
+// scale = amax / 127, inverse = 1/scale or 0 for an all-zero block
+// (kernel/quant_x.c:24-27); both divisions correctly rounded.
+__device__ __forceinline__ float quant_scale(float amax) { return amax / 127.0f; }
+__device__ __forceinline__ float quant_inverse(float d) { return d != 0.0f ? 1.0f / d : 0.0f; }
+
+// Code of x: x*inverse rounded to nearest, ties to even, by adding 1.5*2^23 so
+// the fp32 add rounds, and reading the integer back out of the low mantissa
+// bits; the low byte of that difference is the code (kernel/quant_x.c:5-10,31).
+__device__ __forceinline__ uint32_t quant_code(float x, float inv) {
+#pragma clang fp contract(off)
+    const float scaled = x * inv;
+    const float shifted = scaled + 12582912.0f;
+    return (__float_as_uint(shifted) - 0x4B400000u) & 0xFFu;
+}
+
+// Gather the 32 codes of a block into dwords: lane j (j % 4 == 0 within the
+// 32-lane group) gets codes j..j+3 little-endian, ready for a 4-byte store at
+// block offset 4 + j.
+__device__ __forceinline__ uint32_t pack_codes4(uint32_t code) {
+    const uint32_t c1 = __shfl_down(code, 1, 32);
+    const uint32_t c2 = __shfl_down(code, 2, 32);
+    const uint32_t c3 = __shfl_down(code, 3, 32);
+    return code | (c1 << 8) | (c2 << 16) | (c3 << 24);
+}
+
+// Quantize the block owned by this lane's 32-lane group and store it at
+// `blk` (a 36-byte block_q8 in global or shared memory).
+__device__ __forceinline__ void quantize_store32(float x, unsigned char *blk) {
+    const int lane = threadIdx.x & 31;
+    const float d = quant_scale(block_amax32(x));
+    const uint32_t code = quant_code(x, quant_inverse(d));
+    const uint32_t word = pack_codes4(code);
+    if (lane == 0) *reinterpret_cast<float *>(blk) = d;
+    if ((lane & 3) == 0) *reinterpret_cast<uint32_t *>(blk + 4 + lane) = word;
+}
+
+// ---------------------------------------------------------------------------
+// RoPE, rotate-half pairing i <-> i + hd/2 (model/rope.c:14-22):
+//   lower half: x0*c - x1*s      upper half: x0*s + x1*c
+// with x0 = x[i], x1 = x[i + hd/2], c/s from the host table.
+__device__ __forceinline__ float rope_lower(float x0, float x1, float c, float s) {
+#pragma clang fp contract(off)
+    return x0 * c - x1 * s;
+}
+__device__ __forceinline__ float rope_upper(float x0, float x1, float c, float s) {
+#pragma clang fp contract(off)
+    return x0 * s + x1 * c;
+}
+
+// Element e of a head after RoPE (cos_t == nullptr: no rotation).
+__device__ __forceinline__ float rope_elem(const float *head, int e, int hd, const float *cos_t,
+                                           const float *sin_t) {
+    if (cos_t == nullptr) return head[e];
+    const int half = hd >> 1;
+    if (e < half) return rope_lower(head[e], head[e + half], cos_t[e], sin_t[e]);
+    const int i = e - half;
+    return rope_upper(head[i], head[e], cos_t[i], sin_t[i]);
+}
+
+// ---------------------------------------------------------------------------
+// Paged cache view.  page[kvh][K|V][16][nb] block_q8.
+struct PagedView {
+    unsigned char *pool;
+    const int32_t *page_table;  // [max_seqs][max_pages]
+    int max_seqs;
+    int max_pages;
+    int n_pages;
+    int n_kv_heads;
+    int nb;
+    size_t page_bytes;  // n_kv_heads * head_run
+    size_t head_run;    // 2 * kv_chunk
+    size_t kv_chunk;    // 16 * nb * 36
+    size_t row_bytes;   // nb * 36
+};
+
+// Physical page holding logical page lp of seq, or -1.
+__device__ __forceinline__ int phys_page(const PagedView &v, int seq, int lp) {
+    if (seq < 0 || seq >= v.max_seqs || lp < 0 || lp >= v.max_pages) return -1;
+    const int p = v.page_table[(size_t)seq * v.max_pages + lp];
+    return (p >= 0 && p < v.n_pages) ? p : -1;
+}
+
+__device__ __forceinline__ unsigned char *head_run_ptr(const PagedView &v, int phys, int kvh) {
+    return v.pool + (size_t)phys * v.page_bytes + (size_t)kvh * v.head_run;
+}
+
+}  // namespace tq
+
+// ---------------------------------------------------------------------------
+// Launchers (host side, implemented in the .hip files, used by shim.hip).
+
+struct TqDecodeArgs {
+    tq::PagedView view;
+    const int32_t *seq_of;   // [n_q], or null: every query reads sequence seq_const
+    const int32_t *len_of;   // [n_q] tokens to attend minus len_plus, or null:
+                             // query i attends pos0 + i + 1 tokens
+    const float *q;          // [n_q][n_q_heads][hd]
+    const float *cos_t;      // [n_q][hd/2] or null
+    const float *sin_t;
+    const float *k_new;      // step mode: [n_q][n_kv_heads][hd] (pre-RoPE), else null
+    const float *v_new;
+    float *out;              // [n_q][n_q_heads][hd]
+    float *partials;         // [n_q][n_kv][n_splits][G*(hd+2)] when n_splits > 1
+    int n_q;
+    int n_q_heads;
+    int n_kv_heads;
+    int head_dim;
+    int split_tokens;
+    int n_splits;
+    float scale;
+    int seq_const;
+    int pos0;
+    int len_plus;            // step mode passes positions and 1 here
+};
+
+hipError_t tq_launch_quantize(const float *x, block_q8 *out, int n, hipStream_t s);
+hipError_t tq_launch_rope(float *x, int n_heads, int hd, const float *c, const float *sn,
+                          hipStream_t s);
+hipError_t tq_launch_scores(const block_q8 *q, int g, const block_q8 *k, int n, int nb,
+                            float scale, float *scores, size_t stride, hipStream_t s);
+hipError_t tq_launch_accum(const float *w, size_t w_stride, int g, const block_q8 *v, int n,
+                           int nb, float *out, size_t out_stride, hipStream_t s);
+hipError_t tq_launch_softmax(float *x, int n, int rows, size_t stride, hipStream_t s);
+// seq null: every row goes to seq_const; pos null: row r goes to pos0 + r.
+hipError_t tq_launch_append(const tq::PagedView &view, int n_rows, const int32_t *seq,
+                            const int32_t *pos, int seq_const, int pos0, const float *k,
+                            const float *v, const float *c, const float *sn, int hd,
+                            hipStream_t s);
+// Tokens per sub-chunk of the decode kernel for a head_dim.
+int tq_decode_tsub(int head_dim);
+bool tq_decode_supported(int head_dim, int group);
+hipError_t tq_launch_decode(const TqDecodeArgs &a, hipStream_t s);

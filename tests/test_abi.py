@@ -1,0 +1,79 @@
+"""CPU checks of the C-ABI: the libraries load, export every symbol the
+headers declare, and reject bad arguments before touching a device."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared(header: str, prefix: str) -> set[str]:
+    text = open(os.path.join(ROOT, "include", "tq", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(" + prefix + r"\w*)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from tailorquantkernel_amd import native
+    return native.load()
+
+
+def test_tq_hip_exports_every_declared_symbol(lib):
+    from tailorquantkernel_amd import native
+    names = declared("tq_hip.h", "tq_hip_")
+    assert len(names) >= 25
+    for n in sorted(names):
+        assert hasattr(lib, n), f"libtqhip.so does not export {n}"
+    assert names == set(native.EXPORTS), "ctypes prototypes out of step with tq_hip.h"
+
+
+def test_host_validation_without_device(lib):
+    from tailorquantkernel_amd import native
+    h = C.c_void_p()
+    bad = [(0, 2, 64, 4, 1, 4), (8, 0, 64, 4, 1, 4), (8, 3, 64, 4, 1, 4), (8, 2, 48, 4, 1, 4),
+           (8, 2, 64, 0, 1, 4), (8, 2, 64, 4, 0, 4), (8, 2, 64, 4, 1, 0)]
+    for d in bad:
+        desc = native.KVDesc(*d)
+        assert lib.tq_hip_kv_create(C.byref(h), C.byref(desc)) == native.EINVAL, d
+        assert h.value is None
+    assert lib.tq_hip_kv_create(None, None) == native.EINVAL
+    for d in [(8, 2, 96, 4, 1, 4), (40, 2, 64, 4, 1, 4)]:
+        desc = native.KVDesc(*d)
+        assert lib.tq_hip_kv_create(C.byref(h), C.byref(desc)) == native.ETYPE, d
+    lib.tq_hip_kv_destroy(None)
+    assert lib.tq_hip_kv_capacity(None, 0) == native.EINVAL
+    assert lib.tq_hip_kv_set_pages(None, 0, None, 0) == native.EINVAL
+    assert lib.tq_hip_kv_append(None, 0, 0, None, None, None, None) == native.EINVAL
+    assert lib.tq_hip_attend(None, 0, 0, None, None, None, None) == native.EINVAL
+    assert lib.tq_hip_prefill(None, 0, 0, 1, None, None, None, None, None, None) == native.EINVAL
+    assert lib.tq_hip_quantize_row_q8(None, None, -1, None) == native.EINVAL
+    assert lib.tq_hip_attn_scores_q8(None, 0, None, 1, 1, 1.0, None, 1, None) == native.EINVAL
+    assert lib.tq_hip_attn_accum_q8(None, 1, 1, None, 1, 1, None, 8, None) == native.EINVAL
+    assert lib.tq_hip_softmax(None, -1, 1, 1, None) == native.EINVAL
+    for code, text in ((0, "ok"), (-1, "argument out of range"), (-3, "unsupported head_dim or group size")):
+        assert native.strerror(code) == text
+
+
+def test_init_reports_missing_device(lib):
+    """Without a GPU (this CPU suite) tq_hip_init returns an error, never aborts."""
+    from tailorquantkernel_amd import native
+    rc = lib.tq_hip_init(0)
+    if rc == 0:
+        pytest.skip("a gfx950 device is present")
+    assert rc == native.ENODEV or rc <= native.EHIP_BASE
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    from tailorquantkernel_amd import native
+    saved = native._lib
+    native._lib = None
+    try:
+        with pytest.raises(RuntimeError, match="no CPU fallback"):
+            native.load(str(tmp_path / "libtqhip.so"))
+    finally:
+        native._lib = saved

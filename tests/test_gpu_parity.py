@@ -1,0 +1,478 @@
+"""GPU parity: the HIP path (through libtqhip.so's C-ABI) against the oracle.
+
+Bar: KV codes and scales, quantize_row_q8, RoPE, attn_scores_q8 and
+attn_accum_q8 bit-exact; attention outputs |gpu - oracle| <= 1e-4 + 1e-3*|oracle|
+(fp32), as the north-star tolerance states.  Edge cases follow the
+reference's tests: g in {1,2,3,4,5,8} x n in {1,7,100,129,300} x hd in
+{32,64,128} with guard values past n / hd (tools/test_model.c:1612-1697),
+n = 1, unused slots untouched (:1093-1135), bad positions write nothing
+(:1015-1049).
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+from oracle.binding import BLOCK_Q8, QK, blocks, dequant
+from tests.golden.gen import fill_random, normal
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-4, 1e-3
+GUARD = 12345.0
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "golden_q8.npz")
+
+
+def assert_close(gpu, ref, what=""):
+    gpu = np.asarray(gpu, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(gpu - ref)
+    bad = err > ATOL + RTOL * np.abs(ref)
+    if bad.any():
+        i = int(np.argmax(err - (ATOL + RTOL * np.abs(ref))))
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside 1e-4 + 1e-3|ref|; "
+                             f"worst at {i}: gpu {gpu.flat[i]!r} ref {ref.flat[i]!r}")
+
+
+@pytest.fixture(scope="module")
+def nat():
+    from tailorquantkernel_amd import native
+    native.init(0)
+    assert native.device_arch().startswith("gfx950")
+    return native
+
+
+def dev(nat, a):
+    return nat.DeviceBuffer.from_numpy(np.ascontiguousarray(a))
+
+
+def sync(nat):
+    nat.check(nat.load().tq_hip_device_synchronize(), "sync")
+
+
+# ---------------------------------------------------------------------------
+# element ops
+# ---------------------------------------------------------------------------
+
+def gpu_quantize(nat, x):
+    x = np.ascontiguousarray(x, np.float32)
+    nbk = x.size // QK
+    dx = dev(nat, x)
+    dq = nat.DeviceBuffer(max(nbk * 36, 1))
+    nat.check(nat.load().tq_hip_quantize_row_q8(dx.ptr, dq.ptr, x.size, None), "quantize")
+    sync(nat)
+    return dq.download((nbk,), BLOCK_Q8)
+
+
+def test_quantize_bitexact_golden(nat):
+    g = np.load(GOLDEN, allow_pickle=False)
+    seed, n = g["quant_x_seed"]
+    x = np.concatenate([fill_random(int(n), int(seed), 3.0), g["quant_edges"].reshape(-1)])
+    qb = gpu_quantize(nat, x)
+    np.testing.assert_array_equal(qb["d"].view(np.uint32), g["quant_d"].view(np.uint32))
+    np.testing.assert_array_equal(qb["q"], g["quant_q"])
+
+
+def test_quantize_bitexact_oracle(nat, oracle):
+    rng = np.random.default_rng(7)
+    for scale in (1e-38, 1e-20, 1e-3, 1.0, 8.0, 1e20):
+        x = (rng.standard_normal(32 * 997) * scale).astype(np.float32)
+        assert gpu_quantize(nat, x).tobytes() == oracle.quantize_row_q8(x).tobytes()
+    # trailing values past the last whole block are ignored, as n / QK drops them
+    x = fill_random(100, 3)
+    assert gpu_quantize(nat, x).tobytes() == oracle.quantize_row_q8(x).tobytes()
+
+
+def test_rope_bitexact(nat, oracle):
+    for hd, pos, th in ((64, 255, 1e4), (128, 4095, 5e5), (128, 7, 1e6), (32, 100, 1e4), (256, 31, 5e5)):
+        x = fill_random(8 * hd, 11 + pos, 3.0)
+        c, s = oracle.rope_table(hd, pos, th)
+        dx, dc, ds = dev(nat, x), dev(nat, c), dev(nat, s)
+        nat.check(nat.load().tq_hip_rope_apply(dx.ptr, 8, hd, dc.ptr, ds.ptr, None), "rope")
+        sync(nat)
+        got = dx.download((8 * hd,), np.float32)
+        exp = np.concatenate([oracle.rope_apply(x[h * hd:(h + 1) * hd], c, s) for h in range(8)])
+        assert got.tobytes() == exp.tobytes()
+
+
+@pytest.mark.parametrize("g", [1, 2, 3, 4, 5, 8])
+def test_scores_accum_bitexact(nat, oracle, g):
+    lib = nat.load()
+    for n in (1, 7, 100, 129, 300):
+        for hd in (32, 64, 128):
+            nb = hd // QK
+            seed = 900 + g * 100 + n * 10 + hd
+            qb = oracle.quantize_row_q8(fill_random(g * hd, seed))
+            kb = oracle.quantize_row_q8(fill_random(n * hd, seed + 1))
+            vb = oracle.quantize_row_q8(fill_random(n * hd, seed + 2))
+            sstride, ostride = n + 4, hd + 8
+            scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+            sc_ref = np.full(g * sstride, GUARD, np.float32)
+            oracle.attn_scores_q8(qb, g, kb, n, nb, scale, sc_ref, sstride)
+            dq, dk = dev(nat, qb), dev(nat, kb)
+            dsc = dev(nat, np.full(g * sstride, GUARD, np.float32))
+            nat.check(lib.tq_hip_attn_scores_q8(dq.ptr, g, dk.ptr, n, nb, scale, dsc.ptr, sstride, None), "scores")
+            sync(nat)
+            assert dsc.download((g * sstride,), np.float32).tobytes() == sc_ref.tobytes(), (g, n, hd)
+
+            w = fill_random(g * sstride, seed + 3)
+            out_ref = np.full(g * ostride, GUARD, np.float32)
+            oracle.attn_accum_q8(w, sstride, g, vb, n, nb, out_ref, ostride)
+            dw, dv = dev(nat, w), dev(nat, vb)
+            dout = dev(nat, np.full(g * ostride, GUARD, np.float32))
+            nat.check(lib.tq_hip_attn_accum_q8(dw.ptr, sstride, g, dv.ptr, n, nb, dout.ptr, ostride, None), "accum")
+            sync(nat)
+            assert dout.download((g * ostride,), np.float32).tobytes() == out_ref.tobytes(), (g, n, hd)
+
+
+def test_softmax_close(nat, oracle):
+    lib = nat.load()
+    for n, scale in ((1, 1.0), (3, 1.0), (1024, 20.0), (4096, 5.0), (5000, 50.0)):
+        rows, stride = 3, n + 5
+        x = np.full(rows * stride, GUARD, np.float32)
+        for r in range(rows):
+            x[r * stride:r * stride + n] = fill_random(n, 10 + n + r, scale)
+        dx = dev(nat, x)
+        nat.check(lib.tq_hip_softmax(dx.ptr, n, rows, stride, None), "softmax")
+        sync(nat)
+        got = dx.download((rows * stride,), np.float32).reshape(rows, stride)
+        for r in range(rows):
+            exp = oracle.softmax(x[r * stride:r * stride + n])
+            np.testing.assert_allclose(got[r, :n], exp, rtol=2e-6, atol=1e-9)
+            assert (got[r, n:] == GUARD).all()
+
+
+def test_attention_head_q8(nat, oracle):
+    lib = nat.load()
+    for hd, n in ((32, 1), (32, 7), (128, 100), (128, 16), (64, 300), (128, 4096)):
+        nb = hd // QK
+        q = fill_random(hd, 70 + n)
+        kb = oracle.quantize_row_q8(fill_random(n * hd, 1070 + n))
+        vb = oracle.quantize_row_q8(fill_random(n * hd, 2070 + n))
+        out_ref, qq_ref, sc_ref = oracle.attention_head_q8(q, kb, vb, n, hd)
+        dq, dk, dv = dev(nat, q), dev(nat, kb), dev(nat, vb)
+        dqq, dsc, dout = nat.DeviceBuffer(nb * 36), nat.DeviceBuffer(n * 4), nat.DeviceBuffer(hd * 4)
+        nat.check(lib.tq_hip_attention_head_q8(dq.ptr, dqq.ptr, dk.ptr, dv.ptr, n, hd, dsc.ptr, dout.ptr, None),
+                  "attention_head_q8")
+        sync(nat)
+        assert dqq.download((nb,), BLOCK_Q8).tobytes() == qq_ref.tobytes()
+        assert_close(dout.download((hd,), np.float32), out_ref, f"head hd={hd} n={n}")
+        if n == 1:
+            np.testing.assert_array_equal(dout.download((hd,), np.float32), dequant(vb))
+
+
+def test_golden_kernels_on_gpu(nat, oracle):
+    """The reference's own scores/softmax/accum outputs (golden) reproduced on the GPU."""
+    g_ = np.load(GOLDEN, allow_pickle=False)
+    lib = nat.load()
+    for i, (g, n, hd) in enumerate(g_["kern_cases"]):
+        g, n, hd = int(g), int(n), int(hd)
+        nb = hd // QK
+        seed = 900 + 7 * i
+        qb = oracle.quantize_row_q8(fill_random(g * hd, seed))
+        kb = oracle.quantize_row_q8(fill_random(n * hd, seed + 1))
+        vb = oracle.quantize_row_q8(fill_random(n * hd, seed + 2))
+        w = fill_random(g * n, seed + 3)
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+        dq, dk, dv, dw = dev(nat, qb), dev(nat, kb), dev(nat, vb), dev(nat, w)
+        dsc, dout = nat.DeviceBuffer(g * n * 4), nat.DeviceBuffer(g * hd * 4)
+        nat.check(lib.tq_hip_attn_scores_q8(dq.ptr, g, dk.ptr, n, nb, scale, dsc.ptr, n, None), "scores")
+        nat.check(lib.tq_hip_attn_accum_q8(dw.ptr, n, g, dv.ptr, n, nb, dout.ptr, hd, None), "accum")
+        nat.check(lib.tq_hip_softmax(dsc.ptr, n, g, n, None), "softmax")
+        sync(nat)
+        np.testing.assert_array_equal(dout.download((g * hd,), np.float32).view(np.uint32),
+                                      g_[f"kern_accum_{i}"].view(np.uint32))
+        np.testing.assert_allclose(dsc.download((g * n,), np.float32), g_[f"kern_softmax_{i}"], rtol=2e-6, atol=1e-9)
+
+
+# ---------------------------------------------------------------------------
+# paged cache: append / attend / step / batch / prefill
+# ---------------------------------------------------------------------------
+
+def flat_from_paged(kv, seq, n):
+    """Device cache rows [0, n) as the reference's flat arrays [nkv][n][nb]."""
+    k, v = kv.read(seq, 0, n)
+    return k.reshape(-1), v.reshape(-1)
+
+
+@pytest.mark.parametrize("shape", [(8, 2, 64, 256, 1e4), (32, 8, 128, 4096, 5e5), (4, 2, 32, 40, 1e6),
+                                   (6, 2, 256, 48, 1e4), (5, 1, 64, 70, 1e4)])
+def test_append_bitexact_and_untouched(nat, oracle, shape):
+    nq, nkv, hd, T, theta = shape
+    nb = hd // QK
+    kv = nat.PagedKV.single(nq, nkv, hd, T)
+    sent_k = blocks(nkv * T * nb).reshape(nkv, T, nb)
+    sent_k["d"] = 999.0
+    sent_k["q"] = 127
+    kv.write(0, 0, sent_k, sent_k)
+    kc, vc = sent_k.reshape(-1).copy(), sent_k.reshape(-1).copy()
+    for pos in sorted({0, 1, T // 2, T - 1}):
+        k = fill_random(nkv * hd, 100 + pos)
+        v = fill_random(nkv * hd, 200 + pos)
+        c, s = oracle.rope_table(hd, pos, theta)
+        assert kv.append(0, pos, k, v, c, s) == 0
+        kr = np.concatenate([oracle.rope_apply(k[h * hd:(h + 1) * hd], c, s) for h in range(nkv)])
+        assert oracle.lib.oracle_store_kv_q8(kc.ctypes.data, vc.ctypes.data, nkv, hd, T, pos,
+                                             kr.ctypes.data, v.ctypes.data) == 0
+    gk, gv = flat_from_paged(kv, 0, T)
+    assert gk.tobytes() == kc.tobytes() and gv.tobytes() == vc.tobytes()
+    # bad positions return -1 and write nothing
+    for bad in (-1, kv.capacity(0), kv.capacity(0) + 5):
+        assert kv.append(0, bad, fill_random(nkv * hd, 1), fill_random(nkv * hd, 2)) == -1
+    gk2, gv2 = flat_from_paged(kv, 0, T)
+    assert gk2.tobytes() == gk.tobytes() and gv2.tobytes() == gv.tobytes()
+    kv.close()
+
+
+def _step_compare(nat, oracle, nq, nkv, hd, T, theta, positions, seed):
+    """Device append + attend per position vs the oracle's attention core."""
+    nb = hd // QK
+    kv = nat.PagedKV.single(nq, nkv, hd, T)
+    kc, vc = blocks(nkv * T * nb), blocks(nkv * T * nb)
+    for pos in positions:
+        q = fill_random(nq * hd, seed + 3 * pos)
+        k = fill_random(nkv * hd, seed + 3 * pos + 1)
+        v = fill_random(nkv * hd, seed + 3 * pos + 2)
+        c, s = oracle.rope_table(hd, pos, theta)
+        rc, out_ref = oracle.attention_qkv(kc, vc, nq, nkv, hd, T, theta, pos, q, k, v)
+        assert rc == 0
+        assert kv.append(0, pos, k, v, c, s) == 0
+        rc, out = kv.attend(0, pos, q, c, s)
+        assert rc == 0
+        assert_close(out, out_ref, f"attend nq={nq} nkv={nkv} hd={hd} pos={pos}")
+    return kv, kc, vc
+
+
+def test_attend_c1_every_position(nat, oracle):
+    """8q/2kv/hd64, theta 1e4: every step of a 256-token context."""
+    kv, kc, vc = _step_compare(nat, oracle, 8, 2, 64, 256, 1e4, range(256), 5000)
+    gk, gv = flat_from_paged(kv, 0, 256)
+    assert gk.tobytes() == kc.tobytes() and gv.tobytes() == vc.tobytes()
+    kv.close()
+
+
+@pytest.mark.parametrize("g", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("hd", [32, 64, 128, 256])
+def test_attend_group_sizes(nat, oracle, g, hd):
+    nkv = 2
+    positions = [0, 1, 15, 16, 63, 64, 100, 255, 299]
+    kv, kc, vc = _step_compare(nat, oracle, g * nkv, nkv, hd, 300, 1e4, positions, 700 + g + hd)
+    kv.close()
+
+
+def test_attend_c2_full_context(nat, oracle):
+    """32q/8kv/hd128, theta 5e5, context 4096: cache filled, then the last steps."""
+    nq, nkv, hd, T, theta = 32, 8, 128, 4096, 5e5
+    nb = hd // QK
+    kc = oracle.quantize_row_q8(normal(nkv * T * hd, 1))
+    vc = oracle.quantize_row_q8(normal(nkv * T * hd, 2))
+    kv = nat.PagedKV.single(nq, nkv, hd, T)
+    kv.write(0, 0, kc.reshape(nkv, T, nb), vc.reshape(nkv, T, nb))
+    for pos in (0, 1000, 4094, 4095):
+        q = normal(nq * hd, 10 + pos)
+        k = normal(nkv * hd, 20 + pos)
+        v = normal(nkv * hd, 30 + pos)
+        c, s = oracle.rope_table(hd, pos, theta)
+        rc, out_ref = oracle.attention_qkv(kc, vc, nq, nkv, hd, T, theta, pos, q, k, v)
+        assert rc == 0
+        assert kv.append(0, pos, k, v, c, s) == 0
+        rc, out = kv.attend(0, pos, q, c, s)
+        assert rc == 0
+        assert_close(out, out_ref, f"C2 pos={pos}")
+    gk, gv = flat_from_paged(kv, 0, T)
+    assert gk.tobytes() == kc.tobytes() and gv.tobytes() == vc.tobytes()
+    # deterministic: the same call twice gives the same bits
+    q = normal(nq * hd, 99)
+    _, o1 = kv.attend(0, T - 1, q)
+    _, o2 = kv.attend(0, T - 1, q)
+    assert o1.tobytes() == o2.tobytes()
+    kv.close()
+
+
+def test_attend_single_token_is_dequantized_v(nat, oracle):
+    nq, nkv, hd = 8, 2, 64
+    kv = nat.PagedKV.single(nq, nkv, hd, 16)
+    k = fill_random(nkv * hd, 61)
+    v = fill_random(nkv * hd, 62)
+    assert kv.append(0, 0, k, v) == 0
+    rc, out = kv.attend(0, 0, fill_random(nq * hd, 60))
+    assert rc == 0
+    vq = [dequant(oracle.quantize_row_q8(v[h * hd:(h + 1) * hd])) for h in range(nkv)]
+    g = nq // nkv
+    for h in range(nq):
+        np.testing.assert_array_equal(out[h * hd:(h + 1) * hd], vq[h // g])
+    # bad positions: -1, out untouched
+    for bad in (-1, 16, 100):
+        rc, _ = kv.attend(0, bad, fill_random(nq * hd, 60))
+        assert rc == -1
+    kv.close()
+
+
+def test_decode_step_fused(nat, oracle):
+    """tq_hip_decode_step_async: append + attend in one launch, 2 sequences."""
+    lib = nat.load()
+    nq, nkv, hd, T, theta = 32, 8, 128, 700, 5e5
+    nb = hd // QK
+    pages = (T + 15) // 16
+    kv = nat.PagedKV(nq, nkv, hd, n_pages=2 * pages, max_seqs=2, max_pages_per_seq=pages)
+    perm = np.random.default_rng(3).permutation(2 * pages).astype(np.int32)
+    kv.set_pages(0, perm[:pages])
+    kv.set_pages(1, perm[pages:])
+    caches = [(blocks(nkv * T * nb), blocks(nkv * T * nb)) for _ in range(2)]
+    dseq = dev(nat, np.array([0, 1], np.int32))
+    for step in range(0, T, 37):
+        pos = np.array([step, min(T - 1, step + 5)], np.int32)
+        q = normal(2 * nq * hd, step)
+        k = normal(2 * nkv * hd, step + 1)
+        v = normal(2 * nkv * hd, step + 2)
+        cs = [oracle.rope_table(hd, int(p), theta) for p in pos]
+        cos = np.concatenate([c for c, _ in cs])
+        sin = np.concatenate([s for _, s in cs])
+        dq, dk, dv, dc, ds = dev(nat, q), dev(nat, k), dev(nat, v), dev(nat, cos), dev(nat, sin)
+        dpos, dout = dev(nat, pos), nat.DeviceBuffer(2 * nq * hd * 4)
+        nat.check(lib.tq_hip_decode_step_async(kv.h, 2, dseq.ptr, dpos.ptr, int(pos.max()), dq.ptr, dk.ptr,
+                                               dv.ptr, dc.ptr, ds.ptr, dout.ptr, None), "decode_step")
+        nat.check(lib.tq_hip_stream_synchronize(kv.stream), "sync")
+        out = dout.download((2, nq * hd), np.float32)
+        for i in range(2):
+            kc, vc = caches[i]
+            rc, ref = oracle.attention_qkv(kc, vc, nq, nkv, hd, T, theta, int(pos[i]), q[i * nq * hd:(i + 1) * nq * hd],
+                                           k[i * nkv * hd:(i + 1) * nkv * hd], v[i * nkv * hd:(i + 1) * nkv * hd])
+            assert rc == 0
+            assert_close(out[i], ref, f"step seq {i} pos {pos[i]}")
+    for i in range(2):
+        gk, gv = flat_from_paged(kv, i, T)
+        kc, vc = caches[i]
+        assert gk.tobytes() == kc.tobytes() and gv.tobytes() == vc.tobytes()
+    kv.close()
+
+
+def test_batched_decode_paged(nat, oracle):
+    """Many sequences of ragged lengths on shuffled pages (the batched-decode
+    shape at reduced count); each checked against the oracle on its own rows."""
+    lib = nat.load()
+    nq, nkv, hd = 32, 8, 128
+    nb = hd // QK
+    rng = np.random.default_rng(11)
+    lens = np.array([1, 2, 15, 16, 17, 100, 512, 1000, 2047, 3000, 513, 64], np.int32)
+    nseq = lens.size
+    pages_per = (lens + 15) // 16
+    maxp = int(pages_per.max())
+    total = int(pages_per.sum())
+    kv = nat.PagedKV(nq, nkv, hd, n_pages=total + 3, max_seqs=nseq, max_pages_per_seq=maxp)
+    perm = rng.permutation(total + 3).astype(np.int32)
+    at = 0
+    flats = []
+    for i, L in enumerate(lens):
+        kv.set_pages(i, perm[at:at + pages_per[i]])
+        at += pages_per[i]
+        kc = oracle.quantize_row_q8(normal(nkv * int(L) * hd, 100 + i))
+        vc = oracle.quantize_row_q8(normal(nkv * int(L) * hd, 200 + i))
+        kv.write(i, 0, kc.reshape(nkv, L, nb), vc.reshape(nkv, L, nb))
+        flats.append((kc, vc))
+    q = normal(nseq * nq * hd, 5)
+    order = rng.permutation(nseq).astype(np.int32)          # queries in shuffled sequence order
+    dseq, dlen = dev(nat, order), dev(nat, lens[order])
+    dq, dout = dev(nat, q), nat.DeviceBuffer(nseq * nq * hd * 4)
+    nat.check(lib.tq_hip_decode_async(kv.h, nseq, dseq.ptr, dlen.ptr, int(lens.max()), dq.ptr, None, None,
+                                      dout.ptr, None), "decode_async")
+    nat.check(lib.tq_hip_stream_synchronize(kv.stream), "sync")
+    out = dout.download((nseq, nq * hd), np.float32)
+    for qi, s in enumerate(order):
+        L = int(lens[s])
+        kc, vc = flats[s]
+        rc, ref = oracle.attend_q8(kc, vc, nq, nkv, hd, L, q[qi * nq * hd:(qi + 1) * nq * hd], L - 1)
+        assert rc == 0
+        assert_close(out[qi], ref, f"batch query {qi} seq {s} len {L}")
+    kv.close()
+
+
+def test_long_context_outliers(nat, oracle):
+    """64q/8kv/hd128 at 32,768 tokens (two sequences), 1 % of K/V values at
+    +-8 sigma, split-K over the context."""
+    lib = nat.load()
+    nq, nkv, hd, T = 64, 8, 128, 32768
+    nb = hd // QK
+    nseq = 2
+    pages = T // 16
+    kv = nat.PagedKV(nq, nkv, hd, n_pages=nseq * pages, max_seqs=nseq, max_pages_per_seq=pages)
+    flats = []
+    rng = np.random.default_rng(21)
+    for i in range(nseq):
+        kv.set_pages(i, np.arange(i * pages, (i + 1) * pages, dtype=np.int32))
+        kf = normal(nkv * T * hd, 300 + i)
+        vf = normal(nkv * T * hd, 400 + i)
+        for a in (kf, vf):
+            idx = rng.choice(a.size, a.size // 100, replace=False)
+            a[idx] = np.where(rng.random(idx.size) < 0.5, -8.0, 8.0).astype(np.float32)
+        kc, vc = oracle.quantize_row_q8(kf), oracle.quantize_row_q8(vf)
+        kv.write(i, 0, kc.reshape(nkv, T, nb), vc.reshape(nkv, T, nb))
+        flats.append((kc, vc))
+    q = normal(nseq * nq * hd, 9)
+    dseq, dlen = dev(nat, np.arange(nseq, dtype=np.int32)), dev(nat, np.full(nseq, T, np.int32))
+    dq, dout = dev(nat, q), nat.DeviceBuffer(nseq * nq * hd * 4)
+    nat.check(lib.tq_hip_decode_async(kv.h, nseq, dseq.ptr, dlen.ptr, T, dq.ptr, None, None, dout.ptr, None),
+              "decode_async")
+    nat.check(lib.tq_hip_stream_synchronize(kv.stream), "sync")
+    out = dout.download((nseq, nq * hd), np.float32)
+    for i in range(nseq):
+        kc, vc = flats[i]
+        rc, ref = oracle.attend_q8(kc, vc, nq, nkv, hd, T, q[i * nq * hd:(i + 1) * nq * hd], T - 1)
+        assert rc == 0
+        assert_close(out[i], ref, f"long context seq {i}")
+    kv.close()
+
+
+@pytest.mark.parametrize("shape", [(8, 2, 64, 300, 1e4, 0, 300), (32, 8, 128, 1100, 5e5, 37, 1000),
+                                   (6, 3, 32, 80, 1e6, 5, 70)])
+def test_prefill(nat, oracle, shape):
+    """attention_layer_batch semantics: n tokens stored then attending
+    causally; equal to n sequential oracle steps."""
+    nq, nkv, hd, T, theta, pos0, n = shape
+    nb = hd // QK
+    kc, vc = blocks(nkv * T * nb), blocks(nkv * T * nb)
+    kv = nat.PagedKV.single(nq, nkv, hd, T)
+    if pos0:
+        pre_k = oracle.quantize_row_q8(normal(nkv * T * hd, 1)).reshape(nkv, T, nb)
+        pre_v = oracle.quantize_row_q8(normal(nkv * T * hd, 2)).reshape(nkv, T, nb)
+        pre_k[:, pos0:] = np.zeros(1, BLOCK_Q8)
+        pre_v[:, pos0:] = np.zeros(1, BLOCK_Q8)
+        kv.write(0, 0, pre_k, pre_v)
+        kc[:], vc[:] = pre_k.reshape(-1), pre_v.reshape(-1)
+    q = normal(n * nq * hd, 3)
+    k = normal(n * nkv * hd, 4)
+    v = normal(n * nkv * hd, 5)
+    cos = np.zeros((n, hd // 2), np.float32)
+    sin = np.zeros((n, hd // 2), np.float32)
+    for i in range(n):
+        cos[i], sin[i] = oracle.rope_table(hd, pos0 + i, theta)
+    rc, out_ref = oracle.prefill_qkv(kc, vc, nq, nkv, hd, T, theta, pos0, n, q, k, v)
+    assert rc == 0
+    rc, out = kv.prefill(0, pos0, n, q, k, v, cos, sin)
+    assert rc == 0
+    assert_close(out, out_ref, f"prefill {shape}")
+    gk, gv = flat_from_paged(kv, 0, T)
+    assert gk.tobytes() == kc.tobytes() and gv.tobytes() == vc.tobytes()
+    for bad_pos0, bad_n in ((0, 0), (-1, 3), (kv.capacity(0) - 2, 3)):
+        rc, _ = kv.prefill(0, bad_pos0, bad_n, q, k, v, cos, sin)
+        assert rc == -1
+    kv.close()
+
+
+def test_error_codes(nat):
+    lib = nat.load()
+    import ctypes as C
+    h = C.c_void_p()
+    for desc, code in (((0, 2, 64, 4, 1, 4), nat.EINVAL), ((8, 3, 64, 4, 1, 4), nat.EINVAL),
+                       ((8, 2, 48, 4, 1, 4), nat.EINVAL), ((8, 2, 96, 4, 1, 4), nat.ETYPE),
+                       ((36, 2, 64, 4, 1, 4), nat.ETYPE), ((8, 2, 64, 0, 1, 4), nat.EINVAL)):
+        d = nat.KVDesc(*desc)
+        assert lib.tq_hip_kv_create(C.byref(h), C.byref(d)) == code, desc
+    kv = nat.PagedKV(8, 2, 64, n_pages=4, max_seqs=2, max_pages_per_seq=4)
+    assert lib.tq_hip_kv_set_pages(kv.h, 2, None, 0) == nat.EINVAL
+    assert lib.tq_hip_kv_set_pages(kv.h, 0, np.array([0, 9], np.int32).ctypes.data, 2) == nat.EINVAL
+    assert kv.capacity(0) == 0 and kv.capacity(5) == nat.EINVAL
+    assert kv.append(0, 0, np.zeros(128, np.float32), np.zeros(128, np.float32)) == nat.EINVAL  # no pages
+    kv.close()
