@@ -221,7 +221,7 @@ def bench_c2(args, nat, hip):
     outs = [nat.DeviceBuffer(nq * hd * 4) for _ in range(layers)]
 
     def step(l):
-        nat.check(lib.tq_hip_decode_step_async(kvs[l].h, 1, dseq.ptr, dpos.ptr, pos, dq.ptr, dk.ptr, dv.ptr,
+        nat.check(lib.tq_hip_decode_step_async(kvs[l].h, 1, None, dpos.ptr, pos, dq.ptr, dk.ptr, dv.ptr,
                                                dc.ptr, ds.ptr, outs[l].ptr, stream), "decode_step")
 
     # eager warm-up (allocates split-K scratch before capture)

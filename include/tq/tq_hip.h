@@ -146,7 +146,8 @@ int tq_hip_kv_append_async(tq_hip_kv *kv, int n_rows, const int32_t *d_seq,
  * partials are combined in a fixed order, so results do not depend on timing. */
 int tq_hip_attend(tq_hip_kv *kv, int seq, int pos, const float *q, const float *cos_t,
                   const float *sin_t, float *out);
-/* max_len: an upper bound of every d_len[i] (sizes the grid). */
+/* d_seq may be NULL: query i then reads sequence i.  max_len: an upper bound
+ * of every d_len[i] (sizes the grid); at most 64 * 8192 tokens. */
 int tq_hip_decode_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_len,
                         int max_len, const float *d_q, const float *d_cos, const float *d_sin,
                         float *d_out, void *stream);
@@ -155,7 +156,8 @@ int tq_hip_decode_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int3
  * (model/attention_layer.c:186-191): RoPE on q and k, store_kv of token
  * d_pos[i] of sequence d_seq[i], then attend over [0, d_pos[i]].  The new
  * token's K/V are quantized once, written to the cache and used by the same
- * launch.  max_pos: an upper bound of every d_pos[i]. */
+ * launch.  max_pos: an upper bound of every d_pos[i].  d_seq may be NULL
+ * (query i is sequence i); a sequence appears at most once per call. */
 int tq_hip_decode_step_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq,
                              const int32_t *d_pos, int max_pos, const float *d_q,
                              const float *d_k, const float *d_v, const float *d_cos,

@@ -24,6 +24,8 @@ struct tq_hip_kv {
     tq::PagedView view{};
     float *partials = nullptr;      // split-K scratch, grown on demand
     size_t partials_bytes = 0;
+    int *counters = nullptr;        // split-K arrival counters, zero between launches
+    size_t counters_n = 0;
     unsigned char *stage = nullptr; // device staging for the synchronous calls
     size_t stage_bytes = 0;
 };
@@ -57,7 +59,7 @@ int decode_max_splits() {
     static int v = [] {
         const char *s = getenv("TQ_HIP_DECODE_MAX_SPLITS");
         const int x = s ? atoi(s) : 0;
-        return x > 0 ? x : 64;
+        return x > 0 ? x : 32;
     }();
     return v;
 }
@@ -68,18 +70,29 @@ void plan_splits(const tq_hip_kv *kv, int n_q, int max_len, int *split_tokens, i
     const int tsub = tq_decode_tsub(kv->desc.head_dim);
     const int chunks = std::max(1, (max_len + tsub - 1) / tsub);
     const long pairs = (long)n_q * kv->desc.n_kv_heads;
+    const int cap = std::min(decode_max_splits(),
+                             tq_decode_max_splits(kv->desc.head_dim, kv->desc.n_q_heads / kv->desc.n_kv_heads));
     long want = (decode_wg_target() + pairs - 1) / pairs;
-    want = std::max(1L, std::min<long>(want, decode_max_splits()));
+    want = std::max(1L, std::min<long>(want, cap));
     want = std::min<long>(want, chunks);
+    // a work-group stages at most tq_decode_max_split_tokens() page ids
+    const int max_per = tq_decode_max_split_tokens() / tsub;
+    want = std::max<long>(want, (chunks + max_per - 1) / max_per);
     const int per = (int)((chunks + want - 1) / want);
     *split_tokens = per * tsub;
     *n_splits = (chunks + per - 1) / per;
 }
 
+// Longest context one decode call serves for this cache's shape.
+long max_context(const tq_hip_kv *kv) {
+    const int g = kv->desc.n_q_heads / kv->desc.n_kv_heads;
+    return (long)tq_decode_max_splits(kv->desc.head_dim, g) * tq_decode_max_split_tokens();
+}
+
 int ensure_partials(tq_hip_kv *kv, size_t bytes) {
     if (bytes <= kv->partials_bytes) return TQ_HIP_OK;
     if (kv->partials) {
-        TQ_TRY(hipStreamSynchronize(kv->stream));
+        TQ_TRY(hipDeviceSynchronize());
         TQ_TRY(hipFree(kv->partials));
         kv->partials = nullptr;
         kv->partials_bytes = 0;
@@ -89,6 +102,27 @@ int ensure_partials(tq_hip_kv *kv, size_t bytes) {
         return TQ_HIP_ENOMEM;
     }
     kv->partials_bytes = bytes;
+    return TQ_HIP_OK;
+}
+
+// Counters are zeroed once when allocated, on the stream of the launch that
+// will use them and synchronously (never inside a captured graph: warm up
+// first); the decode kernel's combining work-group puts each back to 0.
+int ensure_counters(tq_hip_kv *kv, size_t n, hipStream_t s) {
+    if (n <= kv->counters_n) return TQ_HIP_OK;
+    if (kv->counters) {
+        TQ_TRY(hipDeviceSynchronize());
+        TQ_TRY(hipFree(kv->counters));
+        kv->counters = nullptr;
+        kv->counters_n = 0;
+    }
+    if (hipMalloc(&kv->counters, n * sizeof(int)) != hipSuccess) {
+        kv->counters = nullptr;
+        return TQ_HIP_ENOMEM;
+    }
+    TQ_TRY(hipMemsetAsync(kv->counters, 0, n * sizeof(int), s));
+    TQ_TRY(hipStreamSynchronize(s));
+    kv->counters_n = n;
     return TQ_HIP_OK;
 }
 
@@ -119,13 +153,15 @@ struct Stage {
 };
 
 int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_len, int len_plus,
-                  int seq_const, int pos0, int max_len, const float *d_q, const float *d_cos,
+                  int seq_const, int seq_stride, int pos0, int max_len, const float *d_q, const float *d_cos,
                   const float *d_sin, const float *d_k, const float *d_v, float *d_out,
                   hipStream_t s) {
     if (n_q <= 0) return TQ_HIP_OK;
     // queries and kv heads are grid dimensions y/z (at most 65535 each)
     if (n_q > 65535 || kv->desc.n_kv_heads > 65535) return TQ_HIP_EINVAL;
     if (max_len <= 0 || !d_q || !d_out) return TQ_HIP_EINVAL;
+    // contexts longer than n_splits * split_tokens allows are not served
+    if ((long)max_len > max_context(kv)) return TQ_HIP_EINVAL;
     if ((d_cos == nullptr) != (d_sin == nullptr)) return TQ_HIP_EINVAL;
     const tq_hip_kv_desc &D = kv->desc;
     TqDecodeArgs a{};
@@ -134,6 +170,7 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
     a.len_of = d_len;
     a.len_plus = len_plus;
     a.seq_const = seq_const;
+    a.seq_stride = seq_stride;
     a.pos0 = pos0;
     a.q = d_q;
     a.cos_t = d_cos;
@@ -150,9 +187,11 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
     if (a.n_splits > 1) {
         const int g = D.n_q_heads / D.n_kv_heads;
         const size_t bytes = (size_t)n_q * D.n_kv_heads * a.n_splits * g * (D.head_dim + 2) * sizeof(float);
-        const int rc = ensure_partials(kv, bytes);
+        int rc = ensure_partials(kv, bytes);
+        if (rc == TQ_HIP_OK) rc = ensure_counters(kv, (size_t)n_q * D.n_kv_heads, s);
         if (rc != TQ_HIP_OK) return rc;
         a.partials = kv->partials;
+        a.counters = kv->counters;
     }
     return herr(tq_launch_decode(a, s));
 }
@@ -354,6 +393,7 @@ void tq_hip_kv_destroy(tq_hip_kv *kv) {
     if (kv->pool) (void)hipFree(kv->pool);
     if (kv->d_page_table) (void)hipFree(kv->d_page_table);
     if (kv->partials) (void)hipFree(kv->partials);
+    if (kv->counters) (void)hipFree(kv->counters);
     if (kv->stage) (void)hipFree(kv->stage);
     if (kv->stream) (void)hipStreamDestroy(kv->stream);
     delete kv;
@@ -475,8 +515,9 @@ int tq_hip_decode_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int3
                         const float *d_q, const float *d_cos, const float *d_sin, float *d_out,
                         void *stream) {
     if (!kv || n_q < 0) return TQ_HIP_EINVAL;
-    if (n_q > 0 && (!d_seq || !d_len)) return TQ_HIP_EINVAL;
-    return decode_common(kv, n_q, d_seq, d_len, 0, 0, 0, max_len, d_q, d_cos, d_sin, nullptr, nullptr,
+    if (n_q > 0 && !d_len) return TQ_HIP_EINVAL;
+    if (!d_seq && n_q > kv->desc.max_seqs) return TQ_HIP_EINVAL;
+    return decode_common(kv, n_q, d_seq, d_len, 0, 0, 1, 0, max_len, d_q, d_cos, d_sin, nullptr, nullptr,
                          d_out, pick(kv, stream));
 }
 
@@ -484,8 +525,9 @@ int tq_hip_decode_step_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const
                              int max_pos, const float *d_q, const float *d_k, const float *d_v,
                              const float *d_cos, const float *d_sin, float *d_out, void *stream) {
     if (!kv || n_q < 0 || max_pos < 0) return TQ_HIP_EINVAL;
-    if (n_q > 0 && (!d_seq || !d_pos || !d_k || !d_v)) return TQ_HIP_EINVAL;
-    return decode_common(kv, n_q, d_seq, d_pos, 1, 0, 0, max_pos + 1, d_q, d_cos, d_sin, d_k, d_v, d_out,
+    if (n_q > 0 && (!d_pos || !d_k || !d_v)) return TQ_HIP_EINVAL;
+    if (!d_seq && n_q > kv->desc.max_seqs) return TQ_HIP_EINVAL;
+    return decode_common(kv, n_q, d_seq, d_pos, 1, 0, 1, 0, max_pos + 1, d_q, d_cos, d_sin, d_k, d_v, d_out,
                          pick(kv, stream));
 }
 
@@ -507,7 +549,7 @@ int tq_hip_attend(tq_hip_kv *kv, int seq, int pos, const float *q, const float *
         TQ_TRY(hipMemcpyAsync(S + oc, cos_t, tb, hipMemcpyHostToDevice, s));
         TQ_TRY(hipMemcpyAsync(S + os, sin_t, tb, hipMemcpyHostToDevice, s));
     }
-    rc = decode_common(kv, 1, nullptr, nullptr, 0, seq, pos, pos + 1, (const float *)(S + oq),
+    rc = decode_common(kv, 1, nullptr, nullptr, 0, seq, 0, pos, pos + 1, (const float *)(S + oq),
                        cos_t ? (const float *)(S + oc) : nullptr, cos_t ? (const float *)(S + os) : nullptr,
                        nullptr, nullptr, (float *)(S + oo), s);
     if (rc != TQ_HIP_OK) return rc;
@@ -527,7 +569,7 @@ int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d
     const hipStream_t s = pick(kv, stream);
     TQ_TRY(tq_launch_append(kv->view, n, nullptr, nullptr, seq, pos0, d_k, d_v, d_cos, d_sin,
                             kv->desc.head_dim, s));
-    return decode_common(kv, n, nullptr, nullptr, 0, seq, pos0, pos0 + n, d_q, d_cos, d_sin, nullptr, nullptr,
+    return decode_common(kv, n, nullptr, nullptr, 0, seq, 0, pos0, pos0 + n, d_q, d_cos, d_sin, nullptr, nullptr,
                          d_out, s);
 }
 

@@ -27,21 +27,65 @@ constexpr int kThreads = 256;     // work-group size of the attention kernels
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
+// Cross-lane moves with DPP (a VALU modifier, a few cycles) instead of
+// ds_bpermute (an LDS-pipe round trip).  Control words of the gfx9 DPP:
+//   quad_perm [a,b,c,d] = a | b<<2 | c<<4 | d<<6;  row_shl:k = 0x100 + k;
+//   row_mirror = 0x140 (lane i <- 15-i);  row_half_mirror = 0x141 (i <- 7-i).
+constexpr int kDppQuadXor1 = 0xB1;   // [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;   // [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float lane_f(float x, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+// Max / sum over each row of 16 lanes, result in every lane of the row.
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp_f<kDppQuadXor1>(x));
+    x = fmaxf(x, dpp_f<kDppQuadXor2>(x));
+    x = fmaxf(x, dpp_f<kDppRowHalfMirror>(x));
+    return fmaxf(x, dpp_f<kDppRowMirror>(x));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f<kDppQuadXor1>(x);
+    x += dpp_f<kDppQuadXor2>(x);
+    x += dpp_f<kDppRowHalfMirror>(x);
+    return x + dpp_f<kDppRowMirror>(x);
+}
+// Over the whole wave (64 lanes); the result is uniform.
+__device__ __forceinline__ float wave_max(float x) {
+    x = row16_max(x);
+    return fmaxf(fmaxf(lane_f(x, 0), lane_f(x, 16)), fmaxf(lane_f(x, 32), lane_f(x, 48)));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+    x = row16_sum(x);
+    return (lane_f(x, 0) + lane_f(x, 16)) + (lane_f(x, 32) + lane_f(x, 48));
+}
+
+// ---------------------------------------------------------------------------
 // Quantization of one 32-value block spread one value per lane over 32
 // consecutive lanes of a wave (lanes 0-31 or 32-63).
 
 // max(0, |x_j|) over the 32 lanes with the reference's strict "val > max"
-// update (kernel/quant_x.c:18-22): NaN never wins, -0 counts as 0.  max is
-// exact, so the butterfly gives the same value as the serial scan.
+// update (kernel/quant_x.c:18-22): NaN never wins, -0 counts as 0.  Only
+// non-NaN values >= +0 enter the reduction and max is exact, so any
+// reduction order gives the serial scan's value.
 __device__ __forceinline__ float block_amax32(float x) {
-    float a = x < 0.0f ? -x : x;
+    const float a = x < 0.0f ? -x : x;
     float m = a > 0.0f ? a : 0.0f;
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) {
-        float o = __shfl_xor(m, off, 32);
-        m = o > m ? o : m;
-    }
-    return m;
+    m = row16_max(m);
+    const float lo = fmaxf(lane_f(m, 0), lane_f(m, 16));
+    const float hi = fmaxf(lane_f(m, 32), lane_f(m, 48));
+    return (threadIdx.x & 32) ? hi : lo;
 }
 
 // scale = amax / 127, inverse = 1/scale or 0 for an all-zero block
@@ -63,9 +107,9 @@ __device__ __forceinline__ uint32_t quant_code(float x, float inv) {
 // 32-lane group) gets codes j..j+3 little-endian, ready for a 4-byte store at
 // block offset 4 + j.
 __device__ __forceinline__ uint32_t pack_codes4(uint32_t code) {
-    const uint32_t c1 = __shfl_down(code, 1, 32);
-    const uint32_t c2 = __shfl_down(code, 2, 32);
-    const uint32_t c3 = __shfl_down(code, 3, 32);
+    const uint32_t c1 = dpp_u<0x55>(code);  // quad_perm [1,1,1,1]
+    const uint32_t c2 = dpp_u<0xAA>(code);  // quad_perm [2,2,2,2]
+    const uint32_t c3 = dpp_u<0xFF>(code);  // quad_perm [3,3,3,3]
     return code | (c1 << 8) | (c2 << 16) | (c3 << 24);
 }
 
@@ -137,7 +181,7 @@ __device__ __forceinline__ unsigned char *head_run_ptr(const PagedView &v, int p
 
 struct TqDecodeArgs {
     tq::PagedView view;
-    const int32_t *seq_of;   // [n_q], or null: every query reads sequence seq_const
+    const int32_t *seq_of;   // [n_q], or null: query i reads seq_const + seq_stride*i
     const int32_t *len_of;   // [n_q] tokens to attend minus len_plus, or null:
                              // query i attends pos0 + i + 1 tokens
     const float *q;          // [n_q][n_q_heads][hd]
@@ -147,6 +191,7 @@ struct TqDecodeArgs {
     const float *v_new;
     float *out;              // [n_q][n_q_heads][hd]
     float *partials;         // [n_q][n_kv][n_splits][G*(hd+2)] when n_splits > 1
+    int *counters;           // [n_q][n_kv] arrival counters, zero between launches
     int n_q;
     int n_q_heads;
     int n_kv_heads;
@@ -155,6 +200,7 @@ struct TqDecodeArgs {
     int n_splits;
     float scale;
     int seq_const;
+    int seq_stride;
     int pos0;
     int len_plus;            // step mode passes positions and 1 here
 };
@@ -174,5 +220,9 @@ hipError_t tq_launch_append(const tq::PagedView &view, int n_rows, const int32_t
                             hipStream_t s);
 // Tokens per sub-chunk of the decode kernel for a head_dim.
 int tq_decode_tsub(int head_dim);
+// Upper bounds of n_splits (for a head_dim and group size) and of
+// split_tokens that the decode kernel handles.
+int tq_decode_max_splits(int head_dim, int group);
+int tq_decode_max_split_tokens();
 bool tq_decode_supported(int head_dim, int group);
 hipError_t tq_launch_decode(const TqDecodeArgs &a, hipStream_t s);

@@ -291,6 +291,35 @@ def test_attend_c2_full_context(nat, oracle):
     kv.close()
 
 
+def test_split_combine_first_call_and_repeats(nat, oracle):
+    """Split-K combine: a fresh cache whose very first call uses several splits
+    (arrival counters allocated and zeroed on that call), many times over, then
+    a run of consecutive multi-split steps — every output against the oracle."""
+    nq, nkv, hd, T, theta = 32, 8, 128, 1200, 5e5
+    nb = hd // QK
+    kc = oracle.quantize_row_q8(normal(nkv * T * hd, 31))
+    vc = oracle.quantize_row_q8(normal(nkv * T * hd, 32))
+    for rep in range(8):
+        kv = nat.PagedKV.single(nq, nkv, hd, T)
+        kv.write(0, 0, kc.reshape(nkv, T, nb), vc.reshape(nkv, T, nb))
+        q = normal(nq * hd, 40 + rep)
+        pos = T - 1 - 37 * rep
+        rc, out = kv.attend(0, pos, q)
+        assert rc == 0
+        rc, ref = oracle.attend_q8(kc, vc, nq, nkv, hd, T, q, pos)
+        assert_close(out, ref, f"fresh cache rep {rep} pos {pos}")
+        kv.close()
+    kv = nat.PagedKV.single(nq, nkv, hd, T)
+    kv.write(0, 0, kc.reshape(nkv, T, nb), vc.reshape(nkv, T, nb))
+    for i, pos in enumerate(range(300, T, 29)):
+        q = normal(nq * hd, 100 + i)
+        rc, out = kv.attend(0, pos, q)
+        assert rc == 0
+        rc, ref = oracle.attend_q8(kc, vc, nq, nkv, hd, T, q, pos)
+        assert_close(out, ref, f"consecutive step pos {pos}")
+    kv.close()
+
+
 def test_attend_single_token_is_dequantized_v(nat, oracle):
     nq, nkv, hd = 8, 2, 64
     kv = nat.PagedKV.single(nq, nkv, hd, 16)
@@ -376,10 +405,14 @@ def test_batched_decode_paged(nat, oracle):
     order = rng.permutation(nseq).astype(np.int32)          # queries in shuffled sequence order
     dseq, dlen = dev(nat, order), dev(nat, lens[order])
     dq, dout = dev(nat, q), nat.DeviceBuffer(nseq * nq * hd * 4)
-    nat.check(lib.tq_hip_decode_async(kv.h, nseq, dseq.ptr, dlen.ptr, int(lens.max()), dq.ptr, None, None,
-                                      dout.ptr, None), "decode_async")
-    nat.check(lib.tq_hip_stream_synchronize(kv.stream), "sync")
-    out = dout.download((nseq, nq * hd), np.float32)
+    outs = []
+    for _ in range(3):  # repeated launches: split counters reset, results identical
+        nat.check(lib.tq_hip_decode_async(kv.h, nseq, dseq.ptr, dlen.ptr, int(lens.max()), dq.ptr, None, None,
+                                          dout.ptr, None), "decode_async")
+        nat.check(lib.tq_hip_stream_synchronize(kv.stream), "sync")
+        outs.append(dout.download((nseq, nq * hd), np.float32))
+    assert outs[0].tobytes() == outs[1].tobytes() == outs[2].tobytes()
+    out = outs[0]
     for qi, s in enumerate(order):
         L = int(lens[s])
         kc, vc = flats[s]
