@@ -298,12 +298,180 @@ def bench_c2(args, nat, hip):
     return line
 
 
+# ---------------------------------------------------------------------------
+# batched / long-context decode (C3, C5) and prefill (C4)
+
+def fill_pool_tiled(nat, kv, pattern: np.ndarray, n_pages: int, page_bytes: int):
+    """Write valid quantized pages into the whole pool by tiling a pattern of
+    whole pages (the content only has to be valid block_q8 data)."""
+    lib = nat.load()
+    base, nbytes, _ = kv.pool()
+    assert nbytes == n_pages * page_bytes and pattern.nbytes % page_bytes == 0
+    pat_pages = pattern.nbytes // page_bytes
+    for p0 in range(0, n_pages, pat_pages):
+        n = min(pat_pages, n_pages - p0)
+        nat.check(lib.tq_hip_memcpy_h2d(base + p0 * page_bytes, pattern.ctypes.data, n * page_bytes, None), "fill")
+
+
+def bench_batched(args, nat, hip, *, nq, nkv, hd, lens, theta, outliers, workload, metric):
+    from oracle.binding import Oracle, dequant
+    oracle = Oracle()
+    lib = nat.load()
+    nb = hd // QK
+    nseq = len(lens)
+    pages_per = (lens + PAGE - 1) // PAGE
+    total = int(pages_per.sum())
+    maxp = int(pages_per.max())
+    page_bytes = nkv * 2 * PAGE * nb * BLOCK_BYTES
+    kv = nat.PagedKV(nq, nkv, hd, n_pages=total, max_seqs=nseq, max_pages_per_seq=maxp)
+    rng = np.random.default_rng(7)
+    perm = rng.permutation(total).astype(np.int32)    # physical pages scattered over the pool
+    at = 0
+    for i in range(nseq):
+        kv.set_pages(i, perm[at:at + pages_per[i]])
+        at += pages_per[i]
+    pat_pages = min(total, 512)
+    pk = quantized_normal(oracle, pat_pages * PAGE * nkv * hd, 11, outliers)
+    pv = quantized_normal(oracle, pat_pages * PAGE * nkv * hd, 12, outliers)
+    pattern = paged_pool_bytes(pk, pv, nkv, pat_pages * PAGE, nb, np.arange(pat_pages), pat_pages)
+    fill_pool_tiled(nat, kv, pattern, total, page_bytes)
+    stream = kv.stream
+    kv_bytes = int(lens.sum()) * nkv * 2 * nb * BLOCK_BYTES
+
+    pos = (lens - 1).astype(np.int32)
+    q = rng.standard_normal(nseq * nq * hd, dtype=np.float32)
+    k = rng.standard_normal(nseq * nkv * hd, dtype=np.float32)
+    v = rng.standard_normal(nseq * nkv * hd, dtype=np.float32)
+    tabs = [oracle.rope_table(hd, int(p), theta) for p in pos]
+    cos = np.concatenate([c for c, _ in tabs]); sin = np.concatenate([s_ for _, s_ in tabs])
+    D = nat.DeviceBuffer.from_numpy
+    dq, dk, dv, dc, ds, dpos = D(q), D(k), D(v), D(cos), D(sin), D(pos)
+    dseq = D(np.arange(nseq, dtype=np.int32))
+    out = nat.DeviceBuffer(nseq * nq * hd * 4)
+    max_pos = int(pos.max())
+
+    def step():
+        nat.check(lib.tq_hip_decode_step_async(kv.h, nseq, dseq.ptr, dpos.ptr, max_pos, dq.ptr, dk.ptr, dv.ptr,
+                                               dc.ptr, ds.ptr, out.ptr, stream), "decode_step")
+
+    for _ in range(max(args.warmup // 8, 2)):
+        step()
+    hip.sync()
+    # parity on two sequences: the cache after the step (with the appended row)
+    got = out.download((nseq, nq * hd), np.float32)
+    errs, ok = [], True
+    for i in (0, nseq - 1):
+        L = int(lens[i])
+        kb, vb = kv.read(i, 0, L)
+        c, s_ = tabs[i]
+        qr = np.concatenate([oracle.rope_apply(q[(i * nq + h) * hd:(i * nq + h + 1) * hd], c, s_) for h in range(nq)])
+        rc, ref = oracle.attend_q8(kb.reshape(-1), vb.reshape(-1), nq, nkv, hd, L, qr, L - 1)
+        e = np.abs(got[i].astype(np.float64) - ref)
+        errs.append(float(e.max()))
+        ok = ok and rc == 0 and bool((e <= 1e-4 + 1e-3 * np.abs(ref)).all())
+
+    steps = max(4, args.steps // 64)
+    e0, e1 = hip.event(), hip.event()
+    hip.sync()
+    t0 = time.perf_counter()
+    hip.record(e0, stream)
+    for _ in range(steps):
+        step()
+    hip.record(e1, stream)
+    ms = hip.elapsed_ms(e0, e1) / steps
+    hip.sync()
+    wall = time.perf_counter() - t0
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": metric, "value": nseq * 1e3 / ms, "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+        "warmup": max(args.warmup // 8, 2), "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": workload, "batch": nseq, "n_q_heads": nq, "n_kv_heads": nkv, "head_dim": hd,
+                   "context_sum": int(lens.sum()), "context_max": int(lens.max()), "kv_bytes_per_step": kv_bytes,
+                   "pool_mb": total * page_bytes / 1e6},
+        "kv_gbps": gbs, "wall_s": wall,
+        "parity": {"ok": ok, "max_abs_err": max(errs), "bar": "1e-4 + 1e-3*|ref|", "checked_seqs": 2},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel": f"decode_kernel<{hd},{nq // nkv}>",
+                     "kernel_ms": ms, "algorithmic_bytes": kv_bytes},
+    }
+
+
+def bench_c3(args, nat, hip):
+    lens = np.random.default_rng(2024).integers(512, 8193, size=64).astype(np.int32)
+    return bench_batched(args, nat, hip, nq=32, nkv=8, hd=128, lens=lens, theta=500000.0, outliers=0.0,
+                         workload="Q8 GQA batched decode, 64 sequences, context U[512,8192] (seeded), 16-token "
+                                  "pages scattered over the pool, 32q/8kv/hd128, fused RoPE + append + attend",
+                         metric="Q8 GQA batched decode tokens/sec + achieved HBM GB/s (KV bytes), 1 GPU")
+
+
+def bench_c5(args, nat, hip):
+    lens = np.full(16, 32768, np.int32)
+    return bench_batched(args, nat, hip, nq=64, nkv=8, hd=128, lens=lens, theta=500000.0, outliers=0.01,
+                         workload="Q8 GQA long-context decode, 64q/8kv/hd128 (70B layer), batch 16, context 32768, "
+                                  "1% K/V outliers at +-8 sigma, split-K, fused RoPE + append + attend",
+                         metric="Q8 GQA long-context decode tokens/sec + achieved HBM GB/s (KV bytes), 1 GPU")
+
+
+def bench_c4(args, nat, hip):
+    from oracle.binding import Oracle
+    oracle = Oracle()
+    lib = nat.load()
+    nq, nkv, hd, n, theta = 32, 8, 128, 2048, 500000.0
+    kv = nat.PagedKV.single(nq, nkv, hd, n)
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal(n * nq * hd, dtype=np.float32)
+    k = rng.standard_normal(n * nkv * hd, dtype=np.float32)
+    v = rng.standard_normal(n * nkv * hd, dtype=np.float32)
+    tabs = [oracle.rope_table(hd, p, theta) for p in range(n)]
+    cos = np.stack([c for c, _ in tabs]); sin = np.stack([s_ for _, s_ in tabs])
+    D = nat.DeviceBuffer.from_numpy
+    dq, dk, dv, dc, ds = D(q), D(k), D(v), D(cos), D(sin)
+    out = nat.DeviceBuffer(n * nq * hd * 4)
+    stream = kv.stream
+
+    def step():
+        nat.check(lib.tq_hip_prefill_async(kv.h, 0, 0, n, dq.ptr, dk.ptr, dv.ptr, dc.ptr, ds.ptr, out.ptr, stream),
+                  "prefill")
+
+    step()
+    hip.sync()
+    # parity: the oracle prefill on the first 256 tokens (a causal prefix is unchanged by later tokens)
+    m = 256
+    from oracle.binding import blocks
+    kc, vc = blocks(nkv * n * (hd // QK)), blocks(nkv * n * (hd // QK))
+    rc, ref = oracle.prefill_qkv(kc, vc, nq, nkv, hd, n, theta, 0, m, q[:m * nq * hd], k[:m * nkv * hd], v[:m * nkv * hd])
+    got = out.download((n, nq * hd), np.float32)[:m]
+    e = np.abs(got.astype(np.float64) - ref)
+    ok = bool(rc == 0 and (e <= 1e-4 + 1e-3 * np.abs(ref)).all())
+    steps = max(3, args.steps // 400)
+    e0, e1 = hip.event(), hip.event()
+    hip.sync()
+    hip.record(e0, stream)
+    for _ in range(steps):
+        step()
+    hip.record(e1, stream)
+    ms = hip.elapsed_ms(e0, e1) / steps
+    useful_ops = 2.0 * nq * (n * (n + 1) / 2) * hd * 2      # Q.K^T and P.V over the causal triangle
+    tflops = useful_ops / (ms * 1e-3) / 1e12
+    return {
+        "metric": "Q8 GQA causal prefill tokens/sec + MFMA utilisation, 2048 tokens at 8B shape, 1 GPU",
+        "value": n * 1e3 / ms, "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": 1, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "Q8 GQA causal prefill, 2048 tokens, 32q/8kv/hd128, RoPE theta 5e5, KV append + "
+                               "causal attention", "tokens": n, "useful_ops": useful_ops},
+        "parity": {"ok": ok, "max_abs_err": float(e.max()), "bar": "1e-4 + 1e-3*|ref|", "checked_tokens": m},
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": 5000.0, "unit": "TFLOP/s",
+                     "frac": tflops / 5000.0, "traffic": None, "kernel": "prefill", "kernel_ms": ms},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3200)
     ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--config", default="c2", choices=["c2"])
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"])
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
@@ -316,8 +484,8 @@ def main():
     from tailorquantkernel_amd import native as nat
     nat.init(0)
     hip = Hip()
-    line = bench_c2(args, nat, hip)
-    if not args.no_cpu:
+    line = {"c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.config](args, nat, hip)
+    if not args.no_cpu and args.config == "c2":
         cb = cpu_baseline_c2(32, 8, 128, 4096, 500000.0, args.cpu_budget)
         line["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample")}
     print(json.dumps(line), flush=True)

@@ -29,10 +29,10 @@
 // XCDs), waits for their acknowledgement and bumps an integer arrival counter;
 // the last work-group of a (query, kv head) merges all partials in split order
 // with weights exp(m_s - M)/L.  One launch per step, no float atomics, a result
-// independent of which work-group arrived last, and no L2 write-back fence
-// (which every work-group would pay, serialised per XCD); only the combining
-// work-group invalidates its caches before reading the partials, all of which
-// it requests in one round trip.
+// independent of which work-group arrived last, and no cache write-back or
+// invalidation fence (an L2 write-back per work-group, serialised per XCD,
+// costs ~24 us here; an L2 invalidation ~2 us): the combining work-group reads
+// the partials back with agent-scope atomic loads, all in one round trip.
 //
 // Step mode (k_new != null): the work-group owning position len-1 quantizes
 // the new token's K (after RoPE) and V exactly as store_kv does, writes them to
@@ -45,6 +45,11 @@ using namespace tq;
 
 constexpr int kMaxSplits = 64;
 constexpr int kMaxSplitPages = 512;  // page ids a work-group stages (8,192 tokens)
+
+// A load that observes stores made coherent at agent scope by other XCDs.
+__device__ __forceinline__ float coherent_load(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Lane t of a token's NB consecutive lanes gets the value of lane t + J (row_shl:J).
 template <int J>
@@ -154,6 +159,8 @@ struct Decoder {
     Smem<HD, G> &sm;
     const PagedView &view;
     int tid, lane, wave, kvh, t_begin, t_end, pos_new;
+    int load_end;                // loads cover tokens below this
+    int contig_first, contig_pages;  // contiguous sequence: page = first + lp
     bool owns_new;
     float scale;
     // scores role: (token my_t, block my_b)
@@ -166,10 +173,10 @@ struct Decoder {
     // softmax role: wave owns heads wave, wave + 4
     float m_run[2], l_run[2];
 
-    __device__ __forceinline__ Decoder(Smem<HD, G> &s, const PagedView &v, int kvh_, int t_begin_, int t_end_,
-                                       int pos_new_, bool owns_, float scale_)
-        : sm(s), view(v), kvh(kvh_), t_begin(t_begin_), t_end(t_end_), pos_new(pos_new_), owns_new(owns_),
-          scale(scale_) {
+    __device__ __forceinline__ Decoder(Smem<HD, G> &s, const PagedView &v, int kvh_, int t_begin_, int load_end_,
+                                       int contig_first_, int contig_pages_, float scale_)
+        : sm(s), view(v), kvh(kvh_), t_begin(t_begin_), t_end(load_end_), pos_new(-1), load_end(load_end_),
+          contig_first(contig_first_), contig_pages(contig_pages_), owns_new(false), scale(scale_) {
         tid = threadIdx.x;
         lane = tid & 63;
         wave = tid >> 6;
@@ -186,7 +193,8 @@ struct Decoder {
     }
 
     // 16-byte loads of sub-chunk [c0, c0+TSUB): vector vi is page vi / VEC_PER_PAGE,
-    // byte 16*(vi % VEC_PER_PAGE) of that page's K+V run.  Page ids come from LDS.
+    // byte 16*(vi % VEC_PER_PAGE) of that page's K+V run.  Page ids come from LDS,
+    // or, for a contiguous sequence, from contig_first without any memory access.
     __device__ __forceinline__ void load(u32x4 (&pf)[S::VPT], int c0) const {
 #pragma unroll
         for (int i = 0; i < S::VPT; i++) {
@@ -195,9 +203,15 @@ struct Decoder {
                 const int p = vi / S::VEC_PER_PAGE;
                 const int w = vi - p * S::VEC_PER_PAGE;
                 const int tok0 = c0 + p * kPage;
-                // page id read unconditionally (index clamped into the array)
-                const int phys = sm.pages[min((tok0 - t_begin) / kPage, kMaxSplitPages - 1)];
-                if (tok0 < t_end && phys >= 0)
+                int phys;
+                if (contig_first >= 0) {
+                    const int lp = tok0 / kPage;
+                    phys = lp < contig_pages ? contig_first + lp : -1;
+                } else {
+                    // page id read unconditionally (index clamped into the array)
+                    phys = sm.pages[min((tok0 - t_begin) / kPage, kMaxSplitPages - 1)];
+                }
+                if (tok0 < load_end && phys >= 0)
                     pf[i] = *reinterpret_cast<const u32x4 *>(head_run_ptr(view, phys, kvh) + 16 * w);
             }
         }
@@ -250,7 +264,7 @@ struct Decoder {
             }
             __syncthreads();
         }
-        if (c_next < t_end) load(pf, c_next);
+        if (c_next < load_end) load(pf, c_next);
 
         // ---- scores -------------------------------------------------------------
         {
@@ -284,7 +298,8 @@ struct Decoder {
 #pragma unroll
                 for (int i = 0; i < (TSUB + 63) / 64; i++) {
                     const int t = lane + 64 * i;
-                    sv[i] = t < TSUB ? sp[t * G + gi] : -INFINITY;
+                    const float x = sp[min(t, TSUB - 1) * G + gi];  // unconditional LDS read
+                    sv[i] = t < TSUB ? x : -INFINITY;
                     mloc = fmaxf(mloc, sv[i]);
                 }
                 mloc = wave_max(mloc);
@@ -399,32 +414,47 @@ __global__ __launch_bounds__(256) void decode_kernel(TqDecodeArgs a) {
             else if (e < 2 * HD) nin[i].x = a.v_new[off + e - HD];
         }
     }
-    const int split_pages = a.split_tokens / kPage;
-    int page_id[(kMaxSplitPages + kThreads - 1) / kThreads];
-#pragma unroll
-    for (int i = 0; i < (kMaxSplitPages + kThreads - 1) / kThreads; i++) {
-        const int p = tid + i * kThreads;
-        if (p < split_pages) page_id[i] = phys_page(a.view, seq, t_begin / kPage + p);
-    }
-
-    if (len <= 0 || t_begin >= len) return;
-    const int t_end = min(len, t_begin + a.split_tokens);
-    const int pos_new = len - 1;
-    const bool owns_new = a.k_new != nullptr && pos_new >= t_begin && pos_new < t_end;
-#pragma unroll
-    for (int i = 0; i < (kMaxSplitPages + kThreads - 1) / kThreads; i++) {
-        const int p = tid + i * kThreads;
-        if (p < split_pages) sm.pages[p] = page_id[i];
-    }
-    __syncthreads();
-
-    Decoder<HD, G> d(sm, a.view, kvh, t_begin, t_end, pos_new, owns_new, a.scale);
-
-    // ---- 2. K/V of the first two sub-chunks -------------------------------------------
+    const bool contig = a.contig_first >= 0;
+    Decoder<HD, G> d(sm, a.view, kvh, t_begin, t_begin + a.split_tokens, a.contig_first, a.contig_pages, a.scale);
     u32x4 pfa[S::VPT], pfb[S::VPT];
+    int len_known;
+    if (contig) {
+        // ---- 2a. contiguous sequence: K/V requested at once, before len is known;
+        //      only pages the sequence maps are touched ------------------------------
+        d.load_end = min(t_begin + a.split_tokens, a.contig_pages * kPage);
+        d.load(pfa, t_begin);
+        if (d.load_end > t_begin + TSUB) d.load(pfb, t_begin + TSUB);
+        len_known = len;
+        if (len_known <= 0 || t_begin >= len_known) return;
+    } else {
+        // ---- 2b. paged: the split's page ids into LDS, then K/V ---------------------
+        const int split_pages = a.split_tokens / kPage;
+        int page_id[(kMaxSplitPages + kThreads - 1) / kThreads];
+#pragma unroll
+        for (int i = 0; i < (kMaxSplitPages + kThreads - 1) / kThreads; i++) {
+            const int p = tid + i * kThreads;
+            if (p < split_pages) page_id[i] = phys_page(a.view, seq, t_begin / kPage + p);
+        }
+        len_known = len;
+        if (len_known <= 0 || t_begin >= len_known) return;
+#pragma unroll
+        for (int i = 0; i < (kMaxSplitPages + kThreads - 1) / kThreads; i++) {
+            const int p = tid + i * kThreads;
+            if (p < split_pages) sm.pages[p] = page_id[i];
+        }
+        __syncthreads();
+        d.load_end = min(len_known, t_begin + a.split_tokens);
+        d.load(pfa, t_begin);
+        if (d.load_end > t_begin + TSUB) d.load(pfb, t_begin + TSUB);
+    }
+    const int t_end = min(len_known, t_begin + a.split_tokens);
+    const int pos_new = len_known - 1;
+    const bool owns_new = a.k_new != nullptr && pos_new >= t_begin && pos_new < t_end;
+    d.t_end = t_end;
+    d.load_end = min(d.load_end, t_end);
+    d.pos_new = pos_new;
+    d.owns_new = owns_new;
     const int n_sub = (t_end - t_begin + TSUB - 1) / TSUB;
-    d.load(pfa, t_begin);
-    if (n_sub > 1) d.load(pfb, t_begin + TSUB);
 
     // ---- 3. RoPE + exact quantize of q (and the new row) into LDS ---------------------
 #pragma unroll
@@ -449,7 +479,8 @@ __global__ __launch_bounds__(256) void decode_kernel(TqDecodeArgs a) {
     }
     __syncthreads();
     if (owns_new) {
-        const int phys = sm.pages[(pos_new - t_begin) / kPage];
+        const int lp = pos_new / kPage;
+        const int phys = contig ? (lp < a.contig_pages ? a.contig_first + lp : -1) : sm.pages[(pos_new - t_begin) / kPage];
         if (phys >= 0 && tid < 2 * (ROW / 4)) {
             const bool is_v = tid >= ROW / 4;
             const int w = is_v ? tid - ROW / 4 : tid;
@@ -506,10 +537,12 @@ __global__ __launch_bounds__(256) void decode_kernel(TqDecodeArgs a) {
     __syncthreads();
     if (!sm.last) return;
     if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // drop stale cached copies of the partials
 
-    // one round trip: (m, l) of every split for the wave's heads, then thread
-    // (float4 output u, split subset sg) requests its CL partial rows
+    // The partials are read back with agent-scope atomic loads, coherent across
+    // XCDs like the stores that wrote them, so no cache invalidation (an
+    // acquire fence costs ~2 us here) is needed.  One round trip: (m, l) of
+    // every split for the wave's heads, then thread (float4 output u, split
+    // subset sg) requests its CL partial rows.
     const float *parts = a.partials + pbase * pstride;
     const int wv = tid >> 6, ln = tid & 63;
     float mv[2], lv[2];
@@ -517,8 +550,8 @@ __global__ __launch_bounds__(256) void decode_kernel(TqDecodeArgs a) {
     for (int r = 0; r < 2; r++) {
         const int gi = wv + 4 * r;
         const bool ok = gi < G && ln < nvalid;
-        mv[r] = ok ? parts[ln * pstride + G * HD + gi] : -INFINITY;
-        lv[r] = ok ? parts[ln * pstride + G * HD + G + gi] : 0.0f;
+        mv[r] = ok ? coherent_load(parts + ln * pstride + G * HD + gi) : -INFINITY;
+        lv[r] = ok ? coherent_load(parts + ln * pstride + G * HD + G + gi) : 0.0f;
     }
     float4 *fred = reinterpret_cast<float4 *>(sm.kv);
     for (int u0 = 0; u0 < S::U; u0 += S::TPS) {
@@ -529,7 +562,11 @@ __global__ __launch_bounds__(256) void decode_kernel(TqDecodeArgs a) {
         for (int i = 0; i < S::CL; i++) {
             const int s = sg + S::NSG * i;
             ov[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (act && s < nvalid) ov[i] = *reinterpret_cast<const float4 *>(parts + s * pstride + 4 * u);
+            if (act && s < nvalid) {
+                const float *src = parts + s * pstride + 4 * u;
+                ov[i] = make_float4(coherent_load(src), coherent_load(src + 1), coherent_load(src + 2),
+                                    coherent_load(src + 3));
+            }
         }
         if (u0 == 0) {
 #pragma unroll

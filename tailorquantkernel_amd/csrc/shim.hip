@@ -152,10 +152,22 @@ struct Stage {
     }
 };
 
+int capacity_of(const tq_hip_kv *kv, int seq);
+
+// A sequence whose mapped logical pages 0..n-1 are physical first..first+n-1.
+void seq_contig(const tq_hip_kv *kv, int seq, int *first, int *n) {
+    const int32_t *row = kv->h_page_table.data() + (size_t)seq * kv->desc.max_pages_per_seq;
+    *first = row[0];
+    *n = 0;
+    if (row[0] < 0) return;
+    while (*n < kv->desc.max_pages_per_seq && row[*n] == row[0] + *n) (*n)++;
+}
+
+// contig_seq: the one sequence every query of this call reads, or -1.
 int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_len, int len_plus,
                   int seq_const, int seq_stride, int pos0, int max_len, const float *d_q, const float *d_cos,
                   const float *d_sin, const float *d_k, const float *d_v, float *d_out,
-                  hipStream_t s) {
+                  hipStream_t s, int contig_seq) {
     if (n_q <= 0) return TQ_HIP_OK;
     // queries and kv heads are grid dimensions y/z (at most 65535 each)
     if (n_q > 65535 || kv->desc.n_kv_heads > 65535) return TQ_HIP_EINVAL;
@@ -183,6 +195,17 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
     a.n_kv_heads = D.n_kv_heads;
     a.head_dim = D.head_dim;
     a.scale = 1.0f / sqrtf((float)D.head_dim);  // model/attention_layer.c:131
+    a.contig_first = -1;
+    a.contig_pages = 0;
+    if (contig_seq >= 0) {
+        int first, n;
+        seq_contig(kv, contig_seq, &first, &n);
+        // the whole mapped range must be one run for the kernel to skip the table
+        if (n > 0 && n * TQ_HIP_PAGE_TOKENS >= capacity_of(kv, contig_seq)) {
+            a.contig_first = first;
+            a.contig_pages = n;
+        }
+    }
     plan_splits(kv, n_q, max_len, &a.split_tokens, &a.n_splits);
     if (a.n_splits > 1) {
         const int g = D.n_q_heads / D.n_kv_heads;
@@ -518,7 +541,7 @@ int tq_hip_decode_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int3
     if (n_q > 0 && !d_len) return TQ_HIP_EINVAL;
     if (!d_seq && n_q > kv->desc.max_seqs) return TQ_HIP_EINVAL;
     return decode_common(kv, n_q, d_seq, d_len, 0, 0, 1, 0, max_len, d_q, d_cos, d_sin, nullptr, nullptr,
-                         d_out, pick(kv, stream));
+                         d_out, pick(kv, stream), (!d_seq && n_q == 1) ? 0 : -1);
 }
 
 int tq_hip_decode_step_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_pos,
@@ -528,7 +551,7 @@ int tq_hip_decode_step_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const
     if (n_q > 0 && (!d_pos || !d_k || !d_v)) return TQ_HIP_EINVAL;
     if (!d_seq && n_q > kv->desc.max_seqs) return TQ_HIP_EINVAL;
     return decode_common(kv, n_q, d_seq, d_pos, 1, 0, 1, 0, max_pos + 1, d_q, d_cos, d_sin, d_k, d_v, d_out,
-                         pick(kv, stream));
+                         pick(kv, stream), (!d_seq && n_q == 1) ? 0 : -1);
 }
 
 int tq_hip_attend(tq_hip_kv *kv, int seq, int pos, const float *q, const float *cos_t, const float *sin_t,
@@ -551,7 +574,7 @@ int tq_hip_attend(tq_hip_kv *kv, int seq, int pos, const float *q, const float *
     }
     rc = decode_common(kv, 1, nullptr, nullptr, 0, seq, 0, pos, pos + 1, (const float *)(S + oq),
                        cos_t ? (const float *)(S + oc) : nullptr, cos_t ? (const float *)(S + os) : nullptr,
-                       nullptr, nullptr, (float *)(S + oo), s);
+                       nullptr, nullptr, (float *)(S + oo), s, seq);
     if (rc != TQ_HIP_OK) return rc;
     TQ_TRY(hipMemcpyAsync(out, S + oo, qb, hipMemcpyDeviceToHost, s));
     return herr(hipStreamSynchronize(s));
@@ -570,7 +593,7 @@ int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d
     TQ_TRY(tq_launch_append(kv->view, n, nullptr, nullptr, seq, pos0, d_k, d_v, d_cos, d_sin,
                             kv->desc.head_dim, s));
     return decode_common(kv, n, nullptr, nullptr, 0, seq, 0, pos0, pos0 + n, d_q, d_cos, d_sin, nullptr, nullptr,
-                         d_out, s);
+                         d_out, s, seq);
 }
 
 int tq_hip_prefill(tq_hip_kv *kv, int seq, int pos0, int n, const float *q, const float *k, const float *v,

@@ -203,6 +203,8 @@ struct TqDecodeArgs {
     int seq_stride;
     int pos0;
     int len_plus;            // step mode passes positions and 1 here
+    int contig_first;        // >= 0: every query reads one sequence whose logical
+    int contig_pages;        // page lp < contig_pages is physical contig_first + lp
 };
 
 hipError_t tq_launch_quantize(const float *x, block_q8 *out, int n, hipStream_t s);
