@@ -114,6 +114,8 @@ void tq_hip_kv_destroy(tq_hip_kv *kv);
 int tq_hip_kv_set_pages(tq_hip_kv *kv, int seq, const int32_t *pages, int n_pages);
 /* Tokens addressable in `seq` (mapped logical pages * 16), or < 0. */
 int tq_hip_kv_capacity(const tq_hip_kv *kv, int seq);
+/* The shape the cache was created with. */
+int tq_hip_kv_get_desc(const tq_hip_kv *kv, tq_hip_kv_desc *desc);
 void *tq_hip_kv_stream(tq_hip_kv *kv);
 /* Device base and size of the pool; device pointer of the page tables
  * ([max_seqs][max_pages_per_seq] int32). */

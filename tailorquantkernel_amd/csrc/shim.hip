@@ -440,6 +440,12 @@ int tq_hip_kv_capacity(const tq_hip_kv *kv, int seq) {
     return capacity_of(kv, seq);
 }
 
+int tq_hip_kv_get_desc(const tq_hip_kv *kv, tq_hip_kv_desc *desc) {
+    if (!kv || !desc) return TQ_HIP_EINVAL;
+    *desc = kv->desc;
+    return TQ_HIP_OK;
+}
+
 void *tq_hip_kv_stream(tq_hip_kv *kv) { return kv ? (void *)kv->stream : nullptr; }
 
 int tq_hip_kv_pool(tq_hip_kv *kv, void **base, size_t *bytes, int32_t **page_table) {

@@ -57,6 +57,7 @@ _PROTOS = {
     "tq_hip_kv_destroy": (None, [_vp]),
     "tq_hip_kv_set_pages": (_i, [_vp, _i, _vp, _i]),
     "tq_hip_kv_capacity": (_i, [_vp, _i]),
+    "tq_hip_kv_get_desc": (_i, [_vp, C.POINTER(KVDesc)]),
     "tq_hip_kv_stream": (_vp, [_vp]),
     "tq_hip_kv_pool": (_i, [_vp, _vpp, C.POINTER(_sz), _vpp]),
     "tq_hip_kv_write": (_i, [_vp, _i, _i, _i, _vp, _vp]),
