@@ -256,6 +256,27 @@ def cpu_leg_c2(nq, nkv, hd, T, theta, budget_s: float, check):
     return baseline, parity
 
 
+def host_boundary_us(nq, nkv, hd, T, theta, q, k, v, calls=200):
+    """Wall time of one synchronous tq_attention_core call at position T-1
+    (host q/k/v in, host out back: copies, one launch, stream sync), from
+    Python through ctypes."""
+    from tailorquantkernel_amd import attn
+    cfg = attn.AttnConfig(nq, nkv, hd, nq * hd, theta, 1e-6)
+    cache = attn.Cache(attn.TQ_KV_Q8_DEVICE, cfg, T)
+    if cache.rc != 0:
+        raise RuntimeError(f"tq_kv_cache_init failed: {cache.rc}")
+    for _ in range(10):
+        cache.attention_core(T - 1, q, k, v)
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        rc, _ = cache.attention_core(T - 1, q, k, v)
+        if rc != 0:
+            raise RuntimeError(f"tq_attention_core failed: {rc}")
+    us = (time.perf_counter() - t0) / calls * 1e6
+    cache.free()
+    return us
+
+
 # ---------------------------------------------------------------------------
 # C2: batch-1 decode at the 8B shape
 
@@ -313,6 +334,7 @@ def bench_c2(args, nat, hip):
     # the kernel's average launch duration (including back-to-back gaps)
     achieved = kv_bytes / (ms_per_step * 1e-3) / 1e9
     traffic = measured_traffic("decode_c2_pmc.txt")
+    boundary_us = host_boundary_us(nq, nkv, hd, T, theta, q, k, v)
 
     line = {
         "metric": METRIC,
@@ -336,6 +358,7 @@ def bench_c2(args, nat, hip):
         "tokens_per_s_32_layers": 1e3 / ms_per_step / 32,
         "wall_s": wall,
         "graph_replay_equals_eager": replay_same,
+        "host_boundary_us_per_call": boundary_us,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "kernel": "decode_kernel<128, 4> (fused RoPE + append + split-K attend + combine)",
