@@ -497,7 +497,8 @@ def bench_c4(args, nat, hip):
         "repeat_equals_first": repeat_same,
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": 5000.0, "unit": "TFLOP/s",
                      "frac": tflops / 5000.0, "traffic": measured_traffic("prefill_c4_pmc.txt"),
-                     "kernel": "prefill", "kernel_ms": ms},
+                     "kernel": "append_kernel + prefill_stage_kernel<128> + prefill_kernel<128, 4, 2> (one step)",
+                     "kernel_ms": ms},
     }
 
 

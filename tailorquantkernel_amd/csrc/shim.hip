@@ -28,6 +28,8 @@ struct tq_hip_kv {
     size_t counters_n = 0;
     unsigned char *stage = nullptr; // device staging for the synchronous calls
     size_t stage_bytes = 0;
+    unsigned char *img = nullptr;   // prefill key-tile images, grown on demand
+    size_t img_bytes = 0;
 };
 
 namespace {
@@ -51,6 +53,16 @@ int decode_wg_target() {
         const char *s = getenv("TQ_HIP_DECODE_WG_TARGET");
         const int x = s ? atoi(s) : 0;
         return x > 0 ? x : 1024;
+    }();
+    return v;
+}
+
+// The dense MFMA prefill kernel (default) or, with TQ_HIP_PREFILL_DENSE=0,
+// the decode kernel run once per token with causal lengths.
+bool prefill_dense() {
+    static bool v = [] {
+        const char *s = getenv("TQ_HIP_PREFILL_DENSE");
+        return !(s && s[0] == '0');
     }();
     return v;
 }
@@ -123,6 +135,22 @@ int ensure_counters(tq_hip_kv *kv, size_t n, hipStream_t s) {
     TQ_TRY(hipMemsetAsync(kv->counters, 0, n * sizeof(int), s));
     TQ_TRY(hipStreamSynchronize(s));
     kv->counters_n = n;
+    return TQ_HIP_OK;
+}
+
+int ensure_img(tq_hip_kv *kv, size_t bytes) {
+    if (bytes <= kv->img_bytes) return TQ_HIP_OK;
+    if (kv->img) {
+        TQ_TRY(hipDeviceSynchronize());
+        TQ_TRY(hipFree(kv->img));
+        kv->img = nullptr;
+        kv->img_bytes = 0;
+    }
+    if (hipMalloc(&kv->img, bytes) != hipSuccess) {
+        kv->img = nullptr;
+        return TQ_HIP_ENOMEM;
+    }
+    kv->img_bytes = bytes;
     return TQ_HIP_OK;
 }
 
@@ -418,6 +446,7 @@ void tq_hip_kv_destroy(tq_hip_kv *kv) {
     if (kv->partials) (void)hipFree(kv->partials);
     if (kv->counters) (void)hipFree(kv->counters);
     if (kv->stage) (void)hipFree(kv->stage);
+    if (kv->img) (void)hipFree(kv->img);
     if (kv->stream) (void)hipStreamDestroy(kv->stream);
     delete kv;
 }
@@ -598,6 +627,30 @@ int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d
     const hipStream_t s = pick(kv, stream);
     TQ_TRY(tq_launch_append(kv->view, n, nullptr, nullptr, seq, pos0, d_k, d_v, d_cos, d_sin,
                             kv->desc.head_dim, s));
+    const tq_hip_kv_desc &D = kv->desc;
+    if (prefill_dense() && tq_prefill_mfma_supported(D.head_dim, D.n_q_heads / D.n_kv_heads, pos0 + n)) {
+        TqPrefillArgs t;
+        t.view = kv->view;
+        t.seq = seq;
+        t.pos0 = pos0;
+        t.n = n;
+        t.q = d_q;
+        t.cos_t = d_cos;
+        t.sin_t = d_sin;
+        t.out = d_out;
+        t.n_q_heads = D.n_q_heads;
+        t.n_kv_heads = D.n_kv_heads;
+        t.head_dim = D.head_dim;
+        t.scale = 1.0f / sqrtf((float)D.head_dim);
+        int first = -1, pages = 0;
+        seq_contig(kv, seq, &first, &pages);
+        t.contig_first = pages > 0 ? first : -1;
+        t.contig_pages = pages;
+        const int rc = ensure_img(kv, tq_prefill_image_bytes(D.head_dim, D.n_kv_heads, pos0 + n));
+        if (rc != TQ_HIP_OK) return rc;
+        t.img = kv->img;
+        return herr(tq_launch_prefill(t, s));
+    }
     return decode_common(kv, n, nullptr, nullptr, 0, seq, 0, pos0, pos0 + n, d_q, d_cos, d_sin, nullptr, nullptr,
                          d_out, s, seq);
 }

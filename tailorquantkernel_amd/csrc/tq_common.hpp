@@ -228,3 +228,26 @@ int tq_decode_max_splits(int head_dim, int group);
 int tq_decode_max_split_tokens();
 bool tq_decode_supported(int head_dim, int group);
 hipError_t tq_launch_decode(const TqDecodeArgs &a, hipStream_t s);
+
+struct TqPrefillArgs {
+    tq::PagedView view;
+    int seq;
+    int pos0;
+    int n;                 // tokens pos0 .. pos0+n-1 (already appended)
+    const float *q;        // [n][n_q_heads][hd]
+    const float *cos_t;    // [n][hd/2] or null (q already rotated)
+    const float *sin_t;
+    float *out;            // [n][n_q_heads][hd]
+    int n_q_heads;
+    int n_kv_heads;
+    int head_dim;
+    float scale;
+    int contig_first;      // as in TqDecodeArgs
+    int contig_pages;
+    unsigned char *img;    // tq_prefill_image_bytes() of scratch for the staged key tiles
+};
+// The MFMA causal prefill covers head_dim 64/128, groups 1/2/4/8 and keys
+// [0, kend) up to 65536.
+bool tq_prefill_mfma_supported(int head_dim, int group, int kend);
+size_t tq_prefill_image_bytes(int head_dim, int n_kv_heads, int kend);
+hipError_t tq_launch_prefill(const TqPrefillArgs &a, hipStream_t s);

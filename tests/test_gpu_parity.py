@@ -458,8 +458,16 @@ def test_long_context_outliers(nat, oracle):
     kv.close()
 
 
-@pytest.mark.parametrize("shape", [(8, 2, 64, 300, 1e4, 0, 300), (32, 8, 128, 1100, 5e5, 37, 1000),
-                                   (6, 3, 32, 80, 1e6, 5, 70)])
+PREFILL_SHAPES = [
+    # nq, nkv, hd, T, theta, pos0, n — dense MFMA kernel: hd 64/128, g 1/2/4/8
+    (8, 2, 64, 300, 1e4, 0, 300), (32, 8, 128, 1100, 5e5, 37, 1000), (4, 4, 64, 200, 1e4, 0, 200),
+    (16, 8, 128, 300, 5e5, 0, 257), (64, 8, 128, 400, 1e6, 16, 333), (8, 2, 64, 1200, 1e4, 0, 1100),
+    (2, 1, 128, 40, 1e4, 0, 1), (8, 2, 64, 90, 1e4, 70, 17),
+    # shapes the dense kernel does not cover run the decode form per token
+    (6, 3, 32, 80, 1e6, 5, 70), (8, 2, 256, 100, 1e4, 3, 90), (12, 4, 128, 120, 1e4, 0, 100)]
+
+
+@pytest.mark.parametrize("shape", PREFILL_SHAPES)
 def test_prefill(nat, oracle, shape):
     """attention_layer_batch semantics: n tokens stored then attending
     causally; equal to n sequential oracle steps."""
@@ -491,6 +499,74 @@ def test_prefill(nat, oracle, shape):
     for bad_pos0, bad_n in ((0, 0), (-1, 3), (kv.capacity(0) - 2, 3)):
         rc, _ = kv.prefill(0, bad_pos0, bad_n, q, k, v, cos, sin)
         assert rc == -1
+    kv.close()
+
+
+def test_prefill_scattered_pages(nat, oracle):
+    """Prefill of a sequence whose pages are scattered over the pool, after
+    earlier context, next to another sequence that must stay untouched."""
+    nq, nkv, hd, theta, pos0, n = 16, 4, 128, 5e5, 45, 150
+    nb = hd // QK
+    T = 208   # 13 pages
+    n_pages = 32
+    kv = nat.PagedKV(nq, nkv, hd, n_pages=n_pages, max_seqs=2, max_pages_per_seq=13)
+    rng = np.random.default_rng(11)
+    perm = rng.permutation(n_pages).astype(np.int32)
+    kv.set_pages(1, perm[:13])
+    kv.set_pages(0, perm[13:26])
+    other_k = oracle.quantize_row_q8(normal(nkv * T * hd, 21)).reshape(nkv, T, nb)
+    kv.write(0, 0, other_k, other_k)
+    pre_k = oracle.quantize_row_q8(normal(nkv * T * hd, 22)).reshape(nkv, T, nb)
+    pre_v = oracle.quantize_row_q8(normal(nkv * T * hd, 23)).reshape(nkv, T, nb)
+    pre_k[:, pos0:] = np.zeros(1, BLOCK_Q8)
+    pre_v[:, pos0:] = np.zeros(1, BLOCK_Q8)
+    kv.write(1, 0, pre_k, pre_v)
+    kc, vc = pre_k.reshape(-1).copy(), pre_v.reshape(-1).copy()
+    q, k, v = normal(n * nq * hd, 24), normal(n * nkv * hd, 25), normal(n * nkv * hd, 26)
+    cos = np.zeros((n, hd // 2), np.float32)
+    sin = np.zeros((n, hd // 2), np.float32)
+    for i in range(n):
+        cos[i], sin[i] = oracle.rope_table(hd, pos0 + i, theta)
+    rc, out_ref = oracle.prefill_qkv(kc, vc, nq, nkv, hd, T, theta, pos0, n, q, k, v)
+    assert rc == 0
+    rc, out = kv.prefill(1, pos0, n, q, k, v, cos, sin)
+    assert rc == 0
+    assert_close(out, out_ref, "prefill on scattered pages")
+    gk, gv = kv.read(1, 0, T)
+    assert gk.reshape(-1).tobytes() == kc.tobytes() and gv.reshape(-1).tobytes() == vc.tobytes()
+    ok_, ov_ = kv.read(0, 0, T)
+    assert ok_.tobytes() == other_k.tobytes() and ov_.tobytes() == other_k.tobytes()
+    kv.close()
+
+
+def test_prefill_c4_sampled(nat, oracle):
+    """The 8B-shape causal prefill of 2048 tokens: outputs of sampled tokens
+    against attend_q8 of the oracle on the cache the prefill left (token i
+    reads rows [0, i] only), and a repeat of the call is bit-identical."""
+    nq, nkv, hd, n, theta = 32, 8, 128, 2048, 5e5
+    nb = hd // QK
+    kv = nat.PagedKV.single(nq, nkv, hd, n)
+    q, k, v = normal(n * nq * hd, 31), normal(n * nkv * hd, 32), normal(n * nkv * hd, 33)
+    cos = np.zeros((n, hd // 2), np.float32)
+    sin = np.zeros((n, hd // 2), np.float32)
+    for i in range(n):
+        cos[i], sin[i] = oracle.rope_table(hd, i, theta)
+    rc, out = kv.prefill(0, 0, n, q, k, v, cos, sin)
+    assert rc == 0
+    gk, gv = kv.read(0, 0, n)
+    for i in (0, 1, 31, 32, 100, 511, 1024, 1500, 2046, 2047):
+        qi = q[i * nq * hd:(i + 1) * nq * hd]
+        qr = np.concatenate([oracle.rope_apply(qi[h * hd:(h + 1) * hd], cos[i], sin[i]) for h in range(nq)])
+        rc, ref = oracle.attend_q8(gk.reshape(-1), gv.reshape(-1), nq, nkv, hd, n, qr, i)
+        assert rc == 0
+        assert_close(out[i], ref, f"C4 token {i}")
+    # K rows are the quantized, rotated k (spot-check token 1999 of every head)
+    t = 1999
+    for h in range(nkv):
+        kr = oracle.rope_apply(k[(t * nkv + h) * hd:(t * nkv + h + 1) * hd], cos[t], sin[t])
+        assert gk[h, t].tobytes() == oracle.quantize_row_q8(kr).tobytes()
+    rc, out2 = kv.prefill(0, 0, n, q, k, v, cos, sin)
+    assert rc == 0 and out2.tobytes() == out.tobytes()
     kv.close()
 
 
