@@ -1,0 +1,696 @@
+// decode3.hip — attend_q8 (model/attention_layer.c:125-150) on the paged cache,
+// with both contractions on the matrix cores.
+//
+// Grid (split, kv head, query); a work-group of four waves owns the tokens
+// [split*split_tokens, +split_tokens) of one kv head and all G query heads that
+// read it, so every K/V byte is fetched once per step.  The range is cut into
+// tiles of 32 keys (two pages); wave w takes tiles w, w+4, w+8, ... and runs
+// its own online softmax over them, so the key loop has no barrier at all.
+// Tiles are copied straight from HBM into the wave's LDS slots by
+// global_load_lds_dwordx4 (no staging registers), two tiles ahead, then:
+//
+//   scores  S[key][(h,b)] on v_mfma_i32_16x16x32_i8.  The N columns of the
+//           product are the (query head h, block b) pairs of the group and the
+//           K dimension one 32-value block: the product for block b' has the q
+//           codes of block b' in the columns with b == b' and zeros elsewhere,
+//           so accumulating the NB products leaves the exact int32 block dot
+//           sum_j q[h][b][j]*k[key][b][j] in column (h,b), every lane useful at
+//           G*NB = 16.  Each lane scales its dots by qd*kd and the NB lanes of
+//           a head add them in block order with DPP moves: the score
+//           ((0 + x_0) + x_1) + ... then *scale is bit-identical to
+//           attn_scores_q8_scalar (model/attn_q8.c:17-34).
+//   softmax online, per lane, exp2 domain; max and sum over the four 16-lane
+//           rows holding the tile's keys with permlane32/16 swaps.  The
+//           running max moves only when a tile exceeds it by more than 2^8,
+//           so rescaling the accumulators is rare (p <= 256 in between).
+//   P.V     O[col][(h,b)] += V[key][col] * W[key][(h,b)] on
+//           v_mfma_f32_16x16x32_bf16, K = 32 keys.  W = p * vd (the weight of
+//           attn_accum_q8's ws = wt * vb[b].d, model/attn_q8.c:48) lies in
+//           exactly the lanes and key order the score product left it in, split
+//           into bf16 hi + lo (exact to 2^-18 relative); the int8 V codes are
+//           exact in bf16, so hi.V + lo.V in fp32 carries W's precision.
+//           Column (h,b) of the output is kept for the columns of block b.
+//
+// The four waves merge (m, l, o) through LDS in wave order.  With several
+// splits each work-group writes its partial (o, m, l) with 16-byte stores at
+// agent coherence (sc1: through to the point all XCDs share) and bumps an
+// arrival counter; the last one merges the partials in split order, so results
+// do not depend on arrival order.
+//
+// Step mode (k_new != null): the work-group owning position len-1 quantizes the
+// new token's K (after RoPE) and V exactly as store_kv does, writes them to the
+// cache and patches them into the staged tile: append + attend in one launch.
+#include "tq_common.hpp"
+
+namespace {
+
+using namespace tq;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+constexpr int kWaves = 4;
+constexpr int kTK = 32;                  // keys per tile
+constexpr int kMaxSplits3 = 64;
+constexpr int kMaxSplitPages3 = 512;     // page ids a work-group stages (8,192 tokens)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazy = 8.0f;            // log2 headroom before the running max moves
+constexpr int kCoherent = 16;            // cache policy sc1: agent-coherent access
+constexpr int kBufWord3 = 0x00020000;    // raw buffer descriptor, 32-bit data
+
+template <int HD, int G>
+struct L3 {
+    static constexpr int NB = HD / kQK;
+    static constexpr int ROW = NB * kBlockBytes;        // bytes per token row
+    static constexpr int NCOL = G * NB;                 // (head, block) columns
+    static constexpr int NT = (NCOL + 15) / 16;         // 16-column tiles of them
+    static constexpr int CT = HD / 16;                  // 16-column tiles of the output
+    static constexpr int TILE = 2 * kTK * ROW;          // K rows | V rows
+    static constexpr int NCH = TILE / 16;               // 16-byte chunks per tile
+    static constexpr int CPL = (NCH + 63) / 64;         // chunk loads per lane
+    static constexpr int PAGE_CH = kPage * ROW / 16;    // chunks of one page's K (or V) run
+    static constexpr int QE = (G * HD + kThreads - 1) / kThreads;
+    static constexpr int NE = (2 * HD + kThreads - 1) / kThreads;
+    static constexpr int U = G * HD / 4;                // float4 units of a head group's output
+    static constexpr int PSTRIDE = (G * (HD + 2) + 3) / 4 * 4;   // floats per partial row
+    static constexpr int MERGE = kWaves * G * (HD + 2) * 4;
+    static_assert(NB == 1 || NB == 2 || NB == 4, "a head's blocks share one DPP quad");
+    static_assert(16 % NB == 0, "column tiles hold whole heads");
+    static_assert(kTK * ROW % 16 == 0 && kPage * ROW % 16 == 0, "16-byte chunks");
+    static_assert(MERGE <= kWaves * TILE, "the merge reuses the tile slots");
+    static_assert(U % 1 == 0 && HD % 4 == 0, "float4 units");
+};
+
+template <int HD, int G>
+struct Smem3 {
+    using L = L3<HD, G>;
+    unsigned char qblk[G * L::ROW];          // the group's q rows, quantize_row_q8
+    unsigned char newrow[2 * L::ROW];        // step mode: the new token's K, V
+    int pages[kMaxSplitPages3];              // physical page of each page of the split
+    float wts[G * kMaxSplits3];              // combine weights
+    int last;
+};
+
+__device__ __forceinline__ long lds_ld8(const unsigned char *p) {
+    const uint32_t lo = *reinterpret_cast<const uint32_t *>(p);
+    const uint32_t hi = *reinterpret_cast<const uint32_t *>(p + 4);
+    return (long)(((unsigned long)hi << 32) | lo);
+}
+__device__ __forceinline__ float lds_f(const unsigned char *p) { return *reinterpret_cast<const float *>(p); }
+
+// Key held in slot i (0..7) of lane group g: the rows 4g..4g+3 of the two
+// 16-key halves of the tile, as the score product leaves them.
+__device__ __forceinline__ int slot_key(int g, int i) { return 16 * (i >> 2) + 4 * g + (i & 3); }
+
+// Block-order sum over the NB lanes (h, 0..NB-1) of a head, the same value in
+// each of them: ((0 + x_0) + x_1) + ... as attn_scores_q8_scalar adds.
+template <int NB>
+__device__ __forceinline__ float head_block_sum(float x) {
+#pragma clang fp contract(off)
+    if constexpr (NB == 4) {
+        const float x0 = dpp_f<0x00>(x), x1 = dpp_f<0x55>(x), x2 = dpp_f<0xAA>(x), x3 = dpp_f<0xFF>(x);
+        return (((0.0f + x0) + x1) + x2) + x3;
+    } else if constexpr (NB == 2) {
+        const float x0 = dpp_f<0xA0>(x), x1 = dpp_f<0xF5>(x);   // quad_perm [0,0,2,2], [1,1,3,3]
+        return (0.0f + x0) + x1;
+    } else {
+        return 0.0f + x;
+    }
+}
+
+// Max / sum over lanes l, l^16, l^32, l^48 (the four 16-lane rows), the same
+// value in all four: permlane32_swap pairs rows (0,2) and (1,3),
+// permlane16_swap rows (0,1) and (2,3); lower row first in every add.
+__device__ __forceinline__ float xrow_max(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float xrow_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float m = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+    v2bf v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+// x = hi + lo with hi = bf16(x), lo = bf16(x - hi), four pairs.
+__device__ __forceinline__ void split_bf16(const float (&x)[8], v8bf &hi, v8bf &lo) {
+    u32x4 h, l;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t w = bf16_pair(x[2 * i], x[2 * i + 1]);
+        h[i] = w;
+        l[i] = bf16_pair(x[2 * i] - __uint_as_float(w << 16), x[2 * i + 1] - __uint_as_float(w & 0xFFFF0000u));
+    }
+    hi = __builtin_bit_cast(v8bf, h);
+    lo = __builtin_bit_cast(v8bf, l);
+}
+
+struct RopeIn3 {
+    float x, partner, c, s;
+};
+
+__device__ __forceinline__ RopeIn3 rope_fetch3(const float *head, int col, int hd, const float *ct,
+                                               const float *st) {
+    RopeIn3 r;
+    r.x = head[col];
+    if (ct) {
+        const int half = hd >> 1;
+        const int i = col < half ? col : col - half;
+        r.partner = head[col < half ? col + half : col - half];
+        r.c = ct[i];
+        r.s = st[i];
+    }
+    return r;
+}
+
+__device__ __forceinline__ float rope_value3(const RopeIn3 &r, int col, int hd, bool rotate) {
+    if (!rotate) return r.x;
+    return col < (hd >> 1) ? rope_lower(r.x, r.partner, r.c, r.s) : rope_upper(r.partner, r.x, r.c, r.s);
+}
+
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+
+// 16 bytes from each lane's global address into LDS at dst + 16*lane
+// (global_load_lds_dwordx4; M0 holds the LDS byte address).  Issued as inline
+// assembly so that the compiler does not follow every such copy with a full
+// vmcnt(0) wait before LDS reads: the key loop waits for exactly the slot it
+// reads (wait_copies).  The lgkmcnt(0) makes every earlier LDS read of the slot
+// complete before the copy can land in it.
+__device__ __forceinline__ void dma16(const unsigned char *src, unsigned char *dst) {
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_u8 *)dst;
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(lds)
+                 : "memory", "m0");
+}
+// Wait until at most N copies (vector memory operations) are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_copies() {
+    static_assert(N >= 0 && N < 16, "vmcnt immediate");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
+    using L = L3<HD, G>;
+    constexpr int NB = L::NB, ROW = L::ROW, NT = L::NT, CT = L::CT, CPL = L::CPL;
+    __shared__ __align__(16) Smem3<HD, G> sm;
+    // two tile slots per wave, separate objects so the wait for one slot's
+    // copies does not wait for the other's
+    __shared__ __align__(16) unsigned char slot0[kWaves][L::TILE];
+    __shared__ __align__(16) unsigned char slot1[kWaves][L::TILE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lg = lane >> 4, l16 = lane & 15;
+    const int split = blockIdx.x, kvh = blockIdx.y, qi = blockIdx.z;
+    const int seq = a.seq_of ? a.seq_of[qi] : a.seq_const + a.seq_stride * qi;
+    const int t_begin = split * a.split_tokens;
+    const int split_end = t_begin + a.split_tokens;
+    const PagedView &view = a.view;
+    const bool contig = a.contig_first >= 0;
+
+    // ---- one round trip: len, q rows, new K/V rows, page ids (or K/V itself) ----
+    const int len = a.len_of ? a.len_of[qi] + a.len_plus : a.pos0 + qi + 1;
+    const bool rot = a.cos_t != nullptr;
+    const float *ct_ = rot ? a.cos_t + (size_t)qi * (HD / 2) : nullptr;
+    const float *st_ = rot ? a.sin_t + (size_t)qi * (HD / 2) : nullptr;
+    const float *qg = a.q + ((size_t)qi * a.n_q_heads + (size_t)kvh * G) * HD;
+    RopeIn3 qin[L::QE];
+#pragma unroll
+    for (int i = 0; i < L::QE; i++) {
+        const int e = tid + i * kThreads;
+        if (e < G * HD) qin[i] = rope_fetch3(qg + (e / HD) * HD, e % HD, HD, ct_, st_);
+    }
+    RopeIn3 nin[L::NE];
+    if (a.k_new != nullptr) {
+        const size_t off = ((size_t)qi * a.n_kv_heads + kvh) * HD;
+#pragma unroll
+        for (int i = 0; i < L::NE; i++) {
+            const int e = tid + i * kThreads;
+            if (e < HD) nin[i] = rope_fetch3(a.k_new + off, e, HD, ct_, st_);
+            else if (e < 2 * HD) nin[i].x = a.v_new[off + e - HD];
+        }
+    }
+
+    // Byte offset of this lane's chunk i inside a page's K|V run, and which of
+    // the tile's two pages it comes from: chunk c = lane + 64 i of the tile
+    // image [K page 0 | K page 1 | V page 0 | V page 1].
+    uint32_t coff[CPL];
+    bool csec[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+        const int c = min(lane + 64 * i, L::NCH - 1);
+        const int reg = c / L::PAGE_CH;
+        coff[i] = (uint32_t)((reg >> 1) * (int)view.kv_chunk + 16 * (c - reg * L::PAGE_CH));
+        csec[i] = reg & 1;
+    }
+    const unsigned char *head0 = view.pool + (size_t)kvh * view.head_run;
+    int load_end;   // keys below this are mapped; pages past it are not fetched
+
+    // Physical page of logical page lp of this sequence, or -1.
+    auto page_of = [&](int lp) -> int {
+        if (contig) return lp < a.contig_pages ? a.contig_first + lp : -1;
+        return sm.pages[min(max(lp - t_begin / kPage, 0), kMaxSplitPages3 - 1)];
+    };
+    // Copy the tile with keys [k0, k0+32) into an LDS slot.  A page that is
+    // unmapped (or past load_end) is read from physical page 0 instead: those
+    // keys are masked out.
+    auto fetch = [&](unsigned char *dst, int k0) {
+        int p0 = page_of(k0 / kPage), p1 = page_of(k0 / kPage + 1);
+        p0 = (p0 >= 0 && k0 < load_end) ? p0 : 0;
+        p1 = (p1 >= 0 && k0 + kPage < load_end) ? p1 : 0;
+        const unsigned char *b0 = head0 + (size_t)p0 * view.page_bytes;
+        const unsigned char *b1 = head0 + (size_t)p1 * view.page_bytes;
+#pragma unroll
+        for (int i = 0; i < CPL; i++) {
+            const unsigned char *src = (csec[i] ? b1 : b0) + coff[i];
+            if (64 * (i + 1) <= L::NCH || lane + 64 * i < L::NCH) dma16(src, dst + 1024 * i);
+        }
+    };
+
+    unsigned char *tb0 = slot0[wave];
+    unsigned char *tb1 = slot1[wave];
+    int t_end;
+    if (contig) {
+        // K/V requested at once, before len is known
+        load_end = min(split_end, a.contig_pages * kPage);
+        const int k0 = t_begin + kTK * wave;
+        if (k0 < load_end) fetch(tb0, k0);
+        if (k0 + kTK * kWaves < load_end) fetch(tb1, k0 + kTK * kWaves);
+        if (len <= 0 || t_begin >= len) return;
+        t_end = min(len, split_end);
+        load_end = min(load_end, t_end);
+    } else {
+        const int split_pages = a.split_tokens / kPage;
+        int page_id[(kMaxSplitPages3 + kThreads - 1) / kThreads];
+#pragma unroll
+        for (int i = 0; i < (kMaxSplitPages3 + kThreads - 1) / kThreads; i++) {
+            const int p = tid + i * kThreads;
+            if (p < split_pages) page_id[i] = phys_page(view, seq, t_begin / kPage + p);
+        }
+        if (len <= 0 || t_begin >= len) return;
+#pragma unroll
+        for (int i = 0; i < (kMaxSplitPages3 + kThreads - 1) / kThreads; i++) {
+            const int p = tid + i * kThreads;
+            if (p < split_pages) sm.pages[p] = page_id[i];
+        }
+        t_end = min(len, split_end);
+        load_end = t_end;
+    }
+    const int pos_new = len - 1;
+    const bool owns_new = a.k_new != nullptr && pos_new >= t_begin && pos_new < t_end;
+
+    // ---- RoPE + exact quantize_row_q8 of q (and of the new row) into LDS ----
+#pragma unroll
+    for (int i = 0; i < L::QE; i++) {
+        const int e = tid + i * kThreads;
+        if (e < G * HD) {
+            const int gi = e / HD, col = e % HD;
+            quantize_store32(rope_value3(qin[i], col, HD, rot), sm.qblk + gi * ROW + (col >> 5) * kBlockBytes);
+        }
+    }
+    if (owns_new) {
+#pragma unroll
+        for (int i = 0; i < L::NE; i++) {
+            const int e = tid + i * kThreads;
+            if (e < 2 * HD) {
+                const bool is_v = e >= HD;
+                const int col = is_v ? e - HD : e;
+                const float x = is_v ? nin[i].x : rope_value3(nin[i], col, HD, rot);
+                quantize_store32(x, sm.newrow + (is_v ? ROW : 0) + (col >> 5) * kBlockBytes);
+            }
+        }
+    }
+    __syncthreads();
+    if (!contig) {
+        const int k0 = t_begin + kTK * wave;
+        if (k0 < load_end) fetch(tb0, k0);
+        if (k0 + kTK * kWaves < load_end) fetch(tb1, k0 + kTK * kWaves);
+    }
+    if (owns_new) {
+        const int phys = page_of(pos_new / kPage);
+        if (phys >= 0 && tid < 2 * (ROW / 4)) {
+            const bool is_v = tid >= ROW / 4;
+            const int w = is_v ? tid - ROW / 4 : tid;
+            unsigned char *dst = head_run_ptr(view, phys, kvh) + (is_v ? view.kv_chunk : 0) +
+                                 (pos_new % kPage) * ROW + 4 * w;
+            *reinterpret_cast<uint32_t *>(dst) =
+                *reinterpret_cast<const uint32_t *>(sm.newrow + (is_v ? ROW : 0) + 4 * w);
+        }
+    }
+
+    // ---- per-lane constants: column (h, b) = 16*nt + l16 of the products ----
+    const int bl = l16 % NB;                  // block of this lane's columns (same in every nt)
+    long qb[NT][NB];                          // B operand of the score product for block b'
+    float qdl[NT];                            // qd[h][b]
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int h = (16 * nt + l16) / NB;
+        const bool real = h < G;
+        const unsigned char *qrow = sm.qblk + min(h, G - 1) * ROW;
+        qdl[nt] = real ? lds_f(qrow + bl * kBlockBytes) : 0.0f;
+#pragma unroll
+        for (int bb = 0; bb < NB; bb++) {
+            const long c = lds_ld8(qrow + bb * kBlockBytes + 4 + 8 * lg);
+            qb[nt][bb] = (real && bb == bl) ? c : 0;
+        }
+    }
+
+    v4f o[CT][NT];
+#pragma unroll
+    for (int c = 0; c < CT; c++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) o[c][nt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run[NT], l_run[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        m_run[nt] = -INFINITY;
+        l_run[nt] = 0.0f;
+    }
+    const float scale = a.scale;
+    const int pr_new = owns_new ? pos_new : -1;
+
+    // One staged tile with keys [k0, k0 + 32) in tb.
+    auto process = [&](const unsigned char *tb, int k0) {
+        const unsigned char *Kt = tb;
+        const unsigned char *Vt = tb + kTK * ROW;
+        bool valid[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) valid[i] = k0 + slot_key(lg, i) < t_end;
+
+        // scores: exact int32 block dots, column (h, b) keeps block b
+        v4i acc[2][NT];
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) acc[st][nt] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+#pragma unroll
+            for (int bb = 0; bb < NB; bb++) {
+                const long ka = lds_ld8(Kt + (16 * st + l16) * ROW + bb * kBlockBytes + 4 + 8 * lg);
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    acc[st][nt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ka, qb[nt][bb], acc[st][nt], 0, 0, 0);
+            }
+        }
+        float kd[8], vd[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            kd[i] = lds_f(Kt + slot_key(lg, i) * ROW + bl * kBlockBytes);
+            vd[i] = lds_f(Vt + slot_key(lg, i) * ROW + bl * kBlockBytes);
+        }
+
+        v8bf whi[NT], wlo[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            float s[8];
+            {
+#pragma clang fp contract(off)
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float x = (float)acc[i >> 2][nt][i & 3] * (qdl[nt] * kd[i]);
+                    const float sc = head_block_sum<NB>(x) * scale;
+                    s[i] = valid[i] ? sc * kLog2e : -INFINITY;
+                }
+            }
+            float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+            mx = xrow_max(mx);
+            const float m_new = mx > m_run[nt] + kLazy ? mx : m_run[nt];
+            const float corr = __builtin_amdgcn_exp2f(m_run[nt] - m_new);
+            m_run[nt] = m_new;
+            float w[8];
+            float ps = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float p = __builtin_amdgcn_exp2f(s[i] - m_new);
+                ps += p;
+                w[i] = valid[i] ? p * vd[i] : 0.0f;
+            }
+            l_run[nt] = l_run[nt] * corr + xrow_sum(ps);
+            if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0) {
+#pragma unroll
+                for (int c = 0; c < CT; c++) o[c][nt] *= corr;
+            }
+            split_bf16(w, whi[nt], wlo[nt]);
+        }
+
+        // P.V: A = V codes of 16 columns x the 32 keys in slot order
+#pragma unroll
+        for (int c = 0; c < CT; c++) {
+            const int col = 16 * c + l16;
+            const unsigned char *vcol = Vt + (col >> 5) * kBlockBytes + 4 + (col & 31);
+            float vf[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) vf[i] = (float)(int)(int8_t)vcol[slot_key(lg, i) * ROW];
+            u32x4 pk;
+#pragma unroll
+            for (int i = 0; i < 4; i++) pk[i] = bf16_pair(vf[2 * i], vf[2 * i + 1]);
+            const v8bf av = __builtin_bit_cast(v8bf, pk);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                o[c][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, whi[nt], o[c][nt], 0, 0, 0);
+                o[c][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, wlo[nt], o[c][nt], 0, 0, 0);
+            }
+        }
+    };
+
+    // The new row replaces what the copy saw at pos_new.
+    auto patch = [&](unsigned char *tb, int k0) {
+        if (pr_new >= k0 && pr_new < k0 + kTK) {
+            const int r = pr_new - k0;
+            for (int w = lane; w < 2 * (ROW / 4); w += 64) {
+                const bool is_v = w >= ROW / 4;
+                const int ww = is_v ? w - ROW / 4 : w;
+                *reinterpret_cast<uint32_t *>(tb + (is_v ? kTK * ROW : 0) + r * ROW + 4 * ww) =
+                    *reinterpret_cast<const uint32_t *>(sm.newrow + (is_v ? ROW : 0) + 4 * ww);
+            }
+        }
+    };
+
+    // ---- the key loop: process a slot, refill it eight tiles on ----
+    const int n_tiles = (t_end - t_begin + kTK - 1) / kTK;
+    const int my_tiles = wave < n_tiles ? (n_tiles - wave + kWaves - 1) / kWaves : 0;
+    // Before tile j is read, its copies are done: the copies of tile j+1 (if it
+    // is one of ours, already issued after tile j's) may stay in flight.
+    auto wait_tile = [&](int j) {
+        if (j + 1 < my_tiles)
+            wait_copies<CPL>();
+        else
+            wait_copies<0>();
+    };
+    for (int it = 0; it < my_tiles; it += 2) {
+        {
+            const int k0 = t_begin + kTK * (wave + kWaves * it);
+            wait_tile(it);
+            patch(tb0, k0);
+            process(tb0, k0);
+            const int kn = k0 + 2 * kTK * kWaves;
+            if (kn < load_end) fetch(tb0, kn);
+        }
+        if (it + 1 < my_tiles) {
+            const int k0 = t_begin + kTK * (wave + kWaves * (it + 1));
+            wait_tile(it + 1);
+            patch(tb1, k0);
+            process(tb1, k0);
+            const int kn = k0 + 2 * kTK * kWaves;
+            if (kn < load_end) fetch(tb1, kn);
+        }
+    }
+
+    // ---- merge the four waves in wave order ----
+    __builtin_amdgcn_s_waitcnt(0);   // no copy into a slot is still in flight
+    __syncthreads();                 // every wave is done with its slots
+    float *mw = reinterpret_cast<float *>(&slot0[0][0]);     // [4][G]
+    float *lw = mw + kWaves * G;                               // [4][G]
+    float *ow = lw + kWaves * G;                               // [4][G][HD]
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int h = (16 * nt + l16) / NB;
+        if (h < G) {
+            if (lg == 0 && bl == 0) {
+                mw[wave * G + h] = m_run[nt];
+                lw[wave * G + h] = l_run[nt];
+            }
+#pragma unroll
+            for (int c = 0; c < CT; c++) {
+                if ((c >> 1) == bl)
+                    *reinterpret_cast<v4f *>(ow + (wave * G + h) * HD + 16 * c + 4 * lg) = o[c][nt];
+            }
+        }
+    }
+    __syncthreads();
+
+    const size_t out_row = (size_t)qi * a.n_q_heads + (size_t)kvh * G;
+    const size_t pbase = ((size_t)qi * a.n_kv_heads + kvh) * a.n_splits;
+    const bool single = a.n_splits == 1;
+    // partial rows of this (query, kv head); accesses past n_splits rows read 0
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        single ? a.out : a.partials + pbase * L::PSTRIDE, 0, single ? 0 : a.n_splits * L::PSTRIDE * 4, kBufWord3);
+    for (int u = tid; u < L::U; u += kThreads) {
+        const int h = (4 * u) / HD, j = 4 * u - h * HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, mw[w * G + h]);
+        v4f O = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        float Lsum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            const float f = __builtin_amdgcn_exp2f(mw[w * G + h] - M);
+            O += f * *reinterpret_cast<const v4f *>(ow + (w * G + h) * HD + j);
+            Lsum += f * lw[w * G + h];
+        }
+        if (single) {
+            *reinterpret_cast<v4f *>(a.out + (out_row + h) * HD + j) = O / Lsum;
+        } else {
+            // (the buffer intrinsics move raw 32-bit words: floats go through bit casts)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, O), prs, (split * L::PSTRIDE + 4 * u) * 4,
+                                                   0, kCoherent);
+            if (j == 0) {
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M), prs, (split * L::PSTRIDE + G * HD + h) * 4, 0,
+                                                      kCoherent);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Lsum), prs,
+                                                      (split * L::PSTRIDE + G * HD + G + h) * 4, 0, kCoherent);
+            }
+        }
+    }
+    if (single) return;
+    __builtin_amdgcn_s_waitcnt(0);   // the partial is at the point of coherence
+    __syncthreads();
+
+    // ---- the last work-group of this (query, kv head) to arrive combines ----
+    const int nvalid = (len + a.split_tokens - 1) / a.split_tokens;
+    int *counter = a.counters + (size_t)qi * a.n_kv_heads + kvh;
+    if (tid == 0)
+        sm.last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nvalid - 1;
+    __syncthreads();
+    if (!sm.last) return;
+    if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // Thread (unit u, split subset sg) sums splits sg, sg + NSG, ... of float4
+    // unit u.  The first CL rows are requested together with (m, l), before
+    // the weights are known.
+    constexpr int NSG = L::U >= kThreads ? 1 : kThreads / L::U;
+    constexpr int TPS = L::U >= kThreads ? kThreads : L::U;
+    constexpr int CL = 16;
+    const int sg = tid / TPS;
+    const bool active = sg < NSG;   // TPS * NSG can fall short of the 256 threads
+    float mv[2], lv[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int h = min(wave + kWaves * r, G - 1);
+        mv[r] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(prs, (lane * L::PSTRIDE + G * HD + h) * 4, 0, kCoherent));
+        lv[r] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(prs, (lane * L::PSTRIDE + G * HD + G + h) * 4, 0, kCoherent));
+    }
+    float *red = reinterpret_cast<float *>(&slot1[0][0]);     // [NSG][TPS][4]
+    for (int u0 = 0; u0 < L::U; u0 += TPS) {
+        const int u = u0 + tid % TPS;
+        v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s0 = 0; s0 < nvalid; s0 += NSG * CL) {
+            v4f rows[CL];
+#pragma unroll
+            for (int i = 0; i < CL; i++) {
+                const int s = min(s0 + sg + NSG * i, kMaxSplits3);
+                rows[i] = active ? __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                                               prs, (s * L::PSTRIDE + 4 * u) * 4, 0, kCoherent))
+                                 : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            if (u0 == 0 && s0 == 0) {
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    const int h = wave + kWaves * r;
+                    if (h < G) {
+                        const bool ok = lane < nvalid;
+                        const float m = ok ? mv[r] : -INFINITY;
+                        const float M = wave_max(m);
+                        const float f = ok ? __builtin_amdgcn_exp2f(m - M) : 0.0f;
+                        sm.wts[h * kMaxSplits3 + lane] = f / wave_sum(ok ? lv[r] * f : 0.0f);
+                    }
+                }
+                __syncthreads();
+            }
+            const float *wt = sm.wts + ((4 * u) / HD) * kMaxSplits3;
+#pragma unroll
+            for (int i = 0; i < CL; i++) {
+                // rows past nvalid are stale or zero: selected out, never weighted
+                const int s = s0 + sg + NSG * i;
+                if (s < nvalid) acc += wt[min(s, kMaxSplits3 - 1)] * rows[i];
+            }
+        }
+        if constexpr (NSG == 1) {
+            const int h = (4 * u) / HD;
+            if (active) *reinterpret_cast<v4f *>(a.out + (out_row + h) * HD + (4 * u - h * HD)) = acc;
+        } else {
+            *reinterpret_cast<v4f *>(red + 4 * tid) = acc;
+            __syncthreads();
+            if (tid < TPS) {
+                v4f r = *reinterpret_cast<const v4f *>(red + 4 * tid);
+                for (int g = 1; g < NSG; g++) r += *reinterpret_cast<const v4f *>(red + 4 * (g * TPS + tid));
+                const int uu = u0 + tid;
+                const int h = (4 * uu) / HD;
+                *reinterpret_cast<v4f *>(a.out + (out_row + h) * HD + (4 * uu - h * HD)) = r;
+            }
+            __syncthreads();
+        }
+    }
+}
+
+template <int HD, int G>
+hipError_t launch3_hd_g(const TqDecodeArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL((decode3_kernel<HD, G>), dim3(a.n_splits, a.n_kv_heads, a.n_q), dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch3_hd(const TqDecodeArgs &a, int g, hipStream_t s) {
+    switch (g) {
+        case 1: return launch3_hd_g<HD, 1>(a, s);
+        case 2: return launch3_hd_g<HD, 2>(a, s);
+        case 3: return launch3_hd_g<HD, 3>(a, s);
+        case 4: return launch3_hd_g<HD, 4>(a, s);
+        case 5: return launch3_hd_g<HD, 5>(a, s);
+        case 6: return launch3_hd_g<HD, 6>(a, s);
+        case 7: return launch3_hd_g<HD, 7>(a, s);
+        case 8: return launch3_hd_g<HD, 8>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+bool tq_decode3_supported(int head_dim, int group) {
+    const bool hd_ok = head_dim == 32 || head_dim == 64 || head_dim == 128;
+    return hd_ok && group >= 1 && group <= 8;
+}
+
+int tq_decode3_max_splits() { return kMaxSplits3; }
+int tq_decode3_max_split_tokens() { return kMaxSplitPages3 * kPage; }
+int tq_decode3_partial_floats(int head_dim, int group) { return (group * (head_dim + 2) + 3) / 4 * 4; }
+
+hipError_t tq_launch_decode3(const TqDecodeArgs &a, hipStream_t s) {
+    if (a.n_q <= 0) return hipSuccess;
+    if (a.n_splits < 1 || a.n_splits > kMaxSplits3 || a.split_tokens <= 0 || a.split_tokens % kTK != 0 ||
+        a.split_tokens > kMaxSplitPages3 * kPage)
+        return hipErrorInvalidValue;
+    if (a.n_splits > 1 && (a.partials == nullptr || a.counters == nullptr)) return hipErrorInvalidValue;
+    const int g = a.n_q_heads / a.n_kv_heads;
+    if (!tq_decode3_supported(a.head_dim, g)) return hipErrorInvalidValue;
+    switch (a.head_dim) {
+        case 32: return launch3_hd<32>(a, g, s);
+        case 64: return launch3_hd<64>(a, g, s);
+        case 128: return launch3_hd<128>(a, g, s);
+        default: return hipErrorInvalidValue;
+    }
+}

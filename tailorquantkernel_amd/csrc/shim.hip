@@ -95,6 +95,46 @@ void plan_splits(const tq_hip_kv *kv, int n_q, int max_len, int *split_tokens, i
     *n_splits = (chunks + per - 1) / per;
 }
 
+// Which decode kernel serves a call: the MFMA kernel (decode3.hip) wherever it
+// covers the shape, else the VALU kernel (decode.hip).  TQ_HIP_DECODE_KERNEL=1
+// forces the VALU kernel (for comparisons).
+bool use_decode3(const tq_hip_kv *kv) {
+    static int forced = [] {
+        const char *s = getenv("TQ_HIP_DECODE_KERNEL");
+        return s ? atoi(s) : 0;
+    }();
+    return forced != 1 && tq_decode3_supported(kv->desc.head_dim, kv->desc.n_q_heads / kv->desc.n_kv_heads);
+}
+
+// Longest split (tokens) the MFMA decode gives one work-group when the split
+// count allows: shorter splits keep ragged batches balanced over the CUs.
+int decode3_split_cap() {
+    static int v = [] {
+        const char *s = getenv("TQ_HIP_DECODE_SPLIT_CAP");
+        const int x = s ? atoi(s) : 0;
+        return x > 0 ? x : 1024;
+    }();
+    return v;
+}
+
+// MFMA decode: splits are whole units of 128 tokens (four waves x 32 keys).
+// Aim at decode_wg_target() work-groups, at most decode3_split_cap() tokens per
+// split, and never more splits than the combine takes.
+void plan_splits3(const tq_hip_kv *kv, int n_q, int max_len, int *split_tokens, int *n_splits) {
+    constexpr int unit = 128;
+    const long units = std::max(1, (max_len + unit - 1) / unit);
+    const long pairs = (long)n_q * kv->desc.n_kv_heads;
+    const long cap = tq_decode3_max_splits();
+    long want = (decode_wg_target() + pairs - 1) / pairs;
+    want = std::max(1L, std::min(std::min(want, cap), units));
+    long per = (units + want - 1) / want;
+    per = std::min<long>(per, std::max(1, decode3_split_cap() / unit));
+    per = std::max(per, (units + cap - 1) / cap);
+    per = std::min<long>(per, tq_decode3_max_split_tokens() / unit);
+    *split_tokens = (int)(per * unit);
+    *n_splits = (int)((units + per - 1) / per);
+}
+
 // Longest context one decode call serves for this cache's shape.
 long max_context(const tq_hip_kv *kv) {
     const int g = kv->desc.n_q_heads / kv->desc.n_kv_heads;
@@ -234,17 +274,22 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
             a.contig_pages = n;
         }
     }
-    plan_splits(kv, n_q, max_len, &a.split_tokens, &a.n_splits);
+    const bool v3 = use_decode3(kv);
+    if (v3)
+        plan_splits3(kv, n_q, max_len, &a.split_tokens, &a.n_splits);
+    else
+        plan_splits(kv, n_q, max_len, &a.split_tokens, &a.n_splits);
     if (a.n_splits > 1) {
         const int g = D.n_q_heads / D.n_kv_heads;
-        const size_t bytes = (size_t)n_q * D.n_kv_heads * a.n_splits * g * (D.head_dim + 2) * sizeof(float);
+        const size_t row = v3 ? (size_t)tq_decode3_partial_floats(D.head_dim, g) : (size_t)g * (D.head_dim + 2);
+        const size_t bytes = (size_t)n_q * D.n_kv_heads * a.n_splits * row * sizeof(float);
         int rc = ensure_partials(kv, bytes);
         if (rc == TQ_HIP_OK) rc = ensure_counters(kv, (size_t)n_q * D.n_kv_heads, s);
         if (rc != TQ_HIP_OK) return rc;
         a.partials = kv->partials;
         a.counters = kv->counters;
     }
-    return herr(tq_launch_decode(a, s));
+    return herr(v3 ? tq_launch_decode3(a, s) : tq_launch_decode(a, s));
 }
 
 bool seq_ok(const tq_hip_kv *kv, int seq) { return kv && seq >= 0 && seq < kv->desc.max_seqs; }

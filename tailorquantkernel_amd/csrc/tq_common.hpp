@@ -228,6 +228,15 @@ int tq_decode_max_splits(int head_dim, int group);
 int tq_decode_max_split_tokens();
 bool tq_decode_supported(int head_dim, int group);
 hipError_t tq_launch_decode(const TqDecodeArgs &a, hipStream_t s);
+// The MFMA decode kernel (decode3.hip): head_dim 32/64/128, groups 1..8;
+// split_tokens a multiple of 32, at most tq_decode3_max_splits() splits of at
+// most tq_decode3_max_split_tokens() tokens.
+bool tq_decode3_supported(int head_dim, int group);
+int tq_decode3_max_splits();
+int tq_decode3_max_split_tokens();
+// Floats per split partial row of the MFMA decode (16-byte aligned rows).
+int tq_decode3_partial_floats(int head_dim, int group);
+hipError_t tq_launch_decode3(const TqDecodeArgs &a, hipStream_t s);
 
 struct TqPrefillArgs {
     tq::PagedView view;
