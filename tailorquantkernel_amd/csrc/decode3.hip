@@ -15,10 +15,11 @@
 //           codes of block b' in the columns with b == b' and zeros elsewhere,
 //           so accumulating the NB products leaves the exact int32 block dot
 //           sum_j q[h][b][j]*k[key][b][j] in column (h,b), every lane useful at
-//           G*NB = 16.  Each lane scales its dots by qd*kd and the NB lanes of
-//           a head add them in block order with DPP moves: the score
-//           ((0 + x_0) + x_1) + ... then *scale is bit-identical to
-//           attn_scores_q8_scalar (model/attn_q8.c:17-34).
+//           G*NB = 16.  Each lane scales its dots by qd*kd (qd pre-multiplied
+//           by the softmax scale and log2 e) and the NB lanes of a head add
+//           them with two DPP butterflies: the score of attn_scores_q8_scalar
+//           (model/attn_q8.c:17-34) up to fp32 rounding order, in the exp2
+//           domain.
 //   softmax online, per lane, exp2 domain; max and sum over the four 16-lane
 //           rows holding the tile's keys with permlane32/16 swaps.  The
 //           running max moves only when a tile exceeds it by more than 2^8,
@@ -104,20 +105,13 @@ __device__ __forceinline__ float lds_f(const unsigned char *p) { return *reinter
 // 16-key halves of the tile, as the score product leaves them.
 __device__ __forceinline__ int slot_key(int g, int i) { return 16 * (i >> 2) + 4 * g + (i & 3); }
 
-// Block-order sum over the NB lanes (h, 0..NB-1) of a head, the same value in
-// each of them: ((0 + x_0) + x_1) + ... as attn_scores_q8_scalar adds.
+// Sum over the NB lanes (h, 0..NB-1) of a head, (x0 + x1) + (x2 + x3): the
+// same value in each of them (fp32 add commutes).
 template <int NB>
 __device__ __forceinline__ float head_block_sum(float x) {
-#pragma clang fp contract(off)
-    if constexpr (NB == 4) {
-        const float x0 = dpp_f<0x00>(x), x1 = dpp_f<0x55>(x), x2 = dpp_f<0xAA>(x), x3 = dpp_f<0xFF>(x);
-        return (((0.0f + x0) + x1) + x2) + x3;
-    } else if constexpr (NB == 2) {
-        const float x0 = dpp_f<0xA0>(x), x1 = dpp_f<0xF5>(x);   // quad_perm [0,0,2,2], [1,1,3,3]
-        return (0.0f + x0) + x1;
-    } else {
-        return 0.0f + x;
-    }
+    if constexpr (NB >= 2) x += dpp_f<kDppQuadXor1>(x);
+    if constexpr (NB == 4) x += dpp_f<kDppQuadXor2>(x);
+    return x;
 }
 
 // Max / sum over lanes l, l^16, l^32, l^48 (the four 16-lane rows), the same
@@ -153,50 +147,35 @@ __device__ __forceinline__ void split_bf16(const float (&x)[8], v8bf &hi, v8bf &
     lo = __builtin_bit_cast(v8bf, l);
 }
 
-struct RopeIn3 {
-    float x, partner, c, s;
-};
-
-__device__ __forceinline__ RopeIn3 rope_fetch3(const float *head, int col, int hd, const float *ct,
-                                               const float *st) {
-    RopeIn3 r;
-    r.x = head[col];
-    if (ct) {
-        const int half = hd >> 1;
-        const int i = col < half ? col : col - half;
-        r.partner = head[col < half ? col + half : col - half];
-        r.c = ct[i];
-        r.s = st[i];
-    }
-    return r;
-}
-
-__device__ __forceinline__ float rope_value3(const RopeIn3 &r, int col, int hd, bool rotate) {
-    if (!rotate) return r.x;
-    return col < (hd >> 1) ? rope_lower(r.x, r.partner, r.c, r.s) : rope_upper(r.partner, r.x, r.c, r.s);
-}
-
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
 
 // 16 bytes from each lane's global address into LDS at dst + 16*lane
-// (global_load_lds_dwordx4; M0 holds the LDS byte address).  Issued as inline
-// assembly so that the compiler does not follow every such copy with a full
-// vmcnt(0) wait before LDS reads: the key loop waits for exactly the slot it
-// reads (wait_copies).  The lgkmcnt(0) makes every earlier LDS read of the slot
-// complete before the copy can land in it.
-__device__ __forceinline__ void dma16(const unsigned char *src, unsigned char *dst) {
+// (global_load_lds_dwordx4; M0 holds the LDS byte address and is restored).
+// Issued as inline assembly so that the compiler does not follow every such
+// copy with a full vmcnt(0) wait before LDS accesses: the kernel waits for
+// exactly the copies it needs (wait_copies), counting them in issue order.
+// No memory clobber: LDS reads of a slot are ordered before a refill by
+// wait_lds() (a compiler barrier plus lgkmcnt(0)) and after its copies by
+// wait_copies(); leaving memory unclobbered keeps the uniform loads that
+// precede the copies scalar.
+__device__ __forceinline__ void dma16(const void *src, unsigned char *dst) {
     const uint32_t lds = (uint32_t)(uintptr_t)(lds_u8 *)dst;
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-                 :
-                 : "v"(src), "s"(lds)
-                 : "memory", "m0");
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(lds));
 }
-// Wait until at most N copies (vector memory operations) are outstanding.
+// Wait until at most N vector memory operations of this wave are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_copies() {
-    static_assert(N >= 0 && N < 16, "vmcnt immediate");
+    static_assert(N >= 0 && N < 64, "vmcnt immediate");
     asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
+// Every LDS access issued so far has completed (before a copy may land on
+// memory those accesses touch).
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); }
 
 template <int HD, int G>
 __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
@@ -213,32 +192,49 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lg = lane >> 4, l16 = lane & 15;
     const int split = blockIdx.x, kvh = blockIdx.y, qi = blockIdx.z;
-    const int seq = a.seq_of ? a.seq_of[qi] : a.seq_const + a.seq_stride * qi;
     const int t_begin = split * a.split_tokens;
     const int split_end = t_begin + a.split_tokens;
     const PagedView &view = a.view;
     const bool contig = a.contig_first >= 0;
-
-    // ---- one round trip: len, q rows, new K/V rows, page ids (or K/V itself) ----
-    const int len = a.len_of ? a.len_of[qi] + a.len_plus : a.pos0 + qi + 1;
     const bool rot = a.cos_t != nullptr;
-    const float *ct_ = rot ? a.cos_t + (size_t)qi * (HD / 2) : nullptr;
-    const float *st_ = rot ? a.sin_t + (size_t)qi * (HD / 2) : nullptr;
-    const float *qg = a.q + ((size_t)qi * a.n_q_heads + (size_t)kvh * G) * HD;
-    RopeIn3 qin[L::QE];
-#pragma unroll
-    for (int i = 0; i < L::QE; i++) {
-        const int e = tid + i * kThreads;
-        if (e < G * HD) qin[i] = rope_fetch3(qg + (e / HD) * HD, e % HD, HD, ct_, st_);
-    }
-    RopeIn3 nin[L::NE];
-    if (a.k_new != nullptr) {
-        const size_t off = ((size_t)qi * a.n_kv_heads + kvh) * HD;
-#pragma unroll
-        for (int i = 0; i < L::NE; i++) {
-            const int e = tid + i * kThreads;
-            if (e < HD) nin[i] = rope_fetch3(a.k_new + off, e, HD, ct_, st_);
-            else if (e < 2 * HD) nin[i].x = a.v_new[off + e - HD];
+    const bool step = a.k_new != nullptr;
+    unsigned char *tb0 = slot0[wave];
+    unsigned char *tb1 = slot1[wave];
+    // Uniform inputs: issued first as unconditional scalar loads (a dummy
+    // address when absent), used only after the copies below are issued, so
+    // the copies do not wait for them.
+    const int len_raw = *(a.len_of ? a.len_of + qi : reinterpret_cast<const int32_t *>(a.q));
+    const int seq_raw = *(a.seq_of ? a.seq_of + qi : reinterpret_cast<const int32_t *>(a.q));
+
+    // ---- 1. this wave's copy of the inputs it quantizes, into the tail-free
+    //      front of its second slot: q rows of the group | cos | sin | new K | new V
+    //      (fp32).  These copies go first so that waiting for them lets every
+    //      later K/V copy stay in flight.
+    float *stq = reinterpret_cast<float *>(tb1);
+    float *stc = stq + G * HD;
+    float *sts = stc + HD / 2;
+    float *stk = sts + HD / 2;
+    float *stv = stk + HD;
+    {
+        // 16-byte chunks per part; the cos/sin slots are always there (without
+        // RoPE they repeat q) so every part sits at a fixed offset
+        constexpr int QC = G * HD / 4, RC = HD / 8, NC = HD / 4;
+        const int nch = QC + 2 * RC + (step ? 2 * NC : 0);
+        const float *qg = a.q + ((size_t)qi * a.n_q_heads + (size_t)kvh * G) * HD;
+        const size_t nrow = ((size_t)qi * a.n_kv_heads + kvh) * HD;
+        for (int c0 = 0; c0 < nch; c0 += 64) {
+            const int c = c0 + lane;
+            const float *src = qg;
+            if (c < QC) {
+                src = qg + 4 * c;
+            } else if (c < QC + 2 * RC) {
+                const int r = c - QC;
+                if (rot) src = (r < RC ? a.cos_t : a.sin_t) + (size_t)qi * (HD / 2) + 4 * (r < RC ? r : r - RC);
+            } else if (c < nch) {
+                const int r = c - QC - 2 * RC;
+                src = (r < NC ? a.k_new : a.v_new) + nrow + 4 * (r < NC ? r : r - NC);
+            }
+            if (c0 + 64 <= nch || c < nch) dma16(src, tb1 + 16 * c0);
         }
     }
 
@@ -262,9 +258,9 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
         if (contig) return lp < a.contig_pages ? a.contig_first + lp : -1;
         return sm.pages[min(max(lp - t_begin / kPage, 0), kMaxSplitPages3 - 1)];
     };
-    // Copy the tile with keys [k0, k0+32) into an LDS slot.  A page that is
-    // unmapped (or past load_end) is read from physical page 0 instead: those
-    // keys are masked out.
+    // Copy the tile with keys [k0, k0+32) into an LDS slot (CPL copies).  A page
+    // that is unmapped (or past load_end) is read from physical page 0
+    // instead: those keys are masked out.
     auto fetch = [&](unsigned char *dst, int k0) {
         int p0 = page_of(k0 / kPage), p1 = page_of(k0 / kPage + 1);
         p0 = (p0 >= 0 && k0 < load_end) ? p0 : 0;
@@ -278,19 +274,26 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
         }
     };
 
-    unsigned char *tb0 = slot0[wave];
-    unsigned char *tb1 = slot1[wave];
+    // ---- 2. the first tile (contiguous sequence: before len is known) ----
+    const int k_first = t_begin + kTK * wave;
+    bool first_issued = false;
+    if (contig) {
+        load_end = min(split_end, a.contig_pages * kPage);
+        if (k_first < load_end) {
+            fetch(tb0, k_first);
+            first_issued = true;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int len = a.len_of ? len_raw + a.len_plus : a.pos0 + qi + 1;
+    const int seq = a.seq_of ? seq_raw : a.seq_const + a.seq_stride * qi;
     int t_end;
     if (contig) {
-        // K/V requested at once, before len is known
-        load_end = min(split_end, a.contig_pages * kPage);
-        const int k0 = t_begin + kTK * wave;
-        if (k0 < load_end) fetch(tb0, k0);
-        if (k0 + kTK * kWaves < load_end) fetch(tb1, k0 + kTK * kWaves);
         if (len <= 0 || t_begin >= len) return;
         t_end = min(len, split_end);
         load_end = min(load_end, t_end);
     } else {
+        // paged: the split's page ids through LDS (the only barrier before the merge)
         const int split_pages = a.split_tokens / kPage;
         int page_id[(kMaxSplitPages3 + kThreads - 1) / kThreads];
 #pragma unroll
@@ -306,46 +309,60 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
         }
         t_end = min(len, split_end);
         load_end = t_end;
-    }
-    const int pos_new = len - 1;
-    const bool owns_new = a.k_new != nullptr && pos_new >= t_begin && pos_new < t_end;
-
-    // ---- RoPE + exact quantize_row_q8 of q (and of the new row) into LDS ----
-#pragma unroll
-    for (int i = 0; i < L::QE; i++) {
-        const int e = tid + i * kThreads;
-        if (e < G * HD) {
-            const int gi = e / HD, col = e % HD;
-            quantize_store32(rope_value3(qin[i], col, HD, rot), sm.qblk + gi * ROW + (col >> 5) * kBlockBytes);
+        __syncthreads();
+        if (k_first < load_end) {
+            fetch(tb0, k_first);
+            first_issued = true;
         }
     }
-    if (owns_new) {
-#pragma unroll
-        for (int i = 0; i < L::NE; i++) {
-            const int e = tid + i * kThreads;
-            if (e < 2 * HD) {
-                const bool is_v = e >= HD;
-                const int col = is_v ? e - HD : e;
-                const float x = is_v ? nin[i].x : rope_value3(nin[i], col, HD, rot);
-                quantize_store32(x, sm.newrow + (is_v ? ROW : 0) + (col >> 5) * kBlockBytes);
+    // the staged inputs have landed; the first tile may still be in flight
+    if (first_issued)
+        wait_copies<CPL>();
+    else
+        wait_copies<0>();
+    const int pos_new = len - 1;
+    const bool owns_new = step && pos_new >= t_begin && pos_new < t_end;
+    // the one wave whose tiles hold pos_new appends the new token
+    const bool wave_new = owns_new && ((pos_new - t_begin) / kTK) % kWaves == wave;
+
+    // ---- 3. RoPE + exact quantize_row_q8 of the group's q rows and, in the
+    //      work-group that appends, of the new K (after RoPE) and V rows: the
+    //      32-value blocks are dealt round-robin to the four waves, each half-wave
+    //      one block (every wave staged all inputs) ----
+    {
+        constexpr int NQB = G * NB;
+        const int nblk = NQB + (owns_new ? 2 * NB : 0);
+        for (int j0 = 2 * wave; j0 < nblk; j0 += 2 * kWaves) {
+            const int j = j0 + (lane >> 5);
+            if (j < nblk) {   // a whole 32-lane block is in or out
+                const bool is_q = j < NQB;
+                const int jr = is_q ? j : j - NQB;           // new row: K blocks then V blocks
+                const int b = jr % NB;
+                const int col = 32 * b + (lane & 31);
+                const bool is_v = !is_q && jr >= NB;
+                const float *row = is_q ? stq + (j / NB) * HD : (is_v ? stv : stk);
+                float x = row[col];
+                if (rot && !is_v) {
+                    const int half = HD / 2;
+                    const int pi = col < half ? col : col - half;
+                    x = col < half ? rope_lower(row[col], row[col + half], stc[pi], sts[pi])
+                                   : rope_upper(row[col - half], row[col], stc[pi], sts[pi]);
+                }
+                unsigned char *dst = is_q ? sm.qblk + (j / NB) * ROW : sm.newrow + (is_v ? ROW : 0);
+                quantize_store32(x, dst + b * kBlockBytes);
             }
         }
     }
     __syncthreads();
-    if (!contig) {
-        const int k0 = t_begin + kTK * wave;
-        if (k0 < load_end) fetch(tb0, k0);
-        if (k0 + kTK * kWaves < load_end) fetch(tb1, k0 + kTK * kWaves);
-    }
     if (owns_new) {
         const int phys = page_of(pos_new / kPage);
         if (phys >= 0 && tid < 2 * (ROW / 4)) {
             const bool is_v = tid >= ROW / 4;
-            const int w = is_v ? tid - ROW / 4 : tid;
+            const int ww = is_v ? tid - ROW / 4 : tid;
             unsigned char *dst = head_run_ptr(view, phys, kvh) + (is_v ? view.kv_chunk : 0) +
-                                 (pos_new % kPage) * ROW + 4 * w;
+                                 (pos_new % kPage) * ROW + 4 * ww;
             *reinterpret_cast<uint32_t *>(dst) =
-                *reinterpret_cast<const uint32_t *>(sm.newrow + (is_v ? ROW : 0) + 4 * w);
+                *reinterpret_cast<const uint32_t *>(sm.newrow + (is_v ? ROW : 0) + 4 * ww);
         }
     }
 
@@ -358,13 +375,22 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
         const int h = (16 * nt + l16) / NB;
         const bool real = h < G;
         const unsigned char *qrow = sm.qblk + min(h, G - 1) * ROW;
-        qdl[nt] = real ? lds_f(qrow + bl * kBlockBytes) : 0.0f;
+        qdl[nt] = real ? lds_f(qrow + bl * kBlockBytes) * (a.scale * kLog2e) : 0.0f;
 #pragma unroll
         for (int bb = 0; bb < NB; bb++) {
             const long c = lds_ld8(qrow + bb * kBlockBytes + 4 + 8 * lg);
             qb[nt][bb] = (real && bb == bl) ? c : 0;
         }
     }
+
+    // ---- 4. the second tile goes into the slot the staging used ----
+    const int n_tiles = (t_end - t_begin + kTK - 1) / kTK;
+    const int my_tiles = wave < n_tiles ? (n_tiles - wave + kWaves - 1) / kWaves : 0;
+    if (k_first + kTK * kWaves < load_end) {
+        wait_lds();   // the reads of the staging area are done
+        fetch(tb1, k_first + kTK * kWaves);
+    }
+    (void)seq;
 
     v4f o[CT][NT];
 #pragma unroll
@@ -377,8 +403,7 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
         m_run[nt] = -INFINITY;
         l_run[nt] = 0.0f;
     }
-    const float scale = a.scale;
-    const int pr_new = owns_new ? pos_new : -1;
+    const int pr_new = wave_new ? pos_new : -1;
 
     // One staged tile with keys [k0, k0 + 32) in tb.
     auto process = [&](const unsigned char *tb, int k0) {
@@ -415,14 +440,10 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
             float s[8];
-            {
-#pragma clang fp contract(off)
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const float x = (float)acc[i >> 2][nt][i & 3] * (qdl[nt] * kd[i]);
-                    const float sc = head_block_sum<NB>(x) * scale;
-                    s[i] = valid[i] ? sc * kLog2e : -INFINITY;
-                }
+            for (int i = 0; i < 8; i++) {
+                const float sc = head_block_sum<NB>((float)acc[i >> 2][nt][i & 3] * (qdl[nt] * kd[i]));
+                s[i] = valid[i] ? sc : -INFINITY;
             }
             float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
             mx = xrow_max(mx);
@@ -479,8 +500,6 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
     };
 
     // ---- the key loop: process a slot, refill it eight tiles on ----
-    const int n_tiles = (t_end - t_begin + kTK - 1) / kTK;
-    const int my_tiles = wave < n_tiles ? (n_tiles - wave + kWaves - 1) / kWaves : 0;
     // Before tile j is read, its copies are done: the copies of tile j+1 (if it
     // is one of ours, already issued after tile j's) may stay in flight.
     auto wait_tile = [&](int j) {
@@ -496,7 +515,10 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
             patch(tb0, k0);
             process(tb0, k0);
             const int kn = k0 + 2 * kTK * kWaves;
-            if (kn < load_end) fetch(tb0, kn);
+            if (kn < load_end) {
+                wait_lds();   // every read of the slot has completed
+                fetch(tb0, kn);
+            }
         }
         if (it + 1 < my_tiles) {
             const int k0 = t_begin + kTK * (wave + kWaves * (it + 1));
@@ -504,7 +526,10 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
             patch(tb1, k0);
             process(tb1, k0);
             const int kn = k0 + 2 * kTK * kWaves;
-            if (kn < load_end) fetch(tb1, kn);
+            if (kn < load_end) {
+                wait_lds();
+                fetch(tb1, kn);
+            }
         }
     }
 

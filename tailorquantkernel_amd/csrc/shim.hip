@@ -112,7 +112,7 @@ int decode3_split_cap() {
     static int v = [] {
         const char *s = getenv("TQ_HIP_DECODE_SPLIT_CAP");
         const int x = s ? atoi(s) : 0;
-        return x > 0 ? x : 1024;
+        return x > 0 ? x : 4096;
     }();
     return v;
 }
