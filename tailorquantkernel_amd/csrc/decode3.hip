@@ -52,7 +52,6 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
-constexpr int kWaves = 4;
 constexpr int kTK = 32;                  // keys per tile
 constexpr int kMaxSplits3 = 64;
 constexpr int kMaxSplitPages3 = 512;     // page ids a work-group stages (8,192 tokens)
@@ -60,6 +59,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;            // log2 headroom before the running max moves
 constexpr int kCoherent = 16;            // cache policy sc1: agent-coherent access
 constexpr int kBufWord3 = 0x00020000;    // raw buffer descriptor, 32-bit data
+constexpr int kCounterStride = TQ_DECODE_COUNTER_STRIDE;   // ints: one 256-byte line per counter
 
 template <int HD, int G>
 struct L3 {
@@ -72,15 +72,13 @@ struct L3 {
     static constexpr int NCH = TILE / 16;               // 16-byte chunks per tile
     static constexpr int CPL = (NCH + 63) / 64;         // chunk loads per lane
     static constexpr int PAGE_CH = kPage * ROW / 16;    // chunks of one page's K (or V) run
-    static constexpr int QE = (G * HD + kThreads - 1) / kThreads;
-    static constexpr int NE = (2 * HD + kThreads - 1) / kThreads;
     static constexpr int U = G * HD / 4;                // float4 units of a head group's output
     static constexpr int PSTRIDE = (G * (HD + 2) + 3) / 4 * 4;   // floats per partial row
-    static constexpr int MERGE = kWaves * G * (HD + 2) * 4;
+    static constexpr int MERGE = G * (HD + 2) * 4;      // one wave's share of the merge
     static_assert(NB == 1 || NB == 2 || NB == 4, "a head's blocks share one DPP quad");
     static_assert(16 % NB == 0, "column tiles hold whole heads");
     static_assert(kTK * ROW % 16 == 0 && kPage * ROW % 16 == 0, "16-byte chunks");
-    static_assert(MERGE <= kWaves * TILE, "the merge reuses the tile slots");
+    static_assert(MERGE <= TILE, "the merge reuses the tile slots");
     static_assert(U % 1 == 0 && HD % 4 == 0, "float4 units");
 };
 
@@ -177,9 +175,12 @@ __device__ __forceinline__ void wait_copies() {
 // memory those accesses touch).
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); }
 
-template <int HD, int G>
-__global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
+// W waves per work-group (4, or 8 when each wave has only a tile or two).
+template <int HD, int G, int W>
+__global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
     using L = L3<HD, G>;
+    constexpr int kWaves = W;
+    constexpr int kThreads = 64 * W;
     constexpr int NB = L::NB, ROW = L::ROW, NT = L::NT, CT = L::CT, CPL = L::CPL;
     __shared__ __align__(16) Smem3<HD, G> sm;
     // two tile slots per wave, separate objects so the wait for one slot's
@@ -536,9 +537,9 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
     // ---- merge the four waves in wave order ----
     __builtin_amdgcn_s_waitcnt(0);   // no copy into a slot is still in flight
     __syncthreads();                 // every wave is done with its slots
-    float *mw = reinterpret_cast<float *>(&slot0[0][0]);     // [4][G]
-    float *lw = mw + kWaves * G;                               // [4][G]
-    float *ow = lw + kWaves * G;                               // [4][G][HD]
+    float *mw = reinterpret_cast<float *>(&slot0[0][0]);     // [W][G]
+    float *lw = mw + kWaves * G;                               // [W][G]
+    float *ow = lw + kWaves * G;                               // [W][G][HD]
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int h = (16 * nt + l16) / NB;
@@ -595,7 +596,9 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
 
     // ---- the last work-group of this (query, kv head) to arrive combines ----
     const int nvalid = (len + a.split_tokens - 1) / a.split_tokens;
-    int *counter = a.counters + (size_t)qi * a.n_kv_heads + kvh;
+    // one counter per (query, kv head), each on its own line: the splits of
+    // one head serialize on it, other heads do not add to that
+    int *counter = a.counters + ((size_t)qi * a.n_kv_heads + kvh) * kCounterStride;
     if (tid == 0)
         sm.last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nvalid - 1;
     __syncthreads();
@@ -673,22 +676,25 @@ __global__ __launch_bounds__(kThreads) void decode3_kernel(TqDecodeArgs a) {
 }
 
 template <int HD, int G>
-hipError_t launch3_hd_g(const TqDecodeArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL((decode3_kernel<HD, G>), dim3(a.n_splits, a.n_kv_heads, a.n_q), dim3(kThreads), 0, s, a);
+hipError_t launch3_hd_g(const TqDecodeArgs &a, int waves, hipStream_t s) {
+    if (waves == 8)
+        hipLaunchKernelGGL((decode3_kernel<HD, G, 8>), dim3(a.n_splits, a.n_kv_heads, a.n_q), dim3(512), 0, s, a);
+    else
+        hipLaunchKernelGGL((decode3_kernel<HD, G, 4>), dim3(a.n_splits, a.n_kv_heads, a.n_q), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
 template <int HD>
-hipError_t launch3_hd(const TqDecodeArgs &a, int g, hipStream_t s) {
+hipError_t launch3_hd(const TqDecodeArgs &a, int g, int waves, hipStream_t s) {
     switch (g) {
-        case 1: return launch3_hd_g<HD, 1>(a, s);
-        case 2: return launch3_hd_g<HD, 2>(a, s);
-        case 3: return launch3_hd_g<HD, 3>(a, s);
-        case 4: return launch3_hd_g<HD, 4>(a, s);
-        case 5: return launch3_hd_g<HD, 5>(a, s);
-        case 6: return launch3_hd_g<HD, 6>(a, s);
-        case 7: return launch3_hd_g<HD, 7>(a, s);
-        case 8: return launch3_hd_g<HD, 8>(a, s);
+        case 1: return launch3_hd_g<HD, 1>(a, waves, s);
+        case 2: return launch3_hd_g<HD, 2>(a, waves, s);
+        case 3: return launch3_hd_g<HD, 3>(a, waves, s);
+        case 4: return launch3_hd_g<HD, 4>(a, waves, s);
+        case 5: return launch3_hd_g<HD, 5>(a, waves, s);
+        case 6: return launch3_hd_g<HD, 6>(a, waves, s);
+        case 7: return launch3_hd_g<HD, 7>(a, waves, s);
+        case 8: return launch3_hd_g<HD, 8>(a, waves, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -704,8 +710,9 @@ int tq_decode3_max_splits() { return kMaxSplits3; }
 int tq_decode3_max_split_tokens() { return kMaxSplitPages3 * kPage; }
 int tq_decode3_partial_floats(int head_dim, int group) { return (group * (head_dim + 2) + 3) / 4 * 4; }
 
-hipError_t tq_launch_decode3(const TqDecodeArgs &a, hipStream_t s) {
+hipError_t tq_launch_decode3(const TqDecodeArgs &a, int waves, hipStream_t s) {
     if (a.n_q <= 0) return hipSuccess;
+    if (waves != 4 && waves != 8) return hipErrorInvalidValue;
     if (a.n_splits < 1 || a.n_splits > kMaxSplits3 || a.split_tokens <= 0 || a.split_tokens % kTK != 0 ||
         a.split_tokens > kMaxSplitPages3 * kPage)
         return hipErrorInvalidValue;
@@ -713,9 +720,9 @@ hipError_t tq_launch_decode3(const TqDecodeArgs &a, hipStream_t s) {
     const int g = a.n_q_heads / a.n_kv_heads;
     if (!tq_decode3_supported(a.head_dim, g)) return hipErrorInvalidValue;
     switch (a.head_dim) {
-        case 32: return launch3_hd<32>(a, g, s);
-        case 64: return launch3_hd<64>(a, g, s);
-        case 128: return launch3_hd<128>(a, g, s);
+        case 32: return launch3_hd<32>(a, g, waves, s);
+        case 64: return launch3_hd<64>(a, g, waves, s);
+        case 128: return launch3_hd<128>(a, g, waves, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -117,11 +117,21 @@ int decode3_split_cap() {
     return v;
 }
 
-// MFMA decode: splits are whole units of 128 tokens (four waves x 32 keys).
+// Waves per work-group of the MFMA decode (TQ_HIP_DECODE_WAVES=4|8 forces it).
+int decode3_waves_env() {
+    static int v = [] {
+        const char *s = getenv("TQ_HIP_DECODE_WAVES");
+        const int x = s ? atoi(s) : 0;
+        return (x == 4 || x == 8) ? x : 0;
+    }();
+    return v;
+}
+
+// MFMA decode: splits are whole units of 32*waves tokens (one tile per wave).
 // Aim at decode_wg_target() work-groups, at most decode3_split_cap() tokens per
 // split, and never more splits than the combine takes.
-void plan_splits3(const tq_hip_kv *kv, int n_q, int max_len, int *split_tokens, int *n_splits) {
-    constexpr int unit = 128;
+void plan_splits3(const tq_hip_kv *kv, int n_q, int max_len, int waves, int *split_tokens, int *n_splits) {
+    const int unit = 32 * waves;
     const long units = std::max(1, (max_len + unit - 1) / unit);
     const long pairs = (long)n_q * kv->desc.n_kv_heads;
     const long cap = tq_decode3_max_splits();
@@ -275,8 +285,12 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
         }
     }
     const bool v3 = use_decode3(kv);
+    // eight waves per work-group when the whole call fits in one round of
+    // work-groups at one 32-key tile per wave (latency-bound small batches)
+    int waves = (long)n_q * D.n_kv_heads * ((max_len + 255) / 256) <= 256 ? 8 : 4;
+    if (decode3_waves_env()) waves = decode3_waves_env();
     if (v3)
-        plan_splits3(kv, n_q, max_len, &a.split_tokens, &a.n_splits);
+        plan_splits3(kv, n_q, max_len, waves, &a.split_tokens, &a.n_splits);
     else
         plan_splits(kv, n_q, max_len, &a.split_tokens, &a.n_splits);
     if (a.n_splits > 1) {
@@ -284,12 +298,12 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
         const size_t row = v3 ? (size_t)tq_decode3_partial_floats(D.head_dim, g) : (size_t)g * (D.head_dim + 2);
         const size_t bytes = (size_t)n_q * D.n_kv_heads * a.n_splits * row * sizeof(float);
         int rc = ensure_partials(kv, bytes);
-        if (rc == TQ_HIP_OK) rc = ensure_counters(kv, (size_t)n_q * D.n_kv_heads, s);
+        if (rc == TQ_HIP_OK) rc = ensure_counters(kv, (size_t)n_q * D.n_kv_heads * TQ_DECODE_COUNTER_STRIDE, s);
         if (rc != TQ_HIP_OK) return rc;
         a.partials = kv->partials;
         a.counters = kv->counters;
     }
-    return herr(v3 ? tq_launch_decode3(a, s) : tq_launch_decode(a, s));
+    return herr(v3 ? tq_launch_decode3(a, waves, s) : tq_launch_decode(a, s));
 }
 
 bool seq_ok(const tq_hip_kv *kv, int seq) { return kv && seq >= 0 && seq < kv->desc.max_seqs; }

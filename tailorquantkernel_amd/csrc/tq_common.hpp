@@ -179,6 +179,9 @@ __device__ __forceinline__ unsigned char *head_run_ptr(const PagedView &v, int p
 // ---------------------------------------------------------------------------
 // Launchers (host side, implemented in the .hip files, used by shim.hip).
 
+// Arrival counters of the MFMA decode are TQ_DECODE_COUNTER_STRIDE ints apart.
+#define TQ_DECODE_COUNTER_STRIDE 64
+
 struct TqDecodeArgs {
     tq::PagedView view;
     const int32_t *seq_of;   // [n_q], or null: query i reads seq_const + seq_stride*i
@@ -236,7 +239,9 @@ int tq_decode3_max_splits();
 int tq_decode3_max_split_tokens();
 // Floats per split partial row of the MFMA decode (16-byte aligned rows).
 int tq_decode3_partial_floats(int head_dim, int group);
-hipError_t tq_launch_decode3(const TqDecodeArgs &a, hipStream_t s);
+// waves: 4 or 8 per work-group; split_tokens a multiple of 32*waves keeps the
+// waves' tile counts equal.
+hipError_t tq_launch_decode3(const TqDecodeArgs &a, int waves, hipStream_t s);
 
 struct TqPrefillArgs {
     tq::PagedView view;
