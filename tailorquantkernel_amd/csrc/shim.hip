@@ -27,6 +27,7 @@ struct tq_hip_kv {
     int *counters = nullptr;        // split-K arrival counters, zero between launches
     size_t counters_n = 0;
     unsigned char *stage = nullptr; // device staging for the synchronous calls
+    unsigned char *hstage = nullptr;  // its pinned host mirror: one copy in, one out
     size_t stage_bytes = 0;
     unsigned char *img = nullptr;   // prefill key-tile images, grown on demand
     size_t img_bytes = 0;
@@ -56,6 +57,9 @@ int decode_wg_target() {
     }();
     return v;
 }
+
+// Fewest new tokens for which a prefill call uses the dense kernel.
+constexpr int kPrefillDenseMin = 32;
 
 // The dense MFMA prefill kernel (default) or, with TQ_HIP_PREFILL_DENSE=0,
 // the decode kernel run once per token with causal lengths.
@@ -206,13 +210,19 @@ int ensure_img(tq_hip_kv *kv, size_t bytes) {
 
 int ensure_stage(tq_hip_kv *kv, size_t bytes) {
     if (bytes <= kv->stage_bytes) return TQ_HIP_OK;
-    if (kv->stage) {
-        TQ_TRY(hipStreamSynchronize(kv->stream));
-        TQ_TRY(hipFree(kv->stage));
-        kv->stage = nullptr;
-        kv->stage_bytes = 0;
-    }
+    TQ_TRY(hipStreamSynchronize(kv->stream));
+    if (kv->stage) TQ_TRY(hipFree(kv->stage));
+    if (kv->hstage) TQ_TRY(hipHostFree(kv->hstage));
+    kv->stage = nullptr;
+    kv->hstage = nullptr;
+    kv->stage_bytes = 0;
     if (hipMalloc(&kv->stage, bytes) != hipSuccess) {
+        kv->stage = nullptr;
+        return TQ_HIP_ENOMEM;
+    }
+    if (hipHostMalloc(&kv->hstage, bytes, hipHostMallocDefault) != hipSuccess) {
+        kv->hstage = nullptr;
+        (void)hipFree(kv->stage);
         kv->stage = nullptr;
         return TQ_HIP_ENOMEM;
     }
@@ -220,7 +230,6 @@ int ensure_stage(tq_hip_kv *kv, size_t bytes) {
     return TQ_HIP_OK;
 }
 
-// Bump allocator over the staging buffer (256-byte aligned pieces).
 struct Stage {
     size_t used = 0;
     size_t take(size_t bytes) {
@@ -229,6 +238,22 @@ struct Stage {
         return at;
     }
 };
+
+// The synchronous entry points: host inputs are packed into the pinned mirror,
+// moved to the device staging area in one copy, and the output comes back the
+// same way (pageable copies of a few KB each cost tens of microseconds).
+void pack(tq_hip_kv *kv, size_t off, const void *src, size_t bytes) {
+    if (src) memcpy(kv->hstage + off, src, bytes);
+}
+int copy_in(tq_hip_kv *kv, size_t bytes) {
+    return herr(hipMemcpyAsync(kv->stage, kv->hstage, bytes, hipMemcpyHostToDevice, kv->stream));
+}
+int copy_out_sync(tq_hip_kv *kv, void *dst, size_t off, size_t bytes) {
+    TQ_TRY(hipMemcpyAsync(kv->hstage + off, kv->stage + off, bytes, hipMemcpyDeviceToHost, kv->stream));
+    TQ_TRY(hipStreamSynchronize(kv->stream));
+    memcpy(dst, kv->hstage + off, bytes);
+    return TQ_HIP_OK;
+}
 
 int capacity_of(const tq_hip_kv *kv, int seq);
 
@@ -284,7 +309,10 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
             a.contig_pages = n;
         }
     }
-    const bool v3 = use_decode3(kv);
+    // the MFMA kernel copies its inputs with 16-byte loads
+    const bool aligned = (((uintptr_t)d_q | (uintptr_t)d_cos | (uintptr_t)d_sin | (uintptr_t)d_k | (uintptr_t)d_v) &
+                          15) == 0;
+    const bool v3 = aligned && use_decode3(kv);
     // eight waves per work-group when the whole call fits in one round of
     // work-groups at one 32-key tile per wave (latency-bound small batches)
     int waves = (long)n_q * D.n_kv_heads * ((max_len + 255) / 256) <= 256 ? 8 : 4;
@@ -505,6 +533,7 @@ void tq_hip_kv_destroy(tq_hip_kv *kv) {
     if (kv->partials) (void)hipFree(kv->partials);
     if (kv->counters) (void)hipFree(kv->counters);
     if (kv->stage) (void)hipFree(kv->stage);
+    if (kv->hstage) (void)hipHostFree(kv->hstage);
     if (kv->img) (void)hipFree(kv->img);
     if (kv->stream) (void)hipStreamDestroy(kv->stream);
     delete kv;
@@ -614,12 +643,12 @@ int tq_hip_kv_append(tq_hip_kv *kv, int seq, int pos, const float *k, const floa
     if (rc != TQ_HIP_OK) return rc;
     const hipStream_t s = kv->stream;
     unsigned char *S = kv->stage;
-    TQ_TRY(hipMemcpyAsync(S + ok_, k, kvb, hipMemcpyHostToDevice, s));
-    TQ_TRY(hipMemcpyAsync(S + ov, v, kvb, hipMemcpyHostToDevice, s));
-    if (cos_t) {
-        TQ_TRY(hipMemcpyAsync(S + oc, cos_t, tb, hipMemcpyHostToDevice, s));
-        TQ_TRY(hipMemcpyAsync(S + os, sin_t, tb, hipMemcpyHostToDevice, s));
-    }
+    pack(kv, ok_, k, kvb);
+    pack(kv, ov, v, kvb);
+    pack(kv, oc, cos_t, tb);
+    pack(kv, os, sin_t, tb);
+    rc = copy_in(kv, st.used);
+    if (rc != TQ_HIP_OK) return rc;
     TQ_TRY(tq_launch_append(kv->view, 1, nullptr, nullptr, seq, pos, (const float *)(S + ok_),
                             (const float *)(S + ov), cos_t ? (const float *)(S + oc) : nullptr,
                             cos_t ? (const float *)(S + os) : nullptr, D.head_dim, s));
@@ -656,22 +685,22 @@ int tq_hip_attend(tq_hip_kv *kv, int seq, int pos, const float *q, const float *
     const size_t qb = (size_t)D.n_q_heads * D.head_dim * sizeof(float);
     const size_t tb = (size_t)(D.head_dim / 2) * sizeof(float);
     Stage st;
-    const size_t oq = st.take(qb), oc = st.take(tb), os = st.take(tb), oo = st.take(qb);
+    const size_t oq = st.take(qb), oc = st.take(tb), os = st.take(tb);
+    const size_t in_bytes = st.used, oo = st.take(qb);
     int rc = ensure_stage(kv, st.used);
     if (rc != TQ_HIP_OK) return rc;
     const hipStream_t s = kv->stream;
     unsigned char *S = kv->stage;
-    TQ_TRY(hipMemcpyAsync(S + oq, q, qb, hipMemcpyHostToDevice, s));
-    if (cos_t) {
-        TQ_TRY(hipMemcpyAsync(S + oc, cos_t, tb, hipMemcpyHostToDevice, s));
-        TQ_TRY(hipMemcpyAsync(S + os, sin_t, tb, hipMemcpyHostToDevice, s));
-    }
+    pack(kv, oq, q, qb);
+    pack(kv, oc, cos_t, tb);
+    pack(kv, os, sin_t, tb);
+    rc = copy_in(kv, in_bytes);
+    if (rc != TQ_HIP_OK) return rc;
     rc = decode_common(kv, 1, nullptr, nullptr, 0, seq, 0, pos, pos + 1, (const float *)(S + oq),
                        cos_t ? (const float *)(S + oc) : nullptr, cos_t ? (const float *)(S + os) : nullptr,
                        nullptr, nullptr, (float *)(S + oo), s, seq);
     if (rc != TQ_HIP_OK) return rc;
-    TQ_TRY(hipMemcpyAsync(out, S + oo, qb, hipMemcpyDeviceToHost, s));
-    return herr(hipStreamSynchronize(s));
+    return copy_out_sync(kv, out, oo, qb);
 }
 
 // ---- prefill ---------------------------------------------------------------------
@@ -684,10 +713,18 @@ int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d
     // model/attention_layer.c:203-204
     if (n <= 0 || pos0 < 0 || pos0 + n > capacity_of(kv, seq)) return TQ_HIP_EINVAL;
     const hipStream_t s = pick(kv, stream);
+    const tq_hip_kv_desc &D = kv->desc;
+    // one token: store_kv + attend as the decode step, one launch
+    // (model/attention_layer.c:221-236 with n == 1)
+    if (n == 1)
+        return decode_common(kv, 1, nullptr, nullptr, 0, seq, 0, pos0, pos0 + 1, d_q, d_cos, d_sin, d_k, d_v,
+                             d_out, s, seq);
     TQ_TRY(tq_launch_append(kv->view, n, nullptr, nullptr, seq, pos0, d_k, d_v, d_cos, d_sin,
                             kv->desc.head_dim, s));
-    const tq_hip_kv_desc &D = kv->desc;
-    if (prefill_dense() && tq_prefill_mfma_supported(D.head_dim, D.n_q_heads / D.n_kv_heads, pos0 + n)) {
+    // the dense kernel restages every key tile of [0, pos0+n): worth it from a
+    // few dozen new tokens on; shorter batches attend in the decode form
+    if (prefill_dense() && n >= kPrefillDenseMin &&
+        tq_prefill_mfma_supported(D.head_dim, D.n_q_heads / D.n_kv_heads, pos0 + n)) {
         TqPrefillArgs t;
         t.view = kv->view;
         t.seq = seq;
@@ -724,25 +761,24 @@ int tq_hip_prefill(tq_hip_kv *kv, int seq, int pos0, int n, const float *q, cons
     const size_t kvb = (size_t)n * D.n_kv_heads * D.head_dim * sizeof(float);
     const size_t tb = (size_t)n * (D.head_dim / 2) * sizeof(float);
     Stage st;
-    const size_t oq = st.take(qb), ok_ = st.take(kvb), ov = st.take(kvb), oc = st.take(tb), os = st.take(tb),
-                 oo = st.take(qb);
+    const size_t oq = st.take(qb), ok_ = st.take(kvb), ov = st.take(kvb), oc = st.take(tb), os = st.take(tb);
+    const size_t in_bytes = st.used, oo = st.take(qb);
     int rc = ensure_stage(kv, st.used);
     if (rc != TQ_HIP_OK) return rc;
     const hipStream_t s = kv->stream;
     unsigned char *S = kv->stage;
-    TQ_TRY(hipMemcpyAsync(S + oq, q, qb, hipMemcpyHostToDevice, s));
-    TQ_TRY(hipMemcpyAsync(S + ok_, k, kvb, hipMemcpyHostToDevice, s));
-    TQ_TRY(hipMemcpyAsync(S + ov, v, kvb, hipMemcpyHostToDevice, s));
-    if (cos_t) {
-        TQ_TRY(hipMemcpyAsync(S + oc, cos_t, tb, hipMemcpyHostToDevice, s));
-        TQ_TRY(hipMemcpyAsync(S + os, sin_t, tb, hipMemcpyHostToDevice, s));
-    }
+    pack(kv, oq, q, qb);
+    pack(kv, ok_, k, kvb);
+    pack(kv, ov, v, kvb);
+    pack(kv, oc, cos_t, tb);
+    pack(kv, os, sin_t, tb);
+    rc = copy_in(kv, in_bytes);
+    if (rc != TQ_HIP_OK) return rc;
     rc = tq_hip_prefill_async(kv, seq, pos0, n, (const float *)(S + oq), (const float *)(S + ok_),
                               (const float *)(S + ov), cos_t ? (const float *)(S + oc) : nullptr,
                               cos_t ? (const float *)(S + os) : nullptr, (float *)(S + oo), s);
     if (rc != TQ_HIP_OK) return rc;
-    TQ_TRY(hipMemcpyAsync(out, S + oo, qb, hipMemcpyDeviceToHost, s));
-    return herr(hipStreamSynchronize(s));
+    return copy_out_sync(kv, out, oo, qb);
 }
 
 }  // extern "C"

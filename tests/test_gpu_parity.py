@@ -468,7 +468,9 @@ PREFILL_SHAPES = [
     # nq, nkv, hd, T, theta, pos0, n — dense MFMA kernel: hd 64/128, g 1/2/4/8
     (8, 2, 64, 300, 1e4, 0, 300), (32, 8, 128, 1100, 5e5, 37, 1000), (4, 4, 64, 200, 1e4, 0, 200),
     (16, 8, 128, 300, 5e5, 0, 257), (64, 8, 128, 400, 1e6, 16, 333), (8, 2, 64, 1200, 1e4, 0, 1100),
-    (2, 1, 128, 40, 1e4, 0, 1), (8, 2, 64, 90, 1e4, 70, 17),
+    (8, 2, 64, 120, 1e4, 70, 40), (2, 1, 128, 80, 1e4, 0, 33),
+    # one token: the fused decode step; fewer than 32: the decode form
+    (2, 1, 128, 40, 1e4, 0, 1), (8, 2, 64, 90, 1e4, 70, 17), (32, 8, 128, 300, 5e5, 255, 1),
     # shapes the dense kernel does not cover run the decode form per token
     (6, 3, 32, 80, 1e6, 5, 70), (8, 2, 256, 100, 1e4, 3, 90), (12, 4, 128, 120, 1e4, 0, 100)]
 
