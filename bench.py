@@ -1,6 +1,6 @@
 """Q8 GQA decode benchmark on one MI355X.
 
-Workload (default, --config c2): Llama-3-8B-shaped attention, 32 q heads / 8 kv
+Workload (default, --config decode-8b-4k): Llama-3-8B-shaped attention, 32 q heads / 8 kv
 heads / head_dim 128, batch 1, context 4096.  One step = the attention core of
 one layer for one new token: RoPE (theta 5e5) on q and k, quantize and append
 the token's K/V into that layer's paged HBM cache, and attend over all 4096
@@ -19,9 +19,10 @@ The CPU baseline leg (default on; --no-cpu skips it) times the reference's
 own kernels (oracle/_ref, AVX2 dispatch, OpenMP over kv heads) on host copies
 of the same workload and checks the GPU output of layer 0 against them.
 
-Other workloads: --config c3 (64 sequences, ragged 512..8192, paged),
-c5 (64q/8kv, batch 16, context 32768, 1 % outliers), c4 (causal prefill of
-2048 tokens).  They print the same JSON fields for their own shape.
+Other workloads: --config decode-batched (64 sequences, ragged 512..8192,
+paged), decode-70b-32k (64q/8kv, batch 16, context 32768, 1 % outliers),
+prefill-2k (causal prefill of 2048 tokens).  They print the same JSON fields
+for their own shape.
 
 --copy-calibration BYTES runs one device-to-device copy of BYTES first: its
 FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc give the counters' scale.
@@ -191,7 +192,7 @@ def measured_traffic(name: str):
 # over kv heads from 256 tokens on, as the reference runs them — and the
 # check of the GPU's layer-0 output against the same code.
 
-def cpu_leg_c2(nq, nkv, hd, T, theta, budget_s: float, check):
+def cpu_leg_decode_8b(nq, nkv, hd, T, theta, budget_s: float, check):
     from oracle.binding import Oracle, Ref, ptr
     oracle = Oracle()
     kind = "reference" if Ref.available() else "port"
@@ -278,9 +279,9 @@ def host_boundary_us(nq, nkv, hd, T, theta, q, k, v, calls=200):
 
 
 # ---------------------------------------------------------------------------
-# C2: batch-1 decode at the 8B shape
+# batch-1 decode at the 8B shape, context 4096
 
-def bench_c2(args, nat, hip):
+def bench_decode_8b(args, nat, hip):
     nq, nkv, hd, T, theta = 32, 8, 128, 4096, 500000.0
     nb = hd // QK
     layers = args.layers
@@ -333,7 +334,7 @@ def bench_c2(args, nat, hip):
     # one kernel launch per step, so the step time over the timed region is
     # the kernel's average launch duration (including back-to-back gaps)
     achieved = kv_bytes / (ms_per_step * 1e-3) / 1e9
-    traffic = measured_traffic("decode_c2_pmc.txt")
+    traffic = measured_traffic("decode_8b_ctx4096_b1_pmc.txt")
     boundary_us = host_boundary_us(nq, nkv, hd, T, theta, q, k, v)
 
     line = {
@@ -361,7 +362,7 @@ def bench_c2(args, nat, hip):
         "host_boundary_us_per_call": boundary_us,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "decode_kernel<128, 4> (fused RoPE + append + split-K attend + combine)",
+                     "kernel": "decode3_kernel<128, 4, 8> (fused RoPE + append + split-K attend + combine)",
                      "kernel_ms": ms_per_step, "algorithmic_bytes": kv_bytes},
     }
     check = (kc0.reshape(-1), vc0.reshape(-1), q, k, v, got)
@@ -369,7 +370,7 @@ def bench_c2(args, nat, hip):
 
 
 # ---------------------------------------------------------------------------
-# batched / long-context decode (C3, C5)
+# batched / long-context decode
 
 def bench_batched(args, nat, hip, *, nq, nkv, hd, lens, theta, outliers, workload, metric, profile):
     lib = nat.load()
@@ -436,32 +437,32 @@ def bench_batched(args, nat, hip, *, nq, nkv, hd, lens, theta, outliers, workloa
         "kv_gbps": gbs, "wall_s": wall, "repeat_equals_first": repeat_same,
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": gbs / HBM_PEAK_GBS, "traffic": measured_traffic(profile),
-                     "kernel": f"decode_kernel<{hd}, {nq // nkv}>", "kernel_ms": ms, "algorithmic_bytes": kv_bytes},
+                     "kernel": f"decode3_kernel<{hd}, {nq // nkv}, 4>", "kernel_ms": ms, "algorithmic_bytes": kv_bytes},
     }
 
 
-def bench_c3(args, nat, hip):
+def bench_decode_batched(args, nat, hip):
     lens = np.random.default_rng(2024).integers(512, 8193, size=64).astype(np.int32)
     return bench_batched(args, nat, hip, nq=32, nkv=8, hd=128, lens=lens, theta=500000.0, outliers=0.0,
                          workload="Q8 GQA batched decode, 64 sequences, context U[512,8192] (seeded), 16-token "
                                   "pages scattered over the pool, 32q/8kv/hd128, fused RoPE + append + attend",
                          metric="Q8 GQA batched decode tokens/sec + achieved HBM GB/s (KV bytes), 1 GPU",
-                         profile="decode_c3_pmc.txt")
+                         profile="decode_8b_batch64_ragged_pmc.txt")
 
 
-def bench_c5(args, nat, hip):
+def bench_decode_70b(args, nat, hip):
     lens = np.full(16, 32768, np.int32)
     return bench_batched(args, nat, hip, nq=64, nkv=8, hd=128, lens=lens, theta=500000.0, outliers=0.01,
                          workload="Q8 GQA long-context decode, 64q/8kv/hd128 (70B layer), batch 16, context 32768, "
                                   "1% K/V outliers at +-8 sigma, split-K, fused RoPE + append + attend",
                          metric="Q8 GQA long-context decode tokens/sec + achieved HBM GB/s (KV bytes), 1 GPU",
-                         profile="decode_c5_pmc.txt")
+                         profile="decode_70b_ctx32768_b16_pmc.txt")
 
 
 # ---------------------------------------------------------------------------
-# C4: causal prefill
+# causal prefill, 2048 tokens
 
-def bench_c4(args, nat, hip):
+def bench_prefill_2k(args, nat, hip):
     lib = nat.load()
     nq, nkv, hd, n, theta = 32, 8, 128, 2048, 500000.0
     kv = nat.PagedKV.single(nq, nkv, hd, n)
@@ -496,7 +497,7 @@ def bench_c4(args, nat, hip):
                                "causal attention", "tokens": n, "useful_ops": useful_ops},
         "repeat_equals_first": repeat_same,
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": 5000.0, "unit": "TFLOP/s",
-                     "frac": tflops / 5000.0, "traffic": measured_traffic("prefill_c4_pmc.txt"),
+                     "frac": tflops / 5000.0, "traffic": measured_traffic("prefill_8b_2048_pmc.txt"),
                      "kernel": "append_kernel + prefill_stage_kernel<128> + prefill_kernel<128, 4, 2> (one step)",
                      "kernel_ms": ms},
     }
@@ -507,7 +508,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3200)
     ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="decode-8b-4k",
+                    choices=["decode-8b-4k", "decode-batched", "prefill-2k", "decode-70b-32k"])
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
@@ -523,14 +525,15 @@ def main():
     hip = Hip()
     if args.copy_calibration > 0:
         copy_calibration(nat, hip, args.copy_calibration)
-    if args.config == "c2":
-        line, check = bench_c2(args, nat, hip)
+    if args.config == "decode-8b-4k":
+        line, check = bench_decode_8b(args, nat, hip)
         if not args.no_cpu:
-            baseline, parity = cpu_leg_c2(32, 8, 128, 4096, 500000.0, args.cpu_budget, check)
+            baseline, parity = cpu_leg_decode_8b(32, 8, 128, 4096, 500000.0, args.cpu_budget, check)
             line["cpu_baseline"] = baseline
             line["parity"] = parity
     else:
-        line = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.config](args, nat, hip)
+        line = {"decode-batched": bench_decode_batched, "prefill-2k": bench_prefill_2k,
+                "decode-70b-32k": bench_decode_70b}[args.config](args, nat, hip)
     print(json.dumps(line), flush=True)
 
 
