@@ -9,45 +9,67 @@
 //
 // prefill_stage_kernel — once per (key tile of 32, kv head) over [0, kend):
 //   reads the tile's K and V rows from the paged cache and writes one
-//   contiguous tile image laid out as the MFMA operands want it:
-//     K codes  [2 key tiles][block][lane][8 bytes]  (A of the i8 product)
-//     K scales [block][key]
-//     V' hi|lo [column tile][lane][8 bf16]          (A of the bf16 product)
-//   with V' = code * vd rounded once to fp32 and split into bf16 hi + lo.
-//   Every query block then streams these images instead of re-deriving them.
+//   contiguous tile image laid out as the MFMA operands want them:
+//     K' hi|lo [key half][block][lane][8 bf16]   (A of the score product)
+//     V' hi|lo [column tile][lane][8 bf16]        (A of the P.V product)
+//   with K' = code * kd and V' = code * vd rounded once to fp32 and split into
+//   bf16 hi + lo (hi + lo = x to 2^-18 relative).  Every query block then
+//   streams these images instead of re-deriving them.
 //
 // prefill_kernel — work-group of 256 threads (4 waves), one kv head, 64*NJ
 //   (query, head) rows = QB = 64*NJ/G consecutive query tokens x the G heads
 //   of the group, in row tiles of 16 queries of one head; wave w owns NJ row
-//   tiles.  Key tiles stream through two LDS buffers (16-byte loads into
-//   registers one tile ahead), one barrier per tile:
-//     S^T = K . Q^T per 32-element block on v_mfma_i32_16x16x32_i8 — exact
-//       int32 block dots, as attn_scores_q8 forms them (model/attn_q8.c:24-30)
-//       — scaled by qd*kd per block in fp32 (FMA: scores match within
-//       rounding, not bit for bit);
-//     online softmax per query (exp2 domain), causal mask;
-//     O^T += V'^T . P^T on v_mfma_f32_16x16x32_bf16, P split into bf16 hi + lo
-//       like V': hi.hi + hi.lo + lo.hi carries ~16 significant bits per
-//       product, fp32 accumulation.
+//   tiles.  q is quantized exactly as quantize_row_q8 does, then q' = code *
+//   qd * scale * log2(e) is split into bf16 hi + lo, held in registers.
+//   Key tiles are copied straight into two LDS buffers (global_load_lds), one
+//   tile ahead, one barrier per tile:
+//     S^T = K'.q'^T on v_mfma_f32_16x16x32_bf16 per 32-value block, three
+//       products (hi.hi + hi.lo + lo.hi): the dequantized dot of
+//       attn_scores_q8 (model/attn_q8.c:24-30) to ~2^-17 relative per term,
+//       in the exp2 domain, replacing a per-block int32 -> fp32 rescale on
+//       the VALU;
+//     online softmax per query with a causal mask; the running max moves only
+//       when a tile exceeds it by more than 2^8;
+//     O^T += V'^T . P^T on the same bf16 product, P split into hi + lo.
 //   The S^T orientation leaves each lane with 8 keys of one query: exactly a
 //   B operand of the P.V product (keys permuted identically in A and B), so P
-//   never goes through LDS.  Grid x runs the heaviest (latest) query blocks
-//   first.
+//   never goes through LDS.
+//
+// Balance: under the causal mask the last query block reads every key tile
+// and the first reads one.  Query blocks are paired last with first (p with
+// nb-1-p), so every pair reads about the same number of tiles; a pair's tile
+// sequence (the later block's tiles, then the earlier block's) is cut into nsp
+// equal chunks, one work item each, so all items carry the same work.  An item
+// runs one or two segments (a block and a tile range).  A block covered by
+// several segments gets a partial (o, m, l per row) from each, written with
+// agent-coherent 16-byte stores; an arrival counter picks the last segment to
+// finish, which merges them in segment order, so the result does not depend
+// on which work-group finished last.
+//
+// Grid: one dimension, work-group w serves kv head w % n_kv, so with 8 kv
+// heads each XCD (work-groups go round-robin over the 8 XCDs) works on one
+// head and keeps that head's tile image in its own L2.
+#include <algorithm>
+
 #include "tq_common.hpp"
 
 namespace {
 
 using namespace tq;
 
-typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kKT = 32;                  // keys per tile
 constexpr int kMaxPrefillKeys = 65536;   // keys [0, kend) the dense path serves
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazy = 8.0f;            // log2 headroom before the running max moves
+constexpr int kMaxSplitsP = 8;           // chunks of one query-block pair
+constexpr int kItemOverheadTiles = 3;    // prologue + merge of a work item, in tile times
+constexpr int kCounterStrideP = 64;      // ints: one 256-byte line per counter
+constexpr int kCoherentP = 16;           // cache policy sc1: agent-coherent access
+constexpr int kResidentWGs = 512;        // work-groups resident at once (2 per CU)
 
 // Layout of one tile image (bytes), shared by both kernels.
 template <int HD>
@@ -55,13 +77,13 @@ struct TileImg {
     static constexpr int NB = HD / kQK;
     static constexpr int MT = HD / 16;
     static constexpr int ROW = NB * kBlockBytes;
-    static constexpr int KC_OFF = 0;
-    static constexpr int KD_OFF = KC_OFF + 2 * NB * 64 * 8;
-    static constexpr int VH_OFF = KD_OFF + NB * kKT * 4;
+    static constexpr int KH_OFF = 0;                       // [2][NB][64] x 16 B
+    static constexpr int KL_OFF = KH_OFF + 2 * NB * 64 * 16;
+    static constexpr int VH_OFF = KL_OFF + 2 * NB * 64 * 16;   // [MT][64] x 16 B
     static constexpr int VL_OFF = VH_OFF + MT * 64 * 16;
     static constexpr int BYTES = VL_OFF + MT * 64 * 16;
     static constexpr int CHUNKS = BYTES / 16;
-    static_assert(BYTES % 16 == 0, "16-byte chunks");
+    static_assert(BYTES % 4096 == 0, "whole rounds of 16-byte copies by 256 threads");
 };
 
 // Key slot i (0..7) of lane group g in the MFMA k order used for P.V:
@@ -72,20 +94,49 @@ __device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
     v2bf v = {(__bf16)a, (__bf16)b};
     return __builtin_bit_cast(uint32_t, v);
 }
-// fp32 values of the two bf16 halves of a pair (exact).
-__device__ __forceinline__ float bf16_lo_f(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf16_hi_f(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 // bf16 hi | lo parts of four pairs of values.
 __device__ __forceinline__ void split_bf16(const float (&x)[8], u32x4 &hi, u32x4 &lo) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const uint32_t h = bf16_pair(x[2 * i], x[2 * i + 1]);
         hi[i] = h;
-        lo[i] = bf16_pair(x[2 * i] - bf16_lo_f(h), x[2 * i + 1] - bf16_hi_f(h));
+        lo[i] = bf16_pair(x[2 * i] - __uint_as_float(h << 16), x[2 * i + 1] - __uint_as_float(h & 0xFFFF0000u));
     }
 }
 
 __device__ __forceinline__ v8bf as_v8bf(u32x4 w) { return __builtin_bit_cast(v8bf, w); }
+
+// Max / sum over lanes l, l^16, l^32, l^48 (the four 16-lane rows), the same
+// value in all four: permlane32_swap pairs rows (0,2) and (1,3),
+// permlane16_swap rows (0,1) and (2,3); VALU only, lower row first in adds.
+__device__ __forceinline__ float xrow_max(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float xrow_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float m = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+
+// 16 bytes from each lane's global address into LDS at dst + 16*lane
+// (global_load_lds_dwordx4, M0 = LDS byte address, restored after).  Inline
+// assembly keeps the compiler from following the copy with a full vmcnt(0)
+// wait before every LDS access; the kernel waits for its copies itself.
+__device__ __forceinline__ void dma16(const void *src, unsigned char *dst) {
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_u8 *)dst;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(lds));
+}
 
 struct StageArgs {
     PagedView view;
@@ -134,20 +185,19 @@ __global__ __launch_bounds__(kThreads) void prefill_stage_kernel(StageArgs a) {
     __syncthreads();
     const unsigned char *rk = reinterpret_cast<const unsigned char *>(raw[0]);
     const unsigned char *rv = reinterpret_cast<const unsigned char *>(raw[1]);
-    unsigned char *out = a.img + ((size_t)kvh * a.n_tiles + kt) * I::BYTES;
-    // K codes: entry (mt, b, lane) = key mt*16 + lane%16, block b, bytes 8*(lane/16)..
+    unsigned char *out = a.img + ((size_t)a.n_tiles * kvh + kt) * I::BYTES;
+    // K': entry (mt, b, lane) = key mt*16 + lane%16, block b, values 8*(lane/16)..+7
     for (int e = tid; e < 2 * I::NB * 64; e += kThreads) {
         const int mt = e / (I::NB * 64), b = (e / 64) % I::NB, ln = e % 64;
-        const int off = (mt * 16 + (ln & 15)) * ROW + b * kBlockBytes + 4 + 8 * (ln >> 4);
-        const u32x2 c = {*reinterpret_cast<const uint32_t *>(rk + off),
-                         *reinterpret_cast<const uint32_t *>(rk + off + 4)};
-        *reinterpret_cast<u32x2 *>(out + I::KC_OFF + e * 8) = c;
-    }
-    // K scales [block][key]
-    for (int e = tid; e < I::NB * kKT; e += kThreads) {
-        const int b = e / kKT, key = e % kKT;
-        *reinterpret_cast<float *>(out + I::KD_OFF + e * 4) =
-            *reinterpret_cast<const float *>(rk + key * ROW + b * kBlockBytes);
+        const unsigned char *row = rk + (mt * 16 + (ln & 15)) * ROW + b * kBlockBytes;
+        const float d = *reinterpret_cast<const float *>(row);
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) x[i] = (float)(int8_t)row[4 + 8 * (ln >> 4) + i] * d;
+        u32x4 hi, lo;
+        split_bf16(x, hi, lo);
+        *reinterpret_cast<u32x4 *>(out + I::KH_OFF + e * 16) = hi;
+        *reinterpret_cast<u32x4 *>(out + I::KL_OFF + e * 16) = lo;
     }
     // V' = code * vd: entry (m, lane) = column m*16 + lane%16, keys perm_key(lane/16, 0..7)
     for (int e = tid; e < I::MT * 64; e += kThreads) {
@@ -176,15 +226,21 @@ struct PShape {
     static constexpr int QT = QB / 16;             // query tiles per head
     static constexpr int MT = I::MT;               // output column tiles
     static constexpr int QCS = HD + 8;             // LDS stride of a q code row
-    static constexpr int LOADS = (I::CHUNKS + kThreads - 1) / kThreads;
+    static constexpr int ROUNDS = I::CHUNKS / kThreads;   // copies per thread per tile
     static constexpr int Q_BYTES = RW * QCS + RW * NB * 4;
     static_assert(RW % G == 0 && QB % 16 == 0, "whole query tiles");
-    static_assert(Q_BYTES <= 2 * I::BYTES, "q staging fits the tile buffers");
+    static_assert(Q_BYTES <= I::BYTES, "q staging fits one tile buffer");
+    static_assert(ROUNDS < 32, "vmcnt immediate");
 };
 
 struct PrefillArgs {
     int pos0;
     int n;
+    int qblocks;         // query blocks of QB tokens
+    int nsp;             // chunks per block pair = most segments of one block
+    int n_kv;
+    float *partials;     // [n_kv][qblocks][nsp][RW][HD + 4]
+    int *counters;       // [n_kv][qblocks] x kCounterStrideP
     const float *q;      // [n][n_q_heads][hd], pre-RoPE if cos_t
     const float *cos_t;  // [n][hd/2] or null
     const float *sin_t;
@@ -195,59 +251,116 @@ struct PrefillArgs {
     const unsigned char *img;
 };
 
-// Quantize the 32-value block spread over this lane's 32-lane group and
-// store its scale and codes separately (quantize_row_q8, kernel/quant_x.c:12-33).
-__device__ __forceinline__ void quantize_split32(float x, float *d_out, unsigned char *codes) {
-    const int lane = threadIdx.x & 31;
-    const float d = quant_scale(block_amax32(x));
-    const uint32_t word = pack_codes4(quant_code(x, quant_inverse(d)));
-    if (lane == 0) *d_out = d;
-    if ((lane & 3) == 0) *reinterpret_cast<uint32_t *>(codes + lane) = word;
+// Quantize a 32-value block held 4 values per lane over an aligned group of 8
+// lanes (half a DPP row) and store its scale and this lane's 4 codes
+// (quantize_row_q8, kernel/quant_x.c:12-33).  The absmax keeps the strict
+// "val > max" scan's value as block_amax32 does: |x| with NaN and -0 mapped
+// to 0, then an exact max in any order.
+__device__ __forceinline__ void quantize8x4(const float (&x)[4], float *d_out, unsigned char *codes, bool leader) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a = x[i] < 0.0f ? -x[i] : x[i];
+        m = fmaxf(m, a > 0.0f ? a : 0.0f);
+    }
+    m = fmaxf(m, dpp_f<kDppQuadXor1>(m));
+    m = fmaxf(m, dpp_f<kDppQuadXor2>(m));
+    m = fmaxf(m, dpp_f<kDppRowHalfMirror>(m));
+    const float d = quant_scale(m);
+    const float inv = quant_inverse(d);
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) w |= quant_code(x[i], inv) << (8 * i);
+    if (leader) *d_out = d;
+    *reinterpret_cast<uint32_t *>(codes) = w;
 }
 
+// Key tiles query block b reads: keys [0, pos0 + its last query + 1).
+__host__ __device__ inline int block_tiles(int pos0, int n, int qb, int b) {
+    const int last = (b + 1) * qb < n ? (b + 1) * qb : n;
+    return (pos0 + last + kKT - 1) / kKT;
+}
+
+// One segment: query block blk against key tiles [kt_begin, kt_end), the
+// segment sp of the nsp that cover the block.
 template <int HD, int G, int NJ>
-__global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
+__device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, int blk, int kt_begin, int kt_end,
+                                                int sp, int nsp, unsigned char *tile0, unsigned char *tile1) {
     using S = PShape<HD, G, NJ>;
     using I = TileImg<HD>;
     constexpr int NB = S::NB;
-    __shared__ __attribute__((aligned(16))) unsigned char tile[2][I::BYTES];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int l16 = lane & 15;
     const int lg = lane >> 4;
-    const int kvh = blockIdx.y;
-    const int qblocks = (a.n + S::QB - 1) / S::QB;
-    const int i0 = (qblocks - 1 - (int)blockIdx.x) * S::QB;   // heaviest blocks first
-    const int i_end = min(i0 + S::QB, a.n);
-    const int kend = a.pos0 + i_end;                          // keys [0, kend)
-    const int n_tiles = (kend + kKT - 1) / kKT;
+    const int i0 = blk * S::QB;
+    const unsigned char *img = a.img + (size_t)kvh * a.n_tiles * I::BYTES;
 
-    // ---- q rows of this wave: RoPE + quantize_row_q8 into LDS
-    unsigned char *qc = tile[0];
-    float *qd = reinterpret_cast<float *>(tile[0] + S::RW * S::QCS);
-    for (int pass = 0; pass < 8 * NJ * NB; pass++) {
-        const int blk = pass * 2 + (lane >> 5);          // block of the wave's rows
-        const int r = wave * 16 * NJ + blk / NB;         // row: tile r/16, query r%16
-        const int b = blk % NB;
+    // copy of tile kt into an LDS buffer: thread t's copy r is chunk t + 256 r
+    auto fetch = [&](unsigned char *buf, int kt) {
+        const unsigned char *src = img + (size_t)kt * I::BYTES;
+        const int wu = __builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+        for (int r = 0; r < S::ROUNDS; r++)
+            dma16(src + 16 * (tid + kThreads * r), buf + 16 * (kThreads * r + 64 * wu));
+    };
+    // the first tile flies while q is quantized (q staging uses tile1)
+    fetch(tile0, kt_begin);
+
+    // ---- q rows: RoPE + quantize_row_q8 into LDS.  Task (row r, c) covers
+    //      q[4c..4c+3] and its rotate-half partner q[HD/2+4c..+3]; every load
+    //      of the thread's tasks is issued before the first is used
+    constexpr int HALF = HD / 2;
+    constexpr int CPR = HD / 8;                      // tasks per row; 8 | CPR
+    constexpr int TASKS = S::RW * CPR / kThreads;    // per thread
+    static_assert(S::RW * CPR % kThreads == 0, "whole tasks");
+    unsigned char *qc = tile1;
+    float *qd = reinterpret_cast<float *>(tile1 + S::RW * S::QCS);
+    v4f xl[TASKS], xu[TASKS], cs[TASKS], sn[TASKS];
+#pragma unroll
+    for (int t = 0; t < TASKS; t++) {
+        const int k = tid + kThreads * t;
+        const int r = k / CPR, c = k % CPR;
         const int nt = r >> 4;
-        const int g = nt / S::QT;
         const int qi = i0 + (nt % S::QT) * 16 + (r & 15);
-        float x = 0.0f;
+        xl[t] = xu[t] = cs[t] = sn[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
         if (qi < a.n) {
-            const float *head = a.q + ((size_t)qi * a.n_q_heads + (size_t)kvh * G + g) * HD;
-            const float *ct = a.cos_t ? a.cos_t + (size_t)qi * (HD / 2) : nullptr;
-            const float *st = a.sin_t ? a.sin_t + (size_t)qi * (HD / 2) : nullptr;
-            x = rope_elem(head, b * kQK + (lane & 31), HD, ct, st);
+            const float *head = a.q + ((size_t)qi * a.n_q_heads + (size_t)kvh * G + nt / S::QT) * HD;
+            xl[t] = *reinterpret_cast<const v4f *>(head + 4 * c);
+            xu[t] = *reinterpret_cast<const v4f *>(head + HALF + 4 * c);
+            if (a.cos_t) {
+                cs[t] = *reinterpret_cast<const v4f *>(a.cos_t + (size_t)qi * HALF + 4 * c);
+                sn[t] = *reinterpret_cast<const v4f *>(a.sin_t + (size_t)qi * HALF + 4 * c);
+            }
         }
-        quantize_split32(x, qd + r * NB + b, qc + r * S::QCS + b * kQK);
+    }
+#pragma unroll
+    for (int t = 0; t < TASKS; t++) {
+        const int k = tid + kThreads * t;
+        const int r = k / CPR, c = k % CPR;
+        float lo[4], up[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (a.cos_t) {
+                lo[i] = rope_lower(xl[t][i], xu[t][i], cs[t][i], sn[t][i]);
+                up[i] = rope_upper(xl[t][i], xu[t][i], cs[t][i], sn[t][i]);
+            } else {
+                lo[i] = xl[t][i];
+                up[i] = xu[t][i];
+            }
+        }
+        const bool leader = (c & 7) == 0;
+        quantize8x4(lo, qd + r * NB + c / 8, qc + r * S::QCS + 4 * c, leader);
+        quantize8x4(up, qd + r * NB + (HALF + 4 * c) / kQK, qc + r * S::QCS + HALF + 4 * c, leader);
     }
     __syncthreads();
 
-    // ---- per-lane operands of the wave's query tiles
-    long qb[NJ][NB];      // B operand: 8 codes of query l16, block b, k 8*lg..
-    float qdp[NJ][NB];    // its scale * softmax scale * log2(e)
+    // ---- per-lane B operands: q' = code * qd * scale * log2(e) of query l16,
+    //      values 32b + 8lg .. +7, as bf16 hi | lo
+    v8bf qh[NJ][NB], ql[NJ][NB];
     int qpos[NJ];
+    const float qscale = a.scale * kLog2e;
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const int r = (wave * NJ + j) * 16 + l16;
@@ -257,30 +370,17 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
         qpos[j] = a.pos0 + qi;
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            qb[j][b] = *reinterpret_cast<const long *>(qc + r * S::QCS + b * kQK + 8 * lg);
-            qdp[j][b] = qd[r * NB + b] * (a.scale * kLog2e);
+            const float s = qd[r * NB + b] * qscale;
+            const unsigned char *c = qc + r * S::QCS + b * kQK + 8 * lg;
+            float x[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) x[i] = (float)(int8_t)c[i] * s;
+            u32x4 hi, lo;
+            split_bf16(x, hi, lo);
+            qh[j][b] = as_v8bf(hi);
+            ql[j][b] = as_v8bf(lo);
         }
     }
-    __syncthreads();   // the q area is reused by the tile buffers below
-
-    // ---- tile streaming: 16-byte chunks, one tile ahead in registers
-    const unsigned char *img = a.img + (size_t)kvh * a.n_tiles * I::BYTES;
-    u32x4 stg[S::LOADS];
-    auto load_tile = [&](int kt) {
-        const unsigned char *src = img + (size_t)kt * I::BYTES;
-#pragma unroll
-        for (int i = 0; i < S::LOADS; i++) {
-            const int c = tid + kThreads * i;
-            if (c < I::CHUNKS) stg[i] = *reinterpret_cast<const u32x4 *>(src + c * 16);
-        }
-    };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < S::LOADS; i++) {
-            const int c = tid + kThreads * i;
-            if (c < I::CHUNKS) *reinterpret_cast<u32x4 *>(tile[buf] + c * 16) = stg[i];
-        }
-    };
 
     // ---- the key loop
     v4f o[S::MT][NJ];
@@ -295,15 +395,17 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
         lsum[j] = 0.0f;
     }
 
-    load_tile(0);
-    for (int kt = 0; kt < n_tiles; kt++) {
-        const int buf = kt & 1;
-        store_tile(buf);
-        if (kt + 1 < n_tiles) load_tile(kt + 1);
+    for (int kt = kt_begin; kt < kt_end; kt++) {
+        const bool odd = (kt - kt_begin) & 1;
+        unsigned char *T = odd ? tile1 : tile0;
+        // this thread's copies of tile kt have landed; the barrier makes every
+        // thread's visible and frees the other buffer (tile kt-1, or the q
+        // staging) for the next copy
+        asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
         __syncthreads();
-        const unsigned char *T = tile[buf];
+        if (kt + 1 < kt_end) fetch(odd ? tile0 : tile1, kt + 1);
 
-        // S^T = K . Q^T for keys [32kt, 32kt+32) x the wave's queries
+        // S^T = K'.q'^T for keys [32kt, 32kt+32) x the wave's queries
         v4f s[2][NJ];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
@@ -313,13 +415,13 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
         for (int b = 0; b < NB; b++) {
 #pragma unroll
             for (int mt = 0; mt < 2; mt++) {
-                const long ka = *reinterpret_cast<const long *>(T + I::KC_OFF + ((mt * NB + b) * 64 + lane) * 8);
-                const v4f kdv = *reinterpret_cast<const v4f *>(T + I::KD_OFF + (b * kKT + mt * 16 + 4 * lg) * 4);
+                const v8bf kh = as_v8bf(*reinterpret_cast<const u32x4 *>(T + I::KH_OFF + ((mt * NB + b) * 64 + lane) * 16));
+                const v8bf kl = as_v8bf(*reinterpret_cast<const u32x4 *>(T + I::KL_OFF + ((mt * NB + b) * 64 + lane) * 16));
 #pragma unroll
                 for (int j = 0; j < NJ; j++) {
-                    const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(ka, qb[j][b], v4i{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) s[mt][j][r] = fmaf((float)acc[r], qdp[j][b] * kdv[r], s[mt][j][r]);
+                    s[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[j][b], s[mt][j], 0, 0, 0);
+                    s[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[j][b], s[mt][j], 0, 0, 0);
+                    s[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[j][b], s[mt][j], 0, 0, 0);
                 }
             }
         }
@@ -340,10 +442,12 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
             }
             float mx = fmaxf(fmaxf(fmaxf(s[0][j][0], s[0][j][1]), fmaxf(s[0][j][2], s[0][j][3])),
                              fmaxf(fmaxf(s[1][j][0], s[1][j][1]), fmaxf(s[1][j][2], s[1][j][3])));
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mnew = fmaxf(mrow[j], mx);
-            const float corr = __builtin_amdgcn_exp2f(mrow[j] - mnew);
+            mx = xrow_max(mx);
+            const float mnew = mx > mrow[j] + kLazy ? mx : mrow[j];
+            // a split's first tiles can be fully masked for its early rows:
+            // offset by 0 while the max is still -inf (p = 0, no NaN)
+            const float moff = mnew == -INFINITY ? 0.0f : mnew;
+            const float corr = __builtin_amdgcn_exp2f(mrow[j] - moff);
             mrow[j] = mnew;
             float p[8];
             float ps = 0.0f;
@@ -351,7 +455,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
             for (int mt = 0; mt < 2; mt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    p[mt * 4 + r] = __builtin_amdgcn_exp2f(s[mt][j][r] - mnew);
+                    p[mt * 4 + r] = __builtin_amdgcn_exp2f(s[mt][j][r] - moff);
                     ps += p[mt * 4 + r];
                 }
             lsum[j] = lsum[j] * corr + ps;
@@ -377,21 +481,117 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     }
 
     // ---- normalise and store: lane holds columns 16m + 4lg .. +3 of query l16
+    float lrow[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) lrow[j] = xrow_sum(lsum[j]);
+    auto store_out = [&]() {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const float inv = 1.0f / lrow[j];
+            const int nt = wave * NJ + j;
+            const int g = nt / S::QT;
+            const int qi = i0 + (nt % S::QT) * 16 + l16;
+            if (qi < a.n) {
+                float *orow = a.out + ((size_t)qi * a.n_q_heads + (size_t)kvh * G + g) * HD;
+#pragma unroll
+                for (int m = 0; m < S::MT; m++)
+                    *reinterpret_cast<v4f *>(orow + m * 16 + 4 * lg) = o[m][j] * inv;
+            }
+        }
+    };
+    if (nsp == 1) {
+        store_out();
+        return;
+    }
+
+    // ---- split: partial rows [RW][HD + 4] (o unnormalised, m, l) of this split
+    constexpr int PS = HD + 4;
+    const size_t pblock = ((size_t)kvh * a.qblocks + blk) * a.nsp;
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc(a.partials + pblock * S::RW * PS, 0, nsp * S::RW * PS * 4, 0x00020000);
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        float l = lsum[j];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
-        const float inv = 1.0f / l;
-        const int nt = wave * NJ + j;
-        const int g = nt / S::QT;
-        const int qi = i0 + (nt % S::QT) * 16 + l16;
-        if (qi < a.n) {
-            float *orow = a.out + ((size_t)qi * a.n_q_heads + (size_t)kvh * G + g) * HD;
+        const int r = (wave * NJ + j) * 16 + l16;
+        const int base = (sp * S::RW + r) * PS;
 #pragma unroll
-            for (int m = 0; m < S::MT; m++)
-                *reinterpret_cast<v4f *>(orow + m * 16 + 4 * lg) = o[m][j] * inv;
+        for (int m = 0; m < S::MT; m++)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[m][j]), prs,
+                                                   (base + m * 16 + 4 * lg) * 4, 0, kCoherentP);
+        if (lg == 0) {
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(mrow[j]), prs, (base + HD) * 4, 0, kCoherentP);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lrow[j]), prs, (base + HD + 1) * 4, 0, kCoherentP);
         }
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // the partial is at the point of coherence
+    __syncthreads();
+    int *counter = a.counters + ((size_t)kvh * a.qblocks + blk) * kCounterStrideP;
+    int *flag = reinterpret_cast<int *>(tile0);
+    if (tid == 0) *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsp - 1;
+    __syncthreads();
+    if (!*flag) return;
+    if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // ---- the last split merges all of them in split order (its own from registers)
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int r = (wave * NJ + j) * 16 + l16;
+        float M = -INFINITY, L = 0.0f;
+        v4f acc[S::MT];
+#pragma unroll
+        for (int m = 0; m < S::MT; m++) acc[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s2 = 0; s2 < nsp; s2++) {
+            const int base = (s2 * S::RW + r) * PS;
+            float ms, ls;
+            v4f os[S::MT];
+            if (s2 == sp) {
+                ms = mrow[j];
+                ls = lrow[j];
+#pragma unroll
+                for (int m = 0; m < S::MT; m++) os[m] = o[m][j];
+            } else {
+                ms = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, (base + HD) * 4, 0, kCoherentP));
+                ls = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, (base + HD + 1) * 4, 0, kCoherentP));
+#pragma unroll
+                for (int m = 0; m < S::MT; m++)
+                    os[m] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        prs, (base + m * 16 + 4 * lg) * 4, 0, kCoherentP));
+            }
+            const float Mn = fmaxf(M, ms);
+            const float fo = __builtin_amdgcn_exp2f(M - Mn);   // 0 while M is -inf
+            const float fs = __builtin_amdgcn_exp2f(ms - Mn);
+#pragma unroll
+            for (int m = 0; m < S::MT; m++) acc[m] = acc[m] * fo + os[m] * fs;
+            L = L * fo + ls * fs;
+            M = Mn;
+        }
+#pragma unroll
+        for (int m = 0; m < S::MT; m++) o[m][j] = acc[m];
+        lrow[j] = L;
+    }
+    store_out();
+}
+
+template <int HD, int G, int NJ>
+__global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
+    using S = PShape<HD, G, NJ>;
+    using I = TileImg<HD>;
+    __shared__ __attribute__((aligned(16))) unsigned char tile0[I::BYTES];
+    __shared__ __attribute__((aligned(16))) unsigned char tile1[I::BYTES];
+    const int kvh = (int)blockIdx.x % a.n_kv;
+    const int item = (int)blockIdx.x / a.n_kv;
+    const int p = item / a.nsp, c = item % a.nsp;
+    // pair p: the later block bh, then the earlier bl (none for the middle block)
+    const int bh = a.qblocks - 1 - p, bl = p;
+    const int th = block_tiles(a.pos0, a.n, S::QB, bh);
+    const int tp = th + (bl < bh ? block_tiles(a.pos0, a.n, S::QB, bl) : 0);
+    const int C = (tp + a.nsp - 1) / a.nsp;             // tiles per chunk
+    const int c0 = c * C, c1 = min(tp, c0 + C);          // this chunk of the pair's sequence
+    if (c0 < min(c1, th))
+        prefill_segment<HD, G, NJ>(a, kvh, bh, c0, min(c1, th), c, (th + C - 1) / C, tile0, tile1);
+    if (c1 > max(c0, th)) {
+        __syncthreads();   // the LDS buffers are free again
+        prefill_segment<HD, G, NJ>(a, kvh, bl, max(c0, th) - th, c1 - th, c - th / C, (tp + C - 1) / C - th / C,
+                                   tile0, tile1);
     }
 }
 
@@ -406,11 +606,48 @@ int prefill_rows(int g) {
     return forced == 64 ? 64 : 128;
 }
 
+// Query tokens per work-group for a shape (the kernel's QB).
+int prefill_qb(int g) { return 64 * (prefill_rows(g) == 128 ? 2 : 1) / g; }
+
+// Chunk plan: nsp chunks per block pair, the count that minimises the time of
+// the item waves (items of ceil(tp/nsp) tiles each, kItemOverheadTiles extra,
+// resident work-groups at once per wave).
+struct PrefillPlan {
+    int qblocks, nsp, rows, items;
+};
+PrefillPlan plan_prefill(int hd, int g, int n_kv_heads, int pos0, int n) {
+    PrefillPlan p;
+    const int qb = prefill_qb(g);
+    p.rows = 64 * (prefill_rows(g) == 128 ? 2 : 1);
+    p.qblocks = (n + qb - 1) / qb;
+    const int pairs = (p.qblocks + 1) / 2;
+    int tp_max = 0;
+    for (int q = 0; q < pairs; q++) {
+        const int bh = p.qblocks - 1 - q;
+        const int tp = block_tiles(pos0, n, qb, bh) + (q < bh ? block_tiles(pos0, n, qb, q) : 0);
+        tp_max = std::max(tp_max, tp);
+    }
+    const long slots = 256L * (hd == 128 ? 2 : 4);   // resident work-groups: 2 or 4 per CU
+    long best = -1;
+    p.nsp = 1;
+    for (int k = 1; k <= kMaxSplitsP; k++) {
+        const int C = (tp_max + k - 1) / k;
+        if (k > 1 && C < 4) break;
+        const long waves = ((long)pairs * k * n_kv_heads + slots - 1) / slots;
+        const long cost = waves * (C + kItemOverheadTiles);
+        if (best < 0 || cost < best) {
+            best = cost;
+            p.nsp = k;
+        }
+    }
+    p.items = pairs * p.nsp;
+    return p;
+}
+
 template <int HD, int G, int NJ>
 hipError_t launch_hd_g(const PrefillArgs &a, int n_kv_heads, hipStream_t s) {
-    using S = PShape<HD, G, NJ>;
-    const int qblocks = (a.n + S::QB - 1) / S::QB;
-    hipLaunchKernelGGL((prefill_kernel<HD, G, NJ>), dim3(qblocks, n_kv_heads), dim3(kThreads), 0, s, a);
+    const int items = (a.qblocks + 1) / 2 * a.nsp;
+    hipLaunchKernelGGL((prefill_kernel<HD, G, NJ>), dim3(items * n_kv_heads), dim3(kThreads), 0, s, a);
     return hipGetLastError();
 }
 
@@ -445,6 +682,13 @@ bool tq_prefill_mfma_supported(int head_dim, int group, int kend) {
     return hd_ok && g_ok && kend > 0 && kend <= kMaxPrefillKeys;
 }
 
+void tq_prefill_scratch(int head_dim, int group, int n_kv_heads, int pos0, int n, size_t *partial_bytes,
+                        size_t *counter_ints) {
+    const PrefillPlan p = plan_prefill(head_dim, group, n_kv_heads, pos0, n);
+    *partial_bytes = (size_t)n_kv_heads * p.qblocks * p.nsp * p.rows * (head_dim + 4) * sizeof(float);
+    *counter_ints = (size_t)n_kv_heads * p.qblocks * kCounterStrideP;
+}
+
 size_t tq_prefill_image_bytes(int head_dim, int n_kv_heads, int kend) {
     const size_t tiles = (size_t)(kend + kKT - 1) / kKT;
     const size_t per = head_dim == 64 ? TileImg<64>::BYTES : TileImg<128>::BYTES;
@@ -465,5 +709,12 @@ hipError_t tq_launch_prefill(const TqPrefillArgs &t, hipStream_t s) {
     a.scale = t.scale;
     a.n_tiles = (t.pos0 + t.n + kKT - 1) / kKT;
     a.img = t.img;
+    const PrefillPlan p = plan_prefill(t.head_dim, g, t.n_kv_heads, t.pos0, t.n);
+    a.qblocks = p.qblocks;
+    a.nsp = p.nsp;
+    a.n_kv = t.n_kv_heads;
+    a.partials = t.partials;
+    a.counters = t.counters;
+    if (p.nsp > 1 && (!t.partials || !t.counters)) return hipErrorInvalidValue;
     return t.head_dim == 64 ? launch_hd<64>(t, a, g, s) : launch_hd<128>(t, a, g, s);
 }

@@ -31,6 +31,10 @@ struct tq_hip_kv {
     size_t stage_bytes = 0;
     unsigned char *img = nullptr;   // prefill key-tile images, grown on demand
     size_t img_bytes = 0;
+    float *ppartials = nullptr;     // prefill split-K partials, grown on demand
+    size_t ppartials_bytes = 0;
+    int *pcounters = nullptr;       // prefill split-K arrival counters
+    size_t pcounters_n = 0;
 };
 
 namespace {
@@ -205,6 +209,36 @@ int ensure_img(tq_hip_kv *kv, size_t bytes) {
         return TQ_HIP_ENOMEM;
     }
     kv->img_bytes = bytes;
+    return TQ_HIP_OK;
+}
+
+// Prefill split-K scratch: partials (grown), counters (grown, zeroed once; the
+// kernel's merging work-group puts each back to 0).
+int ensure_prefill_scratch(tq_hip_kv *kv, size_t pbytes, size_t cn, hipStream_t s) {
+    if (pbytes > kv->ppartials_bytes) {
+        TQ_TRY(hipDeviceSynchronize());
+        if (kv->ppartials) TQ_TRY(hipFree(kv->ppartials));
+        kv->ppartials = nullptr;
+        kv->ppartials_bytes = 0;
+        if (hipMalloc(&kv->ppartials, pbytes) != hipSuccess) {
+            kv->ppartials = nullptr;
+            return TQ_HIP_ENOMEM;
+        }
+        kv->ppartials_bytes = pbytes;
+    }
+    if (cn > kv->pcounters_n) {
+        TQ_TRY(hipDeviceSynchronize());
+        if (kv->pcounters) TQ_TRY(hipFree(kv->pcounters));
+        kv->pcounters = nullptr;
+        kv->pcounters_n = 0;
+        if (hipMalloc(&kv->pcounters, cn * sizeof(int)) != hipSuccess) {
+            kv->pcounters = nullptr;
+            return TQ_HIP_ENOMEM;
+        }
+        TQ_TRY(hipMemsetAsync(kv->pcounters, 0, cn * sizeof(int), s));
+        TQ_TRY(hipStreamSynchronize(s));
+        kv->pcounters_n = cn;
+    }
     return TQ_HIP_OK;
 }
 
@@ -535,6 +569,8 @@ void tq_hip_kv_destroy(tq_hip_kv *kv) {
     if (kv->stage) (void)hipFree(kv->stage);
     if (kv->hstage) (void)hipHostFree(kv->hstage);
     if (kv->img) (void)hipFree(kv->img);
+    if (kv->ppartials) (void)hipFree(kv->ppartials);
+    if (kv->pcounters) (void)hipFree(kv->pcounters);
     if (kv->stream) (void)hipStreamDestroy(kv->stream);
     delete kv;
 }
@@ -723,7 +759,9 @@ int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d
                             kv->desc.head_dim, s));
     // the dense kernel restages every key tile of [0, pos0+n): worth it from a
     // few dozen new tokens on; shorter batches attend in the decode form
-    if (prefill_dense() && n >= kPrefillDenseMin &&
+    // the dense kernel moves q, cos/sin and out in 16-byte vectors
+    const bool aligned16 = (((uintptr_t)d_q | (uintptr_t)d_cos | (uintptr_t)d_sin | (uintptr_t)d_out) & 15) == 0;
+    if (prefill_dense() && n >= kPrefillDenseMin && aligned16 &&
         tq_prefill_mfma_supported(D.head_dim, D.n_q_heads / D.n_kv_heads, pos0 + n)) {
         TqPrefillArgs t;
         t.view = kv->view;
@@ -742,9 +780,15 @@ int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d
         seq_contig(kv, seq, &first, &pages);
         t.contig_first = pages > 0 ? first : -1;
         t.contig_pages = pages;
-        const int rc = ensure_img(kv, tq_prefill_image_bytes(D.head_dim, D.n_kv_heads, pos0 + n));
+        int rc = ensure_img(kv, tq_prefill_image_bytes(D.head_dim, D.n_kv_heads, pos0 + n));
+        if (rc != TQ_HIP_OK) return rc;
+        size_t pbytes = 0, cn = 0;
+        tq_prefill_scratch(D.head_dim, D.n_q_heads / D.n_kv_heads, D.n_kv_heads, pos0, n, &pbytes, &cn);
+        rc = ensure_prefill_scratch(kv, std::max<size_t>(pbytes, 16), std::max<size_t>(cn, 1), s);
         if (rc != TQ_HIP_OK) return rc;
         t.img = kv->img;
+        t.partials = kv->ppartials;
+        t.counters = kv->pcounters;
         return herr(tq_launch_prefill(t, s));
     }
     return decode_common(kv, n, nullptr, nullptr, 0, seq, 0, pos0, pos0 + n, d_q, d_cos, d_sin, nullptr, nullptr,

@@ -259,7 +259,13 @@ struct TqPrefillArgs {
     int contig_first;      // as in TqDecodeArgs
     int contig_pages;
     unsigned char *img;    // tq_prefill_image_bytes() of scratch for the staged key tiles
+    float *partials;       // split-K partials (tq_prefill_scratch bytes)
+    int *counters;         // split-K arrival counters, zero between launches
 };
+// Scratch the prefill of tokens [pos0, pos0+n) needs beyond the image: split-K
+// partials (bytes) and arrival counters (ints, zero-initialised by the caller).
+void tq_prefill_scratch(int head_dim, int group, int n_kv_heads, int pos0, int n, size_t *partial_bytes,
+                        size_t *counter_ints);
 // The MFMA causal prefill covers head_dim 64/128, groups 1/2/4/8 and keys
 // [0, kend) up to 65536.
 bool tq_prefill_mfma_supported(int head_dim, int group, int kend);
