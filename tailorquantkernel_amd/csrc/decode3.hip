@@ -1,11 +1,13 @@
 // decode3.hip — attend_q8 (model/attention_layer.c:125-150) on the paged cache,
 // with both contractions on the matrix cores.
 //
-// Grid (split, kv head, query); a work-group of four waves owns the tokens
-// [split*split_tokens, +split_tokens) of one kv head and all G query heads that
-// read it, so every K/V byte is fetched once per step.  The range is cut into
-// tiles of 32 keys (two pages); wave w takes tiles w, w+4, w+8, ... and runs
-// its own online softmax over them, so the key loop has no barrier at all.
+// Grid (split, kv head, query); a work-group of W waves (4, or 8 for short
+// splits) owns the tokens [split*split_tokens, +split_tokens) of one kv head
+// and all G query heads that read it, so every K/V byte is fetched once per
+// step.  The range is cut into tiles of 32 keys (two pages); wave w takes tiles
+// w, w+W, w+2W, ... and runs its own online softmax over them, so the key loop
+// has no barrier at all.  Each wave quantizes the group's q rows itself, from
+// its own staged copy, straight into the lanes of its score operand.
 // Tiles are copied straight from HBM into the wave's LDS slots by
 // global_load_lds_dwordx4 (no staging registers), two tiles ahead, then:
 //
@@ -32,7 +34,7 @@
 //           exact in bf16, so hi.V + lo.V in fp32 carries W's precision.
 //           Column (h,b) of the output is kept for the columns of block b.
 //
-// The four waves merge (m, l, o) through LDS in wave order.  With several
+// The W waves merge (m, l, o) through LDS in wave order.  With several
 // splits each work-group writes its partial (o, m, l) with 16-byte stores at
 // agent coherence (sc1: through to the point all XCDs share) and bumps an
 // arrival counter; the last one merges the partials in split order, so results
@@ -85,7 +87,6 @@ struct L3 {
 template <int HD, int G>
 struct Smem3 {
     using L = L3<HD, G>;
-    unsigned char qblk[G * L::ROW];          // the group's q rows, quantize_row_q8
     unsigned char newrow[2 * L::ROW];        // step mode: the new token's K, V
     int pages[kMaxSplitPages3];              // physical page of each page of the split
     float wts[G * kMaxSplits3];              // combine weights
@@ -326,22 +327,73 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
     // the one wave whose tiles hold pos_new appends the new token
     const bool wave_new = owns_new && ((pos_new - t_begin) / kTK) % kWaves == wave;
 
-    // ---- 3. RoPE + exact quantize_row_q8 of the group's q rows and, in the
-    //      work-group that appends, of the new K (after RoPE) and V rows: the
-    //      32-value blocks are dealt round-robin to the four waves, each half-wave
-    //      one block (every wave staged all inputs) ----
-    {
-        constexpr int NQB = G * NB;
-        const int nblk = NQB + (owns_new ? 2 * NB : 0);
-        for (int j0 = 2 * wave; j0 < nblk; j0 += 2 * kWaves) {
+    // ---- 3. the B operand of the score product, per wave from its own staged
+    //      copy (no barrier): lane (l16, lg) holds column (h, b) = 16 nt + l16,
+    //      values 8 lg .. 8 lg + 7 of q block b of head h after RoPE, quantized
+    //      exactly as quantize_row_q8 does (kernel/quant_x.c:12-33): the block's
+    //      absmax is the max over its four lanes (l16 + 16 lg) ----
+    const int bl = l16 % NB;                  // block of this lane's columns (same in every nt)
+    long qb[NT][NB];                          // B operand of the score product for block b'
+    float qdl[NT];                            // qd[h][b] * scale * log2 e
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int h = (16 * nt + l16) / NB;
+        const bool real = h < G;
+        const float *row = stq + min(h, G - 1) * HD;
+        const int e0 = kQK * bl + 8 * lg;
+        float x[8];
+        *reinterpret_cast<v4f *>(&x[0]) = *reinterpret_cast<const v4f *>(row + e0);
+        *reinterpret_cast<v4f *>(&x[4]) = *reinterpret_cast<const v4f *>(row + e0 + 4);
+        if (rot) {
+            constexpr int HALF = HD / 2;
+            const bool lower = e0 < HALF;
+            const int pi = lower ? e0 : e0 - HALF;
+            const float *pr = row + (lower ? e0 + HALF : e0 - HALF);
+            float y[8], c[8], sn[8];
+            *reinterpret_cast<v4f *>(&y[0]) = *reinterpret_cast<const v4f *>(pr);
+            *reinterpret_cast<v4f *>(&y[4]) = *reinterpret_cast<const v4f *>(pr + 4);
+            *reinterpret_cast<v4f *>(&c[0]) = *reinterpret_cast<const v4f *>(stc + pi);
+            *reinterpret_cast<v4f *>(&c[4]) = *reinterpret_cast<const v4f *>(stc + pi + 4);
+            *reinterpret_cast<v4f *>(&sn[0]) = *reinterpret_cast<const v4f *>(sts + pi);
+            *reinterpret_cast<v4f *>(&sn[4]) = *reinterpret_cast<const v4f *>(sts + pi + 4);
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                x[i] = lower ? rope_lower(x[i], y[i], c[i], sn[i]) : rope_upper(y[i], x[i], c[i], sn[i]);
+        }
+        // |x| with NaN and -0 as 0, the strict "val > max" scan's value in any order
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float av = x[i] < 0.0f ? -x[i] : x[i];
+            m = fmaxf(m, av > 0.0f ? av : 0.0f);
+        }
+        m = xrow_max(m);
+        const float d = quant_scale(m);
+        const float inv = quant_inverse(d);
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            w0 |= quant_code(x[i], inv) << (8 * i);
+            w1 |= quant_code(x[4 + i], inv) << (8 * i);
+        }
+        const long codes = (long)(((unsigned long)w1 << 32) | w0);
+        qdl[nt] = real ? d * (a.scale * kLog2e) : 0.0f;
+#pragma unroll
+        for (int bb = 0; bb < NB; bb++) qb[nt][bb] = (real && bb == bl) ? codes : 0;
+    }
+
+    // ---- the work-group that appends: RoPE + exact quantize_row_q8 of the
+    //      new K (after RoPE) and V rows, one 32-value block per half-wave,
+    //      written to the cache and kept for the staged tile ----
+    if (owns_new) {
+        constexpr int NNB = 2 * NB;
+        for (int j0 = 2 * wave; j0 < NNB; j0 += 2 * kWaves) {
             const int j = j0 + (lane >> 5);
-            if (j < nblk) {   // a whole 32-lane block is in or out
-                const bool is_q = j < NQB;
-                const int jr = is_q ? j : j - NQB;           // new row: K blocks then V blocks
-                const int b = jr % NB;
+            if (j < NNB) {   // a whole 32-lane block is in or out
+                const int b = j % NB;
                 const int col = 32 * b + (lane & 31);
-                const bool is_v = !is_q && jr >= NB;
-                const float *row = is_q ? stq + (j / NB) * HD : (is_v ? stv : stk);
+                const bool is_v = j >= NB;
+                const float *row = is_v ? stv : stk;
                 float x = row[col];
                 if (rot && !is_v) {
                     const int half = HD / 2;
@@ -349,13 +401,10 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
                     x = col < half ? rope_lower(row[col], row[col + half], stc[pi], sts[pi])
                                    : rope_upper(row[col - half], row[col], stc[pi], sts[pi]);
                 }
-                unsigned char *dst = is_q ? sm.qblk + (j / NB) * ROW : sm.newrow + (is_v ? ROW : 0);
-                quantize_store32(x, dst + b * kBlockBytes);
+                quantize_store32(x, sm.newrow + (is_v ? ROW : 0) + b * kBlockBytes);
             }
         }
-    }
-    __syncthreads();
-    if (owns_new) {
+        __syncthreads();
         const int phys = page_of(pos_new / kPage);
         if (phys >= 0 && tid < 2 * (ROW / 4)) {
             const bool is_v = tid >= ROW / 4;
@@ -364,23 +413,6 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
                                  (pos_new % kPage) * ROW + 4 * ww;
             *reinterpret_cast<uint32_t *>(dst) =
                 *reinterpret_cast<const uint32_t *>(sm.newrow + (is_v ? ROW : 0) + 4 * ww);
-        }
-    }
-
-    // ---- per-lane constants: column (h, b) = 16*nt + l16 of the products ----
-    const int bl = l16 % NB;                  // block of this lane's columns (same in every nt)
-    long qb[NT][NB];                          // B operand of the score product for block b'
-    float qdl[NT];                            // qd[h][b]
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int h = (16 * nt + l16) / NB;
-        const bool real = h < G;
-        const unsigned char *qrow = sm.qblk + min(h, G - 1) * ROW;
-        qdl[nt] = real ? lds_f(qrow + bl * kBlockBytes) * (a.scale * kLog2e) : 0.0f;
-#pragma unroll
-        for (int bb = 0; bb < NB; bb++) {
-            const long c = lds_ld8(qrow + bb * kBlockBytes + 4 + 8 * lg);
-            qb[nt][bb] = (real && bb == bl) ? c : 0;
         }
     }
 
@@ -630,10 +662,12 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
             v4f rows[CL];
 #pragma unroll
             for (int i = 0; i < CL; i++) {
-                const int s = min(s0 + sg + NSG * i, kMaxSplits3);
-                rows[i] = active ? __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
-                                                               prs, (s * L::PSTRIDE + 4 * u) * 4, 0, kCoherent))
-                                 : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                // only the rows of real splits are requested
+                const int s = s0 + sg + NSG * i;
+                rows[i] = (active && s < nvalid) ? __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                            prs, (s * L::PSTRIDE + 4 * u) * 4, 0,
+                                                                            kCoherent))
+                                                 : v4f{0.0f, 0.0f, 0.0f, 0.0f};
             }
             if (u0 == 0 && s0 == 0) {
 #pragma unroll
