@@ -362,7 +362,7 @@ def bench_decode_8b(args, nat, hip):
         "host_boundary_us_per_call": boundary_us,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "decode3_kernel<128, 4, 8> (fused RoPE + append + split-K attend + combine)",
+                     "kernel": "decode3_kernel<128, 4, 4> (fused RoPE + append + split-K attend + combine)",
                      "kernel_ms": ms_per_step, "algorithmic_bytes": kv_bytes},
     }
     check = (kc0.reshape(-1), vc0.reshape(-1), q, k, v, got)
