@@ -175,6 +175,14 @@ int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d
                          const float *d_k, const float *d_v, const float *d_cos,
                          const float *d_sin, float *d_out, void *stream);
 
+/* ---- measurement: streaming-read bandwidth of device memory, the GPU
+ * counterpart of the reference's host RAM probe (tools/membw.h:1-80).  Reads
+ * `bytes` (a multiple of 16) of `buf` once with 16-byte loads; `sink` (device,
+ * tq_hip_membw_sink_bytes() bytes) is written only if the XOR of the data
+ * equals `never`.  Asynchronous on `stream`; the caller times it. */
+size_t tq_hip_membw_sink_bytes(void);
+int tq_hip_membw_read(const void *buf, size_t bytes, void *sink, unsigned int never, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -69,7 +69,6 @@ constexpr int kMaxSplitsP = 8;           // chunks of one query-block pair
 constexpr int kItemOverheadTiles = 3;    // prologue + merge of a work item, in tile times
 constexpr int kCounterStrideP = 64;      // ints: one 256-byte line per counter
 constexpr int kCoherentP = 16;           // cache policy sc1: agent-coherent access
-constexpr int kResidentWGs = 512;        // work-groups resident at once (2 per CU)
 
 // Layout of one tile image (bytes), shared by both kernels.
 template <int HD>

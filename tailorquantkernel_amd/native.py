@@ -69,6 +69,8 @@ _PROTOS = {
     "tq_hip_decode_step_async": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tq_hip_prefill": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tq_hip_prefill_async": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "tq_hip_membw_sink_bytes": (_sz, []),
+    "tq_hip_membw_read": (_i, [_vp, _sz, _vp, C.c_uint, _vp]),
 }
 
 EXPORTS = tuple(_PROTOS)

@@ -55,6 +55,9 @@ def test_host_validation_without_device(lib):
     assert lib.tq_hip_attn_scores_q8(None, 0, None, 1, 1, 1.0, None, 1, None) == native.EINVAL
     assert lib.tq_hip_attn_accum_q8(None, 1, 1, None, 1, 1, None, 8, None) == native.EINVAL
     assert lib.tq_hip_softmax(None, -1, 1, 1, None) == native.EINVAL
+    assert lib.tq_hip_membw_read(None, 1 << 20, None, 0, None) == native.EINVAL
+    assert lib.tq_hip_membw_read(C.c_void_p(16), 100, C.c_void_p(16), 0, None) == native.EINVAL   # not whole 16 B
+    assert lib.tq_hip_membw_sink_bytes() > 0
     for code, text in ((0, "ok"), (-1, "argument out of range"), (-3, "unsupported head_dim or group size")):
         assert native.strerror(code) == text
 
