@@ -1,11 +1,18 @@
 // kv_append.hip — store_kv, Q8 branch (model/attention_layer.c:66-90), fused
 // with RoPE on K (rope_heads, :188), into the paged HBM cache.
 //
-// One work-group per (row, kv head), 2*head_dim threads: threads [0, hd) own
-// the K row, [hd, 2hd) the V row, one value each; each 32-lane group
-// quantizes one block (exact quantize_row_q8) and writes it as a 36-byte
-// block_q8 with dword stores.  Rows whose position has no mapped page are
-// skipped whole.
+// Two kernels, one result:
+//   append_kernel      rows with their own (sequence, position) each: one
+//                      work-group per (row, kv head), 2*head_dim threads, one
+//                      value per thread, a 32-lane group per block.
+//   append_run_kernel  a run of consecutive positions of one sequence (the
+//                      prefill and bulk case): one work-group per (logical
+//                      page, kv head).  Every thread issues all its 16-byte
+//                      loads first, a 32-value block is quantized over 8
+//                      lanes of 4 values, and the page's rows are assembled in
+//                      LDS and written whole, only the rows of the run.
+// Both quantize exactly as quantize_row_q8 does.  Rows whose position has no
+// mapped page are skipped whole.
 #include "tq_common.hpp"
 
 namespace {
@@ -43,6 +50,88 @@ __global__ __launch_bounds__(512) void append_kernel(PagedView view, const int32
     quantize_store32(x, dst);
 }
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int HD>
+__global__ __launch_bounds__(kThreads) void append_run_kernel(PagedView view, int seq, int pos0, int n,
+                                                             const float *__restrict__ k,
+                                                             const float *__restrict__ v,
+                                                             const float *__restrict__ cos_t,
+                                                             const float *__restrict__ sin_t) {
+    constexpr int HALF = HD / 2;
+    constexpr int CPR = HD / 8;                          // tasks per (row, K|V): float4 c of each half
+    constexpr int ROW = HD / kQK * kBlockBytes;          // bytes of a row
+    constexpr int TASKS = kPage * 2 * CPR;
+    constexpr int TPT = (TASKS + kThreads - 1) / kThreads;
+    constexpr int CB = ROW % 16 == 0 ? 16 : 8;           // bytes per copy of a row
+    static_assert(CPR % 8 == 0 && ROW % CB == 0, "whole blocks per half, whole copies per row");
+    __shared__ __align__(16) unsigned char run[2][kPage][ROW];   // the page's K rows | V rows
+    const int lp = pos0 / kPage + (int)blockIdx.x, kvh = blockIdx.y;
+    const int p_lo = max(pos0, lp * kPage), p_hi = min(pos0 + n, lp * kPage + kPage);
+    const int phys = phys_page(view, seq, lp);
+    if (phys < 0) return;
+    const int tid = threadIdx.x;
+    const bool rot = cos_t != nullptr;
+
+    v4f xl[TPT], xu[TPT], cs[TPT], sn[TPT];
+#pragma unroll
+    for (int t = 0; t < TPT; t++) {
+        const int task = tid + kThreads * t;
+        const int r = task / (2 * CPR), kv = (task / CPR) & 1, c = task % CPR;
+        const int pos = lp * kPage + r;
+        xl[t] = xu[t] = cs[t] = sn[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (task < TASKS && pos >= p_lo && pos < p_hi) {
+            const size_t row = (size_t)(pos - pos0);
+            const float *src = (kv ? v : k) + (row * view.n_kv_heads + kvh) * HD;
+            xl[t] = *reinterpret_cast<const v4f *>(src + 4 * c);
+            xu[t] = *reinterpret_cast<const v4f *>(src + HALF + 4 * c);
+            if (!kv && rot) {
+                cs[t] = *reinterpret_cast<const v4f *>(cos_t + row * HALF + 4 * c);
+                sn[t] = *reinterpret_cast<const v4f *>(sin_t + row * HALF + 4 * c);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TPT; t++) {
+        const int task = tid + kThreads * t;
+        if (TPT * kThreads > TASKS && task >= TASKS) break;   // whole 8-lane groups
+        const int r = task / (2 * CPR), kv = (task / CPR) & 1, c = task % CPR;
+        float lo[4], up[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (!kv && rot) {
+                lo[i] = rope_lower(xl[t][i], xu[t][i], cs[t][i], sn[t][i]);
+                up[i] = rope_upper(xl[t][i], xu[t][i], cs[t][i], sn[t][i]);
+            } else {
+                lo[i] = xl[t][i];
+                up[i] = xu[t][i];
+            }
+        }
+        unsigned char *row = run[kv][r];
+        const bool leader = (c & 7) == 0;
+        const int bl = (4 * c) / kQK, bu = (HALF + 4 * c) / kQK;
+        quantize8x4(lo, reinterpret_cast<float *>(row + bl * kBlockBytes), row + bl * kBlockBytes + 4 + (4 * c) % kQK,
+                    leader);
+        quantize8x4(up, reinterpret_cast<float *>(row + bu * kBlockBytes), row + bu * kBlockBytes + 4 + (4 * c) % kQK,
+                    leader);
+    }
+    __syncthreads();
+    // the run's rows of this page, whole rows in CB-byte copies
+    unsigned char *dst = head_run_ptr(view, phys, kvh);
+    constexpr int PER_ROW = ROW / CB;
+    for (int ch = tid; ch < 2 * kPage * PER_ROW; ch += kThreads) {
+        const int kv = ch / (kPage * PER_ROW), r = (ch / PER_ROW) % kPage, j = ch % PER_ROW;
+        const int pos = lp * kPage + r;
+        if (pos < p_lo || pos >= p_hi) continue;
+        unsigned char *g = dst + (kv ? view.kv_chunk : 0) + (size_t)r * ROW + CB * j;
+        if constexpr (CB == 16)
+            *reinterpret_cast<u32x4 *>(g) = *reinterpret_cast<const u32x4 *>(run[kv][r] + CB * j);
+        else
+            *reinterpret_cast<u32x2 *>(g) = *reinterpret_cast<const u32x2 *>(run[kv][r] + CB * j);
+    }
+}
+
 }  // namespace
 
 hipError_t tq_launch_append(const PagedView &view, int n_rows, const int32_t *seq,
@@ -50,6 +139,18 @@ hipError_t tq_launch_append(const PagedView &view, int n_rows, const int32_t *se
                             const float *v, const float *c, const float *sn, int hd,
                             hipStream_t s) {
     if (n_rows <= 0) return hipSuccess;
+    // a run of one sequence with 16-byte aligned inputs: a work-group per page
+    const bool aligned = (((uintptr_t)k | (uintptr_t)v | (uintptr_t)c | (uintptr_t)sn) & 15) == 0;
+    if (!seq && !pos && aligned && (hd == 64 || hd == 128 || hd == 256) && pos0 >= 0) {
+        const int pages = (pos0 + n_rows - 1) / kPage - pos0 / kPage + 1;
+        const dim3 grid(pages, view.n_kv_heads);
+        switch (hd) {
+            case 64: hipLaunchKernelGGL(append_run_kernel<64>, grid, dim3(kThreads), 0, s, view, seq_const, pos0, n_rows, k, v, c, sn); break;
+            case 128: hipLaunchKernelGGL(append_run_kernel<128>, grid, dim3(kThreads), 0, s, view, seq_const, pos0, n_rows, k, v, c, sn); break;
+            default: hipLaunchKernelGGL(append_run_kernel<256>, grid, dim3(kThreads), 0, s, view, seq_const, pos0, n_rows, k, v, c, sn); break;
+        }
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(append_kernel, dim3(n_rows, view.n_kv_heads), dim3(2 * hd), 0, s, view, seq,
                        pos, k, v, c, sn, hd, seq_const, pos0);
     return hipGetLastError();

@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void prefill_stage_kernel(StageArgs a) {
     using I = TileImg<HD>;
     constexpr int ROW = I::ROW;
     constexpr int RDW = kKT * ROW / 4;   // dwords of one tile's K (or V) rows
-    __shared__ uint32_t raw[2][RDW];
+    __shared__ __align__(16) uint32_t raw[2][RDW];
     __shared__ int page[2];
     const int tid = threadIdx.x;
     const int kt = blockIdx.x;
@@ -170,16 +170,20 @@ __global__ __launch_bounds__(kThreads) void prefill_stage_kernel(StageArgs a) {
         page[tid] = p;
     }
     __syncthreads();
-    for (int i = tid; i < 2 * RDW; i += kThreads) {
-        const int kv = i / RDW, rem = i % RDW;
-        const int t = rem / (ROW / 4), w = rem % (ROW / 4);
-        const int p = kt * kKT + t;
-        const int pg = page[t / kPage];
-        uint32_t x = 0;
-        if (p < a.kend && pg >= 0)
-            x = *reinterpret_cast<const uint32_t *>(head_run_ptr(v, pg, kvh) + kv * v.kv_chunk +
-                                                    (p % kPage) * ROW + w * 4);
-        raw[kv][rem] = x;
+    // a page's K (or V) rows are one contiguous run: copy them in CB-byte
+    // pieces, whole rows per piece; rows past the keys (or unmapped) are zero
+    // so that no stale scale reaches P.V
+    constexpr int CB = ROW % 16 == 0 ? 16 : 8;
+    constexpr int PR = kPage * ROW / CB;   // pieces per page run
+    typedef uint32_t piece_t __attribute__((ext_vector_type(CB / 4)));
+    for (int i = tid; i < 2 * 2 * PR; i += kThreads) {
+        const int kv = i / (2 * PR), pg = (i / PR) & 1, ch = i % PR;
+        const int p = kt * kKT + pg * kPage + (ch * CB) / ROW;
+        const int phys = page[pg];
+        piece_t x = piece_t(0u);
+        if (p < a.kend && phys >= 0)
+            x = *reinterpret_cast<const piece_t *>(head_run_ptr(v, phys, kvh) + kv * v.kv_chunk + ch * CB);
+        *reinterpret_cast<piece_t *>(reinterpret_cast<unsigned char *>(raw[kv]) + pg * kPage * ROW + ch * CB) = x;
     }
     __syncthreads();
     const unsigned char *rk = reinterpret_cast<const unsigned char *>(raw[0]);
@@ -250,29 +254,6 @@ struct PrefillArgs {
     const unsigned char *img;
 };
 
-// Quantize a 32-value block held 4 values per lane over an aligned group of 8
-// lanes (half a DPP row) and store its scale and this lane's 4 codes
-// (quantize_row_q8, kernel/quant_x.c:12-33).  The absmax keeps the strict
-// "val > max" scan's value as block_amax32 does: |x| with NaN and -0 mapped
-// to 0, then an exact max in any order.
-__device__ __forceinline__ void quantize8x4(const float (&x)[4], float *d_out, unsigned char *codes, bool leader) {
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float a = x[i] < 0.0f ? -x[i] : x[i];
-        m = fmaxf(m, a > 0.0f ? a : 0.0f);
-    }
-    m = fmaxf(m, dpp_f<kDppQuadXor1>(m));
-    m = fmaxf(m, dpp_f<kDppQuadXor2>(m));
-    m = fmaxf(m, dpp_f<kDppRowHalfMirror>(m));
-    const float d = quant_scale(m);
-    const float inv = quant_inverse(d);
-    uint32_t w = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) w |= quant_code(x[i], inv) << (8 * i);
-    if (leader) *d_out = d;
-    *reinterpret_cast<uint32_t *>(codes) = w;
-}
 
 // Key tiles query block b reads: keys [0, pos0 + its last query + 1).
 __host__ __device__ inline int block_tiles(int pos0, int n, int qb, int b) {

@@ -124,6 +124,30 @@ __device__ __forceinline__ void quantize_store32(float x, unsigned char *blk) {
     if ((lane & 3) == 0) *reinterpret_cast<uint32_t *>(blk + 4 + lane) = word;
 }
 
+// Quantize a 32-value block held 4 values per lane over an aligned group of 8
+// lanes (half a DPP row) and store its scale and this lane's 4 codes
+// (quantize_row_q8, kernel/quant_x.c:12-33).  The absmax keeps the strict
+// "val > max" scan's value as block_amax32 does: |x| with NaN and -0 mapped
+// to 0, then an exact max in any order.
+__device__ __forceinline__ void quantize8x4(const float (&x)[4], float *d_out, unsigned char *codes, bool leader) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a = x[i] < 0.0f ? -x[i] : x[i];
+        m = fmaxf(m, a > 0.0f ? a : 0.0f);
+    }
+    m = fmaxf(m, dpp_f<kDppQuadXor1>(m));
+    m = fmaxf(m, dpp_f<kDppQuadXor2>(m));
+    m = fmaxf(m, dpp_f<kDppRowHalfMirror>(m));
+    const float d = quant_scale(m);
+    const float inv = quant_inverse(d);
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) w |= quant_code(x[i], inv) << (8 * i);
+    if (leader) *d_out = d;
+    *reinterpret_cast<uint32_t *>(codes) = w;
+}
+
 // ---------------------------------------------------------------------------
 // RoPE, rotate-half pairing i <-> i + hd/2 (model/rope.c:14-22):
 //   lower half: x0*c - x1*s      upper half: x0*s + x1*c
