@@ -62,6 +62,7 @@ constexpr float kLazy = 8.0f;            // log2 headroom before the running max
 constexpr int kCoherent = 16;            // cache policy sc1: agent-coherent access
 constexpr int kBufWord3 = 0x00020000;    // raw buffer descriptor, 32-bit data
 constexpr int kCounterStride = TQ_DECODE_COUNTER_STRIDE;   // ints: one 256-byte line per counter
+constexpr int kSortQ = 128;              // ragged batches up to this many queries go longest first
 
 template <int HD, int G>
 struct L3 {
@@ -89,6 +90,8 @@ struct Smem3 {
     using L = L3<HD, G>;
     unsigned char newrow[2 * L::ROW];        // step mode: the new token's K, V
     int pages[kMaxSplitPages3];              // physical page of each page of the split
+    int qlen[kSortQ];                        // the batch's lengths, for the longest-first order
+    int qsel;
     float wts[G * kMaxSplits3];              // combine weights
     int last;
 };
@@ -193,7 +196,33 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lg = lane >> 4, l16 = lane & 15;
-    const int split = blockIdx.x, kvh = blockIdx.y, qi = blockIdx.z;
+    const int split = blockIdx.x, kvh = blockIdx.y;
+    // The query this work-group serves.  A ragged batch goes longest first:
+    // grid z is the rank of the query's length (ties by index), so the
+    // work-groups of the longest sequences are dispatched first and the
+    // short ones fill the gaps at the end (longest-processing-time order).
+    // Each query's result does not depend on the order.
+    int qi = blockIdx.z;
+    if (a.n_q > 1) {
+        if (!a.len_of) {
+            qi = a.n_q - 1 - (int)blockIdx.z;   // query i attends pos0 + i + 1 keys
+        } else if (a.n_q <= kSortQ) {
+            for (int i = tid; i < a.n_q; i += kThreads) sm.qlen[i] = a.len_of[i];
+            __syncthreads();
+            for (int i = tid; i < a.n_q; i += kThreads) {
+                const int li = sm.qlen[i];
+                int r = 0;
+                for (int u = 0; u < a.n_q; u++) {
+                    const int lu = sm.qlen[u];
+                    r += (lu > li) || (lu == li && u < i);
+                }
+                if (r == (int)blockIdx.z) sm.qsel = i;
+            }
+            __syncthreads();
+            qi = sm.qsel;
+        }
+    }
+    qi = __builtin_amdgcn_readfirstlane(qi);
     const int t_begin = split * a.split_tokens;
     const int split_end = t_begin + a.split_tokens;
     const PagedView &view = a.view;
