@@ -674,9 +674,10 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
     constexpr int CL = 16;
     const int sg = tid / TPS;
     const bool active = sg < NSG;   // TPS * NSG can fall short of the 256 threads
-    float mv[2], lv[2];
+    constexpr int HR = (G + kWaves - 1) / kWaves;   // heads per wave for the weights
+    float mv[HR], lv[HR];
 #pragma unroll
-    for (int r = 0; r < 2; r++) {
+    for (int r = 0; r < HR; r++) {
         const int h = min(wave + kWaves * r, G - 1);
         mv[r] = __uint_as_float(
             __builtin_amdgcn_raw_buffer_load_b32(prs, (lane * L::PSTRIDE + G * HD + h) * 4, 0, kCoherent));
@@ -700,7 +701,7 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
             }
             if (u0 == 0 && s0 == 0) {
 #pragma unroll
-                for (int r = 0; r < 2; r++) {
+                for (int r = 0; r < HR; r++) {
                     const int h = wave + kWaves * r;
                     if (h < G) {
                         const bool ok = lane < nvalid;
