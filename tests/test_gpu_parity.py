@@ -384,6 +384,49 @@ def test_decode_step_fused(nat, oracle):
     kv.close()
 
 
+@pytest.mark.parametrize("nseq", [40, 160])
+def test_batched_decode_order(nat, oracle, nseq):
+    """Ragged batches with repeated lengths: up to 128 queries are served
+    longest first (ties by index), larger batches in order; either way every
+    query matches the oracle on its own rows and launches repeat bit for bit."""
+    lib = nat.load()
+    nq, nkv, hd = 8, 2, 64
+    nb = hd // QK
+    rng = np.random.default_rng(nseq)
+    lens = rng.choice(np.array([1, 16, 17, 64, 129, 300], np.int32), size=nseq)
+    pages_per = (lens + 15) // 16
+    maxp = int(pages_per.max())
+    total = int(pages_per.sum())
+    kv = nat.PagedKV(nq, nkv, hd, n_pages=total, max_seqs=nseq, max_pages_per_seq=maxp)
+    perm = rng.permutation(total).astype(np.int32)
+    at = 0
+    flats = []
+    for i, L in enumerate(lens):
+        kv.set_pages(i, perm[at:at + pages_per[i]])
+        at += pages_per[i]
+        kc = oracle.quantize_row_q8(normal(nkv * int(L) * hd, 300 + i))
+        vc = oracle.quantize_row_q8(normal(nkv * int(L) * hd, 700 + i))
+        kv.write(i, 0, kc.reshape(nkv, L, nb), vc.reshape(nkv, L, nb))
+        flats.append((kc, vc))
+    q = normal(nseq * nq * hd, 9)
+    dseq, dlen = dev(nat, np.arange(nseq, dtype=np.int32)), dev(nat, lens)
+    dq, dout = dev(nat, q), nat.DeviceBuffer(nseq * nq * hd * 4)
+    outs = []
+    for _ in range(2):
+        nat.check(lib.tq_hip_decode_async(kv.h, nseq, dseq.ptr, dlen.ptr, int(lens.max()), dq.ptr, None, None,
+                                          dout.ptr, None), "decode_async")
+        nat.check(lib.tq_hip_stream_synchronize(kv.stream), "sync")
+        outs.append(dout.download((nseq, nq * hd), np.float32))
+    assert outs[0].tobytes() == outs[1].tobytes()
+    for qi in range(nseq):
+        L = int(lens[qi])
+        kc, vc = flats[qi]
+        rc, ref = oracle.attend_q8(kc, vc, nq, nkv, hd, L, q[qi * nq * hd:(qi + 1) * nq * hd], L - 1)
+        assert rc == 0
+        assert_close(outs[0][qi], ref, f"query {qi} len {L} of {nseq}")
+    kv.close()
+
+
 def test_batched_decode_paged(nat, oracle):
     """Many sequences of ragged lengths on shuffled pages (the batched-decode
     shape at reduced count); each checked against the oracle on its own rows."""
