@@ -538,8 +538,8 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): this path has no multi-GPU "
-              "collective; see the sharding note in DESIGN.md", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): the attention path has no "
+              "cross-GPU collective of its own; it would shard by kv head, one GPU per share", file=sys.stderr)
         sys.exit(2)
 
     from tailorquantkernel_amd import native as nat
