@@ -78,6 +78,10 @@ class Oracle:
         L.oracle_attention_qkv.restype = _i
         L.oracle_prefill_qkv.argtypes = [_vp, _vp, _i, _i, _i, _i, _f, _i, _i, _vp, _vp, _vp, _vp, _vp]
         L.oracle_prefill_qkv.restype = _i
+        L.oracle_pack_matrix_q8.argtypes = [_vp, _i, _i, _vp]
+        L.oracle_matmul_q8.argtypes = [_vp, _vp, _vp, _i, _i]
+        L.oracle_matmul_q8_batch.argtypes = [_vp, _vp, _vp, _i, _i, _i]
+        L.oracle_project_q8.argtypes = [_vp, _i, _i, _vp, _i, _vp]
 
     # --- element ops -------------------------------------------------------
     def quantize_row_q8(self, x) -> np.ndarray:
@@ -139,6 +143,33 @@ class Oracle:
                                          ptr(q), ptr(k), ptr(v), ptr(scores), ptr(out))
         return rc, out
 
+    # --- weight side ---------------------------------------------------------
+    def pack_matrix_q8(self, W) -> np.ndarray:
+        """rows x cols floats -> rows x cols/32 block_q8 (packer/packer.c)."""
+        W = f32(W)
+        rows, cols = W.shape
+        out = blocks(rows * (cols // QK)).reshape(rows, cols // QK)
+        self.lib.oracle_pack_matrix_q8(ptr(W), rows, cols, ptr(out))
+        return out
+
+    def matmul_q8(self, Wq, xq, rows: int, cols: int, n_tok: int = 1) -> np.ndarray:
+        """y[n_tok, rows] from block_q8 weights and n_tok block_q8 rows."""
+        y = np.zeros((n_tok, rows), np.float32)
+        Wq = np.ascontiguousarray(Wq)
+        xq = np.ascontiguousarray(xq)
+        assert Wq.size == rows * (cols // QK) and xq.size == n_tok * (cols // QK)
+        self.lib.oracle_matmul_q8_batch(ptr(Wq), ptr(xq), ptr(y), rows, cols, n_tok)
+        return y
+
+    def project_q8(self, Wq, rows: int, cols: int, x) -> np.ndarray:
+        """quantize_row_q8 of each row of x, then the Q8 matmul: y[n_tok, rows]."""
+        x = f32(x).reshape(-1, cols)
+        y = np.zeros((x.shape[0], rows), np.float32)
+        Wq = np.ascontiguousarray(Wq)
+        assert Wq.size == rows * (cols // QK)
+        self.lib.oracle_project_q8(ptr(Wq), rows, cols, ptr(x), x.shape[0], ptr(y))
+        return y
+
     def attend_q8(self, kc, vc, nq, nkv, hd, max_tokens, q, pos):
         scores = np.zeros(nq * max_tokens, np.float32)
         out = np.zeros(nq * hd, np.float32)
@@ -174,6 +205,12 @@ class Ref:
         L.tqref_attention_qkv.argtypes = [_i, _i, _i, _i, _f, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]
         L.tqref_attention_qkv.restype = _i
         L.tqref_isa.restype = C.c_char_p
+        L.pack_matrix.argtypes = [_vp, _i, _i, _vp, C.c_char]
+        L.pack_matrix.restype = _i
+        simd = ("matmul_q8_avx2",) if not scalar else ()
+        for fn in ("matmul_q8_scalar",) + simd:
+            getattr(L, fn).argtypes = [_vp, _vp, _vp, _i, _i]
+            getattr(L, fn + "_batch").argtypes = [_vp, _vp, _vp, _i, _i, _i]
 
     @staticmethod
     def available(scalar: bool = False) -> bool:
@@ -182,3 +219,23 @@ class Ref:
 
     def isa(self) -> str:
         return self.lib.tqref_isa().decode()
+
+    def pack_matrix_q8(self, W) -> np.ndarray:
+        W = f32(W)
+        rows, cols = W.shape
+        out = blocks(rows * (cols // QK)).reshape(rows, cols // QK)
+        rc = self.lib.pack_matrix(ptr(W), rows, cols, ptr(out), b"8")
+        assert rc == 0
+        return out
+
+    def matmul_q8(self, Wq, xq, rows: int, cols: int, n_tok: int = 1, simd: bool = False):
+        """matmul_q8_scalar / matmul_q8_avx2 (their _batch forms for n_tok > 1)."""
+        y = np.zeros((n_tok, rows), np.float32)
+        Wq = np.ascontiguousarray(Wq)
+        xq = np.ascontiguousarray(xq)
+        name = "matmul_q8_avx2" if simd else "matmul_q8_scalar"
+        if n_tok == 1:
+            getattr(self.lib, name)(ptr(Wq), ptr(xq), ptr(y), rows, cols)
+        else:
+            getattr(self.lib, name + "_batch")(ptr(Wq), ptr(xq), ptr(y), rows, cols, n_tok)
+        return y

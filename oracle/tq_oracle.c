@@ -216,3 +216,76 @@ int oracle_prefill_qkv(block_q8 *k_cache, block_q8 *v_cache, int n_q_heads, int 
     }
     return 0;
 }
+
+/* ---- weight side: packing and the Q8 weight x Q8 activation matmul ------ */
+
+/* packer/packer.c:4-9,11-19,22-31 (quantize, block_scale, pack_row_q8):
+ * per 32 weights, d = amax/127 with 1 in place of 0 for an all-zero block,
+ * inverse 1/d, code = lroundf(w * inverse) (half away from zero) clamped to
+ * [-127, 127].  This differs from quantize_row_q8 on purpose: the activation
+ * quantizer rounds half to even and keeps d = 0. */
+void oracle_pack_matrix_q8(const float *W, int rows, int cols, block_q8 *out) {
+    const int nb = cols / QK;
+    for (int r = 0; r < rows; r++) {
+        for (int b = 0; b < nb; b++) {
+            const float *w = W + (size_t)r * cols + (size_t)b * QK;
+            block_q8 *o = out + (size_t)r * nb + b;
+            float amax = 0.0f;
+            for (int j = 0; j < QK; j++) {
+                const float v = fabsf(w[j]);
+                if (v > amax) amax = v;
+            }
+            float d = amax / 127.0f;
+            if (d == 0.0f) d = 1.0f;
+            const float id = 1.0f / d;
+            o->d = d;
+            for (int j = 0; j < QK; j++) {
+                long q = lroundf(w[j] * id);
+                if (q > 127) q = 127;
+                if (q < -127) q = -127;
+                o->q[j] = (int8_t)q;
+            }
+        }
+    }
+}
+
+/* kernel/q8_scalar.c:3-13: exact int32 dot of each block's codes, then
+ * ((float)s * w.d) * x.d added to one serial fp32 sum in block order. */
+static float dot_q8(const block_q8 *w, const block_q8 *x, int nb) {
+    float sum = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        int32_t s = 0;
+        for (int j = 0; j < QK; j++) s += (int32_t)w[b].q[j] * (int32_t)x[b].q[j];
+        sum += (float)s * w[b].d * x[b].d;
+    }
+    return sum;
+}
+
+/* kernel/q8_scalar.c:15-22: y[r] = dot(W row r, xq). */
+void oracle_matmul_q8(const block_q8 *W, const block_q8 *xq, float *y, int rows, int cols) {
+    const int nb = cols / QK;
+    for (int r = 0; r < rows; r++) y[r] = dot_q8(W + (size_t)r * nb, xq, nb);
+}
+
+/* kernel/q8_scalar.c:25-30: token t reads xq + t*nb and writes y + t*rows. */
+void oracle_matmul_q8_batch(const block_q8 *W, const block_q8 *xq, float *y, int rows, int cols,
+                            int n_tok) {
+    const int nb = cols / QK;
+    for (int t = 0; t < n_tok; t++)
+        oracle_matmul_q8(W, xq + (size_t)t * nb, y + (size_t)t * rows, rows, cols);
+}
+
+/* A projection as attention_layer makes it: quantize_row_q8 of each input
+ * row, then the Q8 matmul (project_qkv for one matrix,
+ * model/attention_layer.c:38-46; project_output, :161-167; the batched
+ * versions quantize every token row first, :210-218 and :238-241).
+ * x: n_tok rows of cols floats; y: n_tok rows of rows floats. */
+void oracle_project_q8(const block_q8 *W, int rows, int cols, const float *x, int n_tok,
+                       float *y) {
+    const int nb = cols / QK;
+    block_q8 xq[nb > 0 ? nb : 1];
+    for (int t = 0; t < n_tok; t++) {
+        oracle_quantize_row_q8(x + (size_t)t * cols, xq, cols);
+        oracle_matmul_q8(W, xq, y + (size_t)t * rows, rows, cols);
+    }
+}

@@ -69,6 +69,21 @@ int oracle_prefill_qkv(block_q8 *k_cache, block_q8 *v_cache, int n_q_heads, int 
                        int head_dim, int max_tokens, float rope_theta, int pos0, int n,
                        float *q, float *k, const float *v, float *scores, float *out);
 
+/* packer/packer.c:4-31 (pack_row_q8 over every row): weights -> block_q8. */
+void oracle_pack_matrix_q8(const float *W, int rows, int cols, block_q8 *out);
+
+/* kernel/q8_scalar.c:3-22 */
+void oracle_matmul_q8(const block_q8 *W, const block_q8 *xq, float *y, int rows, int cols);
+
+/* kernel/q8_scalar.c:25-30 */
+void oracle_matmul_q8_batch(const block_q8 *W, const block_q8 *xq, float *y, int rows, int cols,
+                            int n_tok);
+
+/* quantize_row_q8 per input row, then the Q8 matmul: project_qkv for one
+ * matrix and project_output (model/attention_layer.c:38-46,161-167). */
+void oracle_project_q8(const block_q8 *W, int rows, int cols, const float *x, int n_tok,
+                       float *y);
+
 #ifdef __cplusplus
 }
 #endif

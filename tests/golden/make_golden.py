@@ -19,6 +19,14 @@ rebuilt from seeds by tests/golden/gen.py, the reference's outputs:
   K/V rows and the attention output.
 
 Output: tests/golden/golden_q8.npz (inputs by seed + checksum, outputs in full).
+
+    python tests/golden/make_golden.py weights
+
+writes tests/golden/golden_matmul_q8.npz instead: the weight side of the
+path, on the shapes the reference's own kernel test runs
+(tools/test_kernel.c:178-180,187-190) — pack_matrix (packer/packer.c:22-31)
+of seeded weights, quantize_row_q8 of seeded activations and
+matmul_q8_scalar / matmul_q8_scalar_batch (kernel/q8_scalar.c:15-30).
 """
 from __future__ import annotations
 
@@ -185,5 +193,50 @@ def main() -> None:
     print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes, {len(data)} arrays)")
 
 
+WEIGHTS_OUT = os.path.join(HERE, "golden_matmul_q8.npz")
+
+
+def weights() -> None:
+    ref = Ref(scalar=True)
+    L = ref.lib
+    data: dict[str, np.ndarray] = {}
+    # (rows, cols, n_tok, x kind): the reference test's shapes (random x),
+    # its constant-x and zero-x cases, and two token batches.
+    cases = [(256, 512, 1, 0), (7, 64, 1, 0), (10, 32, 1, 0), (1027, 96, 1, 0),
+             (1024, 1024, 1, 0), (256, 512, 1, 1), (256, 512, 1, 2), (64, 256, 5, 0),
+             (96, 160, 9, 0)]
+    data["cases"] = np.array(cases, np.int64)
+    for i, (rows, cols, n_tok, kind) in enumerate(cases):
+        nb = cols // QK
+        W = fill_random(rows * cols, 3000 + 17 * i, 1.0)
+        if kind == 0:
+            x = fill_random(n_tok * cols, 4000 + 17 * i, 1.0)
+        elif kind == 1:
+            x = np.ones(n_tok * cols, np.float32)
+        else:
+            x = np.zeros(n_tok * cols, np.float32)
+        Wq = blocks(rows * nb)
+        assert L.pack_matrix(ptr(W), rows, cols, ptr(Wq), b"8") == 0
+        xq = blocks(n_tok * nb)
+        for t in range(n_tok):
+            xt = np.ascontiguousarray(x[t * cols:(t + 1) * cols])
+            xb = blocks(nb)
+            L.quantize_row_q8(ptr(xt), ptr(xb), cols)
+            xq[t * nb:(t + 1) * nb] = xb
+        y = np.zeros(n_tok * rows, np.float32)
+        if n_tok == 1:
+            L.matmul_q8_scalar(ptr(Wq), ptr(xq), ptr(y), rows, cols)
+        else:
+            L.matmul_q8_scalar_batch(ptr(Wq), ptr(xq), ptr(y), rows, cols, n_tok)
+        data[f"in_sum_{i}"] = np.array([checksum(W), checksum(x)], np.int64)
+        data[f"packed_sum_{i}"] = np.array([checksum(Wq), checksum(xq)], np.int64)
+        data[f"y_{i}"] = y
+    np.savez_compressed(WEIGHTS_OUT, **data)
+    print(f"wrote {WEIGHTS_OUT} ({os.path.getsize(WEIGHTS_OUT)} bytes, {len(data)} arrays)")
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["weights"]:
+        weights()
+    else:
+        main()
