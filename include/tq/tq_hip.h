@@ -175,6 +175,52 @@ int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d
                          const float *d_k, const float *d_v, const float *d_cos,
                          const float *d_sin, float *d_out, void *stream);
 
+/* ---- the weight side: Q8 weight matrices and the projections -----------
+ *
+ * A weight matrix lives on the device in the "tiled Q8" layout, the same
+ * byte count as the reference's rows x cols/32 block_q8 array
+ * (packed_matrix_bytes, packer/packer.c:62-75):
+ *   codes  [rows][cols] int8; each row in groups of up to 64 blocks, a group
+ *          of n blocks holding the first 16 codes of each block (block order)
+ *          and then the last 16 codes of each;
+ *   scales [rows][cols/32] fp32 at byte offset rows*cols.
+ * Matrices and the output are device memory; every call is asynchronous on
+ * `stream` (hipStream_t as void*, NULL = the null stream).  cols must be a
+ * multiple of 32; W 16-byte aligned; block_q8 and fp32 arrays 4-byte
+ * aligned (16-byte aligned activations are copied in wider pieces).
+ */
+
+/* Bytes of a tiled rows x cols matrix (0 for a bad shape). */
+size_t tq_hip_q8_matrix_bytes(int rows, int cols);
+/* The reference's block_q8 rows (pack_matrix output, packer/packer.c:77-89,
+ * already on the device) -> tiled; and back (as unpack_matrix reads them,
+ * :91-103, the block_q8 bytes are restored exactly). */
+int tq_hip_q8_pack(void *dst, const block_q8 *src, int rows, int cols, void *stream);
+int tq_hip_q8_unpack(block_q8 *dst, const void *src, int rows, int cols, void *stream);
+
+/* y[r] = sum over blocks of (int dot of codes) * w.d * x.d: the Q8 MatmulFn
+ * (kernel/kernel.h:13, kernel/q8_scalar.c:15-22, kernel/q8_avx2.c:18-25). */
+int tq_hip_matmul_q8(const void *W, const block_q8 *xq, float *y, int rows, int cols, void *stream);
+/* n_tok activation rows xq[t*cols/32 ...] -> y[t*rows + r]: the Q8
+ * MatmulBatchFn (kernel/kernel.h:17-20, kernel/q8_scalar.c:25-30,
+ * kernel/avx2_util.h:26-66). */
+int tq_hip_matmul_q8_batch(const void *W, const block_q8 *xq, float *y, int rows, int cols,
+                           int n_tok, void *stream);
+
+/* project_qkv for n_tok rows of xn [n_tok][hidden] (model/attention_layer.c:38-46,
+ * batched :210-218): quantize_row_q8 of every row into xq_ws (n_tok*hidden/32
+ * block_q8, the reference's xn_q8 / ws->xq), then q = wq.xq, k = wk.xq,
+ * v = wv.xq in one launch over the concatenated rows; q [n_tok][q_rows],
+ * k and v [n_tok][kv_rows].  wq is q_rows x hidden, wk and wv kv_rows x hidden. */
+int tq_hip_project_qkv(const void *wq, const void *wk, const void *wv, int q_rows, int kv_rows,
+                       int hidden, const float *xn, int n_tok, block_q8 *xq_ws, float *q, float *k,
+                       float *v, void *stream);
+/* project_output (model/attention_layer.c:161-167, batched :238-241):
+ * quantize_row_q8 of attn [n_tok][cols] into xq_ws, then out = wo.xq,
+ * out [n_tok][rows]. */
+int tq_hip_project_output(const void *wo, int rows, int cols, const float *attn, int n_tok,
+                          block_q8 *xq_ws, float *out, void *stream);
+
 /* ---- measurement: streaming-read bandwidth of device memory, the GPU
  * counterpart of the reference's host RAM probe (tools/membw.h:1-80).  Reads
  * `bytes` (a multiple of 16) of `buf` once with 16-byte loads; `sink` (device,

@@ -1,0 +1,467 @@
+// gemv_q8.hip — the Q8 weight side of the attention layer on gfx950: the
+// weight x Q8-activation matmul (kernel/q8_scalar.c:3-30, kernel/kernel.h:13-20)
+// and the projections around attention that use it (project_qkv and
+// project_output, model/attention_layer.c:38-46,161-167, and their batched
+// forms, :210-218,238-241).
+//
+// Device weight layout ("tiled Q8"), exactly the byte count of the
+// reference's rows x cols/32 block_q8 array:
+//   codes  [rows][cols] int8.  A row is cut into groups of up to 64 blocks
+//          (2048 codes); a group of n blocks holds the first 16 codes of each
+//          of its n blocks (16 B per block, in block order), then the last 16
+//          codes of each.  Lane l of a wave reads block 64g+l of a row as two
+//          16-byte loads, each wave-wide load one contiguous 1 KiB.
+//   scales [rows][cols/32] fp32 at byte offset rows*cols, one coalesced
+//          dword per lane per group.
+// tq_hip_q8_pack turns the reference's block_q8 rows into this layout on the
+// device; tq_hip_q8_unpack turns it back.
+//
+// Matmul: the work is one pass over the weight bytes (HBM-bound).  A
+// 256-thread work-group runs 4 waves; a wave owns RW consecutive rows.  The
+// work-group first copies the activation rows (up to T tokens of block_q8,
+// the reference's activation format) straight into LDS with
+// global_load_lds_dwordx4, then every wave issues the loads of its first 8
+// (row, group) units, and only then waits: the copies, issued first, are
+// complete once no more than those 3*8 weight loads are outstanding, so the
+// activation copy hides under the weight latency.
+// Per block: int32 dot of the 32 code pairs (8 v_dot4_i32_i8), then
+// ((float)s * w_d) * x_d as the scalar reference rounds it; the per-lane sums
+// over groups and the 64-lane sum replace the reference's serial block-order
+// sum (the reference's own SIMD kernels reorder that sum as well).
+//
+// The projections (project_qkv: wq, wk and wv in one launch over their
+// concatenated rows; project_output) quantize their fp32 input rows with
+// quantize_row_q8 into a caller-provided block_q8 workspace first, as the
+// reference does into xn_q8 / ws->xq.
+#include "tq_common.hpp"
+
+#include <stdlib.h>
+
+namespace {
+
+using namespace tq;
+
+constexpr int kGemvWaves = 4;
+constexpr int kGroupBlocks = 64;
+constexpr int kGroupBytes = kGroupBlocks * kQK;   // 2048
+constexpr int kMaxSegs = 3;
+constexpr size_t kMaxStageBytes = 65536;          // activation rows in LDS per work-group
+
+int herr(hipError_t e) { return e == hipSuccess ? TQ_HIP_OK : TQ_HIP_EHIP_BASE - (int)e; }
+
+// Byte offset inside a tiled row of code j (0..31) of block b.
+__host__ __device__ __forceinline__ int tiled_offset(int nb, int b, int j) {
+    const int g = b / kGroupBlocks;
+    const int rest = nb - g * kGroupBlocks;
+    const int n = rest < kGroupBlocks ? rest : kGroupBlocks;
+    const int i = b - g * kGroupBlocks;
+    return g * kGroupBytes + (j < 16 ? 16 * i + j : 16 * n + 16 * i + (j - 16));
+}
+
+// ---------------------------------------------------------------------------
+// block_q8 rows <-> tiled layout.  One thread per block.
+__global__ __launch_bounds__(256) void pack_kernel(unsigned char *__restrict__ dst,
+                                                   const unsigned char *__restrict__ src,
+                                                   int rows, int nb) {
+    const long long k = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (k >= (long long)rows * nb) return;
+    const int r = (int)(k / nb), b = (int)(k - (long long)r * nb);
+    const uint32_t *blk = reinterpret_cast<const uint32_t *>(src + (size_t)k * kBlockBytes);
+    u32x4 lo, hi;
+    lo.x = blk[1]; lo.y = blk[2]; lo.z = blk[3]; lo.w = blk[4];
+    hi.x = blk[5]; hi.y = blk[6]; hi.z = blk[7]; hi.w = blk[8];
+    const int cols = nb * kQK;
+    unsigned char *row = dst + (size_t)r * cols;
+    *reinterpret_cast<u32x4 *>(row + tiled_offset(nb, b, 0)) = lo;
+    *reinterpret_cast<u32x4 *>(row + tiled_offset(nb, b, 16)) = hi;
+    reinterpret_cast<uint32_t *>(dst + (size_t)rows * cols)[k] = blk[0];
+}
+
+__global__ __launch_bounds__(256) void unpack_kernel(unsigned char *__restrict__ dst,
+                                                     const unsigned char *__restrict__ src,
+                                                     int rows, int nb) {
+    const long long k = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (k >= (long long)rows * nb) return;
+    const int r = (int)(k / nb), b = (int)(k - (long long)r * nb);
+    const int cols = nb * kQK;
+    const unsigned char *row = src + (size_t)r * cols;
+    const u32x4 lo = *reinterpret_cast<const u32x4 *>(row + tiled_offset(nb, b, 0));
+    const u32x4 hi = *reinterpret_cast<const u32x4 *>(row + tiled_offset(nb, b, 16));
+    uint32_t *blk = reinterpret_cast<uint32_t *>(dst + (size_t)k * kBlockBytes);
+    blk[0] = reinterpret_cast<const uint32_t *>(src + (size_t)rows * cols)[k];
+    blk[1] = lo.x; blk[2] = lo.y; blk[3] = lo.z; blk[4] = lo.w;
+    blk[5] = hi.x; blk[6] = hi.y; blk[7] = hi.z; blk[8] = hi.w;
+}
+
+// ---------------------------------------------------------------------------
+// Matmul over up to three row-concatenated matrices sharing one input
+// (project_qkv runs wq, wk and wv in one launch).
+
+struct GemvSeg {
+    const unsigned char *w;   // tiled matrix
+    float *y;                 // y[t * rows + r]
+    int rows;
+};
+
+struct GemvArgs {
+    GemvSeg seg[kMaxSegs];
+    int seg_end[kMaxSegs];    // cumulative row ends
+    int rows_total;
+    int cols, nb, ng;
+    const unsigned char *xq;  // block_q8 [n_tok][nb], 16-byte aligned
+    int n_tok;                // rows of input in this launch (<= T)
+};
+
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+
+// 16 bytes from each active lane's global address into LDS at dst + 16*lane
+// (global_load_lds_dwordx4; M0 holds the LDS byte address and is restored;
+// dst must be the same for the whole wave).
+// The memory clobber keeps every later load after it in program order, which
+// the vmcnt arithmetic below relies on.
+__device__ __forceinline__ void dma16(const void *src, unsigned char *dst) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8 *)dst);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(lds)
+        : "memory");
+}
+
+// Wait until at most N vector memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt immediate");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// 4 bytes from each active lane's global address into LDS at dst + 4*lane
+// (global_load_lds_dword).
+__device__ __forceinline__ void dma4(const void *src, unsigned char *dst) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_u8 *)dst);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\t"
+        "global_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(lds)
+        : "memory");
+}
+
+// Activation bytes (n_tok rows of nb block_q8) into LDS, all by DMA: whole
+// 16-byte chunks when the rows are 16-byte aligned, the last bytes (and
+// everything otherwise) as dwords.  The caller's wait_vm covers the copies.
+__device__ __forceinline__ void stage_x(const GemvArgs &a, unsigned char *xs) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int bytes = a.n_tok * a.nb * kBlockBytes;
+    const int chunks = ((uintptr_t)a.xq & 15) ? 0 : bytes >> 4;
+    for (int c0 = wave * 64; c0 < chunks; c0 += kThreads) {
+        if (c0 + lane < chunks) dma16(a.xq + 16 * (c0 + lane), xs + 16 * c0);
+    }
+    const int words = (bytes - (chunks << 4)) >> 2;
+    const int base = chunks << 4;
+    for (int w0 = wave * 64; w0 < words; w0 += kThreads) {
+        if (w0 + lane < words) dma4(a.xq + base + 4 * (w0 + lane), xs + base + 4 * w0);
+    }
+}
+
+// Every load is unconditional (rows past the end and groups past the last
+// one are clamped to real data and masked out of the sums), so no load
+// result is left unread on any path and the compiler never has to wait for
+// one in-flight load before issuing the next.
+template <int T, int RW, int GC>
+__global__ __launch_bounds__(256) void gemv_q8_kernel(GemvArgs a) {
+#pragma clang fp contract(off)
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * kGemvWaves + wave) * RW;
+    const int cols = a.cols, nb = a.nb, ng = a.ng;
+    unsigned char *xs = smem;   // [T][nb] block_q8, as in global memory
+    stage_x(a, xs);
+
+    const unsigned char *wrow[RW];
+    const float *drow[RW];
+    float *yrow[RW];
+    int ldy[RW];
+#pragma unroll
+    for (int i = 0; i < RW; i++) {
+        const int r = row0 + i < a.rows_total ? row0 + i : a.rows_total - 1;
+        // Field-wise selects keep the segment in scalar registers (an indexed
+        // a.seg[s] would be a vector load of the kernel arguments).
+        const bool s0 = r < a.seg_end[0], s1 = !s0 && r < a.seg_end[1];
+        const unsigned char *w = s0 ? a.seg[0].w : (s1 ? a.seg[1].w : a.seg[2].w);
+        float *y = s0 ? a.seg[0].y : (s1 ? a.seg[1].y : a.seg[2].y);
+        const int rows = s0 ? a.seg[0].rows : (s1 ? a.seg[1].rows : a.seg[2].rows);
+        const int lr = r - (s0 ? 0 : (s1 ? a.seg_end[0] : a.seg_end[1]));
+        wrow[i] = w + (size_t)lr * cols;
+        drow[i] = reinterpret_cast<const float *>(w + (size_t)rows * cols) + (size_t)lr * nb;
+        yrow[i] = y + lr;
+        ldy[i] = rows;
+    }
+
+    float acc[RW][T];
+#pragma unroll
+    for (int i = 0; i < RW; i++)
+#pragma unroll
+        for (int t = 0; t < T; t++) acc[i][t] = 0.0f;
+
+    for (int g0 = 0; g0 < ng; g0 += GC) {
+        u32x4 wlo[GC][RW], whi[GC][RW];
+        float wd[GC][RW];
+#pragma unroll
+        for (int u = 0; u < GC; u++) {
+            const int g = g0 + u < ng ? g0 + u : ng - 1;
+            const int rest = nb - g * kGroupBlocks;
+            const int n = rest < kGroupBlocks ? rest : kGroupBlocks;
+            const int bl = lane < n ? lane : n - 1;
+#pragma unroll
+            for (int i = 0; i < RW; i++) {
+                const unsigned char *p = wrow[i] + g * kGroupBytes + 16 * bl;
+                wlo[u][i] = *reinterpret_cast<const u32x4 *>(p);
+                whi[u][i] = *reinterpret_cast<const u32x4 *>(p + 16 * n);
+                wd[u][i] = drow[i][g * kGroupBlocks + bl];
+            }
+        }
+        if (g0 == 0) {
+            wait_vm<3 * GC * RW>();   // the activation copies, issued first, have landed
+            __syncthreads();
+        }
+#pragma unroll
+        for (int u = 0; u < GC; u++) {
+            const int g = g0 + u < ng ? g0 + u : ng - 1;
+            const int rest = nb - g * kGroupBlocks;
+            const int n = rest < kGroupBlocks ? rest : kGroupBlocks;
+            const bool valid = lane < n && g0 + u < ng;
+            const int bl = lane < n ? lane : n - 1;
+            int s[T][RW];
+            float xd[T];
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                // Block 64g+bl of token t: d, then 8 dwords of codes (a 36-byte
+                // lane stride is 9 banks apart: conflict-free).
+                const uint32_t *xb = reinterpret_cast<const uint32_t *>(
+                    xs + (size_t)(t * nb + g * kGroupBlocks + bl) * kBlockBytes);
+                xd[t] = __uint_as_float(xb[0]);
+#pragma unroll
+                for (int i = 0; i < RW; i++) {
+                    int d = 0;
+                    d = __builtin_amdgcn_sdot4(wlo[u][i].x, xb[1], d, false);
+                    d = __builtin_amdgcn_sdot4(wlo[u][i].y, xb[2], d, false);
+                    d = __builtin_amdgcn_sdot4(wlo[u][i].z, xb[3], d, false);
+                    d = __builtin_amdgcn_sdot4(wlo[u][i].w, xb[4], d, false);
+                    d = __builtin_amdgcn_sdot4(whi[u][i].x, xb[5], d, false);
+                    d = __builtin_amdgcn_sdot4(whi[u][i].y, xb[6], d, false);
+                    d = __builtin_amdgcn_sdot4(whi[u][i].z, xb[7], d, false);
+                    d = __builtin_amdgcn_sdot4(whi[u][i].w, xb[8], d, false);
+                    s[t][i] = d;
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < T; t++)
+#pragma unroll
+                for (int i = 0; i < RW; i++) {
+                    const float p = ((float)s[t][i] * wd[u][i]) * xd[t];
+                    acc[i][t] += valid ? p : 0.0f;
+                }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < RW; i++) {
+        if (row0 + i >= a.rows_total) continue;
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            if (t < a.n_tok) {
+                const float v = wave_sum(acc[i][t]);
+                if (lane == 0) yrow[i][(size_t)t * ldy[i]] = v;
+            }
+        }
+    }
+}
+
+int env_int(const char *name, int dflt) {
+    const char *s = getenv(name);
+    return (s && *s) ? atoi(s) : dflt;
+}
+
+// Rows per wave: enough work-groups to put two on every CU where the row
+// count allows (TQ_HIP_GEMV_RW=1|2|4 overrides).
+int pick_rw(int rows_total) {
+    const int forced = env_int("TQ_HIP_GEMV_RW", 0);
+    if (forced == 1 || forced == 2 || forced == 4) return forced;
+    if (rows_total >= 4 * kGemvWaves * 512) return 4;
+    if (rows_total >= 2 * kGemvWaves * 512) return 2;
+    return 1;
+}
+
+// Groups per row per pass: up to 8 (row, group) units in flight per wave,
+// never more groups than a row has.
+int pick_gc(int ng, int rw) {
+    int gc = 8 / rw;
+    if (gc > 4) gc = 4;
+    while (gc > 1 && gc / 2 >= ng) gc /= 2;
+    return gc;
+}
+
+// Largest token count per launch whose staged rows fit the LDS budget.
+int pick_tokens(int nb) {
+    for (int t : {8, 4, 2, 1})
+        if ((size_t)t * nb * kBlockBytes <= kMaxStageBytes) return t;
+    return 0;
+}
+
+template <int T, int RW, int GC>
+hipError_t launch_t(const GemvArgs &a, hipStream_t s) {
+    const int waves = (a.rows_total + RW - 1) / RW;
+    const int grid = (waves + kGemvWaves - 1) / kGemvWaves;
+    const size_t lds = ((size_t)T * a.nb * kBlockBytes + 15) & ~(size_t)15;
+    hipLaunchKernelGGL((gemv_q8_kernel<T, RW, GC>), dim3(grid), dim3(kThreads), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int RW, int GC>
+hipError_t launch_tok(const GemvArgs &a, int tmax, hipStream_t s) {
+    switch (tmax) {
+        case 8: return launch_t<8, RW, GC>(a, s);
+        case 4: return launch_t<4, RW, GC>(a, s);
+        case 2: return launch_t<2, RW, GC>(a, s);
+        default: return launch_t<1, RW, GC>(a, s);
+    }
+}
+
+hipError_t launch_gemv(const GemvArgs &a, int tcap, int rw, int gc, hipStream_t s) {
+    switch (rw * 16 + gc) {
+        case 0x11: return launch_tok<1, 1>(a, tcap, s);
+        case 0x12: return launch_tok<1, 2>(a, tcap, s);
+        case 0x14: return launch_tok<1, 4>(a, tcap, s);
+        case 0x21: return launch_tok<2, 1>(a, tcap, s);
+        case 0x22: return launch_tok<2, 2>(a, tcap, s);
+        case 0x24: return launch_tok<2, 4>(a, tcap, s);
+        case 0x41: return launch_tok<4, 1>(a, tcap, s);
+        default: return launch_tok<4, 2>(a, tcap, s);
+    }
+}
+
+// Runs the matmul over all tokens, in launches of up to tmax tokens.
+int run_gemv(GemvArgs a, int n_tok, hipStream_t s) {
+    const int tmax = pick_tokens(a.nb);
+    if (tmax == 0) return TQ_HIP_EINVAL;
+    const int rw = pick_rw(a.rows_total);
+    const int gc = pick_gc(a.ng, rw);
+    const unsigned char *xq0 = a.xq;
+    GemvSeg seg0[kMaxSegs];
+    for (int i = 0; i < kMaxSegs; i++) seg0[i] = a.seg[i];
+    for (int t0 = 0; t0 < n_tok; t0 += tmax) {
+        const int nt = n_tok - t0 < tmax ? n_tok - t0 : tmax;
+        int tcap = 1;
+        while (tcap < nt) tcap *= 2;
+        a.n_tok = nt;
+        a.xq = xq0 + (size_t)t0 * a.nb * kBlockBytes;
+        for (int i = 0; i < kMaxSegs; i++)
+            a.seg[i].y = seg0[i].y ? seg0[i].y + (size_t)t0 * seg0[i].rows : nullptr;
+        const hipError_t e = launch_gemv(a, tcap, rw, gc, s);
+        if (e != hipSuccess) return herr(e);
+    }
+    return TQ_HIP_OK;
+}
+
+bool aligned(const void *p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+bool shape_ok(int rows, int cols) { return rows > 0 && cols > 0 && cols % kQK == 0; }
+
+void init_args(GemvArgs &a, int cols) {
+    a = GemvArgs{};
+    a.cols = cols;
+    a.nb = cols / kQK;
+    a.ng = (a.nb + kGroupBlocks - 1) / kGroupBlocks;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t tq_hip_q8_matrix_bytes(int rows, int cols) {
+    if (!shape_ok(rows, cols)) return 0;
+    return (size_t)rows * (size_t)(cols / kQK) * kBlockBytes;
+}
+
+int tq_hip_q8_pack(void *dst, const block_q8 *src, int rows, int cols, void *stream) {
+    if (!shape_ok(rows, cols) || !dst || !src || !aligned(dst, 16) || !aligned(src, 4))
+        return TQ_HIP_EINVAL;
+    const long long n = (long long)rows * (cols / kQK);
+    hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (unsigned char *)dst, (const unsigned char *)src, rows, cols / kQK);
+    return herr(hipGetLastError());
+}
+
+int tq_hip_q8_unpack(block_q8 *dst, const void *src, int rows, int cols, void *stream) {
+    if (!shape_ok(rows, cols) || !dst || !src || !aligned(src, 16) || !aligned(dst, 4))
+        return TQ_HIP_EINVAL;
+    const long long n = (long long)rows * (cols / kQK);
+    hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (unsigned char *)dst, (const unsigned char *)src, rows, cols / kQK);
+    return herr(hipGetLastError());
+}
+
+int tq_hip_matmul_q8_batch(const void *W, const block_q8 *xq, float *y, int rows, int cols, int n_tok,
+                           void *stream) {
+    if (!shape_ok(rows, cols) || n_tok <= 0 || !W || !xq || !y || !aligned(W, 16) || !aligned(xq, 4) ||
+        !aligned(y, 4))
+        return TQ_HIP_EINVAL;
+    GemvArgs a;
+    init_args(a, cols);
+    a.seg[0] = GemvSeg{(const unsigned char *)W, y, rows};
+    a.seg_end[0] = a.seg_end[1] = a.seg_end[2] = rows;
+    a.rows_total = rows;
+    a.xq = (const unsigned char *)xq;
+    return run_gemv(a, n_tok, (hipStream_t)stream);
+}
+
+int tq_hip_matmul_q8(const void *W, const block_q8 *xq, float *y, int rows, int cols, void *stream) {
+    return tq_hip_matmul_q8_batch(W, xq, y, rows, cols, 1, stream);
+}
+
+int tq_hip_project_qkv(const void *wq, const void *wk, const void *wv, int q_rows, int kv_rows,
+                       int hidden, const float *xn, int n_tok, block_q8 *xq_ws, float *q, float *k,
+                       float *v, void *stream) {
+    if (!shape_ok(q_rows, hidden) || kv_rows <= 0 || n_tok <= 0 || !wq || !wk || !wv || !xn ||
+        !xq_ws || !q || !k || !v || !aligned(wq, 16) || !aligned(wk, 16) || !aligned(wv, 16) ||
+        !aligned(xn, 4) || !aligned(xq_ws, 4) || !aligned(q, 4) || !aligned(k, 4) || !aligned(v, 4))
+        return TQ_HIP_EINVAL;
+    const hipStream_t s = (hipStream_t)stream;
+    const hipError_t e = tq_launch_quantize(xn, xq_ws, n_tok * hidden, s);
+    if (e != hipSuccess) return herr(e);
+    GemvArgs a;
+    init_args(a, hidden);
+    a.seg[0] = GemvSeg{(const unsigned char *)wq, q, q_rows};
+    a.seg[1] = GemvSeg{(const unsigned char *)wk, k, kv_rows};
+    a.seg[2] = GemvSeg{(const unsigned char *)wv, v, kv_rows};
+    a.seg_end[0] = q_rows;
+    a.seg_end[1] = q_rows + kv_rows;
+    a.seg_end[2] = q_rows + 2 * kv_rows;
+    a.rows_total = a.seg_end[2];
+    a.xq = (const unsigned char *)xq_ws;
+    return run_gemv(a, n_tok, s);
+}
+
+int tq_hip_project_output(const void *wo, int rows, int cols, const float *attn, int n_tok,
+                          block_q8 *xq_ws, float *out, void *stream) {
+    if (!shape_ok(rows, cols) || n_tok <= 0 || !wo || !attn || !xq_ws || !out || !aligned(wo, 16) ||
+        !aligned(attn, 4) || !aligned(xq_ws, 4) || !aligned(out, 4))
+        return TQ_HIP_EINVAL;
+    const hipStream_t s = (hipStream_t)stream;
+    const hipError_t e = tq_launch_quantize(attn, xq_ws, n_tok * cols, s);
+    if (e != hipSuccess) return herr(e);
+    GemvArgs a;
+    init_args(a, cols);
+    a.seg[0] = GemvSeg{(const unsigned char *)wo, out, rows};
+    a.seg_end[0] = a.seg_end[1] = a.seg_end[2] = rows;
+    a.rows_total = rows;
+    a.xq = (const unsigned char *)xq_ws;
+    return run_gemv(a, n_tok, s);
+}
+
+}  // extern "C"

@@ -58,6 +58,22 @@ def test_host_validation_without_device(lib):
     assert lib.tq_hip_membw_read(None, 1 << 20, None, 0, None) == native.EINVAL
     assert lib.tq_hip_membw_read(C.c_void_p(16), 100, C.c_void_p(16), 0, None) == native.EINVAL   # not whole 16 B
     assert lib.tq_hip_membw_sink_bytes() > 0
+    # weight side: shapes, nulls and alignment are refused before any device call
+    assert lib.tq_hip_q8_matrix_bytes(4096, 4096) == 4096 * 128 * 36
+    assert lib.tq_hip_q8_matrix_bytes(7, 48) == 0 and lib.tq_hip_q8_matrix_bytes(0, 64) == 0
+    p16 = C.c_void_p(4096)
+    assert lib.tq_hip_q8_pack(p16, p16, 4, 48, None) == native.EINVAL
+    assert lib.tq_hip_q8_pack(C.c_void_p(4100), p16, 4, 64, None) == native.EINVAL   # dst not 16 B aligned
+    assert lib.tq_hip_q8_unpack(None, p16, 4, 64, None) == native.EINVAL
+    assert lib.tq_hip_matmul_q8(p16, p16, p16, 0, 64, None) == native.EINVAL
+    assert lib.tq_hip_matmul_q8(p16, p16, p16, 4, 33, None) == native.EINVAL
+    assert lib.tq_hip_matmul_q8(C.c_void_p(4104), p16, p16, 4, 64, None) == native.EINVAL
+    assert lib.tq_hip_matmul_q8_batch(p16, p16, p16, 4, 64, 0, None) == native.EINVAL
+    assert lib.tq_hip_matmul_q8_batch(p16, None, p16, 4, 64, 1, None) == native.EINVAL
+    assert lib.tq_hip_project_qkv(p16, p16, p16, 64, 16, 64, p16, 1, None, p16, p16, p16, None) == native.EINVAL
+    assert lib.tq_hip_project_qkv(p16, p16, p16, 64, 0, 64, p16, 1, p16, p16, p16, p16, None) == native.EINVAL
+    assert lib.tq_hip_project_output(p16, 64, 48, p16, 1, p16, p16, None) == native.EINVAL
+    assert lib.tq_hip_project_output(p16, 64, 64, p16, 0, p16, p16, None) == native.EINVAL
     for code, text in ((0, "ok"), (-1, "argument out of range"), (-3, "unsupported head_dim or group size")):
         assert native.strerror(code) == text
 
