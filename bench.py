@@ -21,8 +21,10 @@ of the same workload and checks the GPU output of layer 0 against them.
 
 Other workloads: --config decode-batched (64 sequences, ragged 512..8192,
 paged), decode-70b-32k (64q/8kv, batch 16, context 32768, 1 % outliers),
-prefill-2k (causal prefill of 2048 tokens).  They print the same JSON fields
-for their own shape.
+prefill-2k (causal prefill of 2048 tokens), project-8b / project-70b (the Q8
+weight GEMVs either side of attention for one token: project_qkv and
+project_output, 32 layers' weights rotated).  They print the same JSON
+fields for their own shape.
 
 --copy-calibration BYTES runs one device-to-device copy of BYTES first: its
 FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc give the counters' scale.
@@ -525,13 +527,200 @@ def bench_prefill_2k(args, nat, hip):
     }
 
 
+# ---------------------------------------------------------------------------
+# the weight side: project_qkv + project_output of one decode token
+
+def random_q8_weights(rng, rows: int, cols: int) -> np.ndarray:
+    """block_q8 rows with codes uniform in [-127, 127] and scales in [5e-4, 2e-3]."""
+    from oracle.binding import blocks
+    w = blocks(rows * (cols // QK))
+    w["q"] = rng.integers(-127, 128, size=w["q"].shape, dtype=np.int8)
+    w["d"] = rng.uniform(5e-4, 2e-3, size=w["d"].shape).astype(np.float32)
+    return w
+
+
+def rel_l2(a, b) -> float:
+    """tools/test_kernel.c:22-30."""
+    a = np.asarray(a, np.float64).reshape(-1)
+    b = np.asarray(b, np.float64).reshape(-1)
+    den = float((b * b).sum())
+    num = float(((a - b) ** 2).sum())
+    return float(np.sqrt(num / den)) if den > 0 else float(np.sqrt(num))
+
+
+def cpu_leg_project(shape, host_w, xn, attn, budget_s: float):
+    """The reference's own quantize_row_q8 + matmul_q8_avx2 (OpenMP over rows) on
+    host copies of the projections, rotating 32 layers of weights (1.5 GB at the 8B
+    shape, beyond any host L3)."""
+    from oracle.binding import Oracle, Ref, blocks, ptr
+    nq, nkv, hd, hidden = shape
+    qr, kr = nq * hd, nkv * hd
+    if Ref.available():
+        kind, lib = "reference", Ref().lib
+        quant, mm, isa = lib.quantize_row_q8, lib.matmul_q8_avx2, Ref().isa()
+    else:
+        kind, lib = "port", Oracle().lib
+        quant, mm, isa = lib.oracle_quantize_row_q8, lib.oracle_matmul_q8, "scalar"
+    layers = 32
+    ws = [tuple(w.copy() for w in host_w) for _ in range(layers)]
+    xq = blocks(max(hidden, qr) // QK)
+    q, k, v, out = (np.zeros(qr, np.float32), np.zeros(kr, np.float32), np.zeros(kr, np.float32),
+                    np.zeros(hidden, np.float32))
+
+    def step(l):
+        wq, wk, wv, wo = ws[l]
+        quant(ptr(xn), ptr(xq), hidden)
+        mm(ptr(wq), ptr(xq), ptr(q), qr, hidden)
+        mm(ptr(wk), ptr(xq), ptr(k), kr, hidden)
+        mm(ptr(wv), ptr(xq), ptr(v), kr, hidden)
+        quant(ptr(attn), ptr(xq), qr)
+        mm(ptr(wo), ptr(xq), ptr(out), hidden, qr)
+
+    for l in range(2):
+        step(l)
+    times = []
+    t_start = time.perf_counter()
+    i = 0
+    while (time.perf_counter() - t_start < budget_s and i < 100000) or i < 5:
+        t0 = time.perf_counter()
+        step(i % layers)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    med = float(np.median(times))
+    wbytes = sum(w.nbytes for w in host_w)
+    omp = int(os.environ.get("OMP_NUM_THREADS", str(os.cpu_count() or 1)))
+    cores = min(omp, os.cpu_count() or 1) if kind == "reference" else 1
+    return {"value": wbytes / med / 1e9, "unit": "GB/s", "cores": cores, "kind": kind,
+            "sample": (f"{len(times)} single-token projection steps (quantize_row_q8 + 3 matmuls, quantize_row_q8 "
+                       f"+ wo matmul, {wbytes / 1e6:.1f} MB of weights) rotating {layers} host layers, median "
+                       f"{med * 1e3:.3f} ms; {isa} kernels, OpenMP over rows (OMP_NUM_THREADS={omp}, "
+                       f"nproc={os.cpu_count()})")}
+
+
+def bench_project(args, nat, hip, *, shape, name):
+    """project_qkv + project_output for one token, weights of `layers` layers rotated."""
+    from oracle.binding import Oracle
+    lib = nat.load()
+    nq, nkv, hd, hidden = shape
+    qr, kr = nq * hd, nkv * hd
+    layers = args.layers
+    rng = np.random.default_rng(11)
+    host_w = (random_q8_weights(rng, qr, hidden), random_q8_weights(rng, kr, hidden),
+              random_q8_weights(rng, kr, hidden), random_q8_weights(rng, hidden, qr))
+    dims = ((qr, hidden), (kr, hidden), (kr, hidden), (hidden, qr))
+    nbytes = [lib.tq_hip_q8_matrix_bytes(r, c) for r, c in dims]
+    layer_bytes = sum(nbytes)
+    big = nat.DeviceBuffer(layers * layer_bytes)
+    off = [0, nbytes[0], nbytes[0] + nbytes[1], nbytes[0] + nbytes[1] + nbytes[2]]
+    for w, (r, c), o in zip(host_w, dims, off):
+        src = nat.DeviceBuffer.from_numpy(w)
+        nat.check(lib.tq_hip_q8_pack(big.ptr + o, src.ptr, r, c, None), "q8_pack")
+        src.free()
+    hip.sync()
+    for l in range(1, layers):
+        nat.check(lib.tq_hip_memcpy_d2d(big.ptr + l * layer_bytes, big.ptr, layer_bytes, None), "d2d")
+    hip.sync()
+    xn = rng.standard_normal(hidden, dtype=np.float32)
+    attn = rng.standard_normal(qr, dtype=np.float32)
+    D = nat.DeviceBuffer.from_numpy
+    dxn, dattn = D(xn), D(attn)
+    ws = nat.DeviceBuffer(max(hidden, qr) // QK * BLOCK_BYTES)
+    dq, dk, dv, dout = (nat.DeviceBuffer(qr * 4), nat.DeviceBuffer(kr * 4), nat.DeviceBuffer(kr * 4),
+                        nat.DeviceBuffer(hidden * 4))
+    stream = C.c_void_p()
+    hip.lib.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
+    hip.ok(hip.lib.hipStreamCreate(C.byref(stream)), "hipStreamCreate")
+    st = stream.value
+
+    def qkv(l):
+        b = big.ptr + l * layer_bytes
+        nat.check(lib.tq_hip_project_qkv(b, b + off[1], b + off[2], qr, kr, hidden, dxn.ptr, 1, ws.ptr,
+                                         dq.ptr, dk.ptr, dv.ptr, st), "project_qkv")
+
+    def wo(l):
+        b = big.ptr + l * layer_bytes
+        nat.check(lib.tq_hip_project_output(b + off[3], hidden, qr, dattn.ptr, 1, ws.ptr, dout.ptr, st),
+                  "project_output")
+
+    for i in range(max(args.warmup, layers)):
+        qkv(i % layers)
+        wo(i % layers)
+    hip.sync()
+    # parity of layer 0 against the oracle (kernel/q8_scalar.c restated)
+    oracle = Oracle()
+    qkv(0)
+    wo(0)
+    hip.sync()
+    got = [dq.download((qr,), np.float32), dk.download((kr,), np.float32), dv.download((kr,), np.float32),
+           dout.download((hidden,), np.float32)]
+    refs = [oracle.project_q8(host_w[0], qr, hidden, xn)[0], oracle.project_q8(host_w[1], kr, hidden, xn)[0],
+            oracle.project_q8(host_w[2], kr, hidden, xn)[0], oracle.project_q8(host_w[3], hidden, qr, attn)[0]]
+    errs = [rel_l2(g, r) for g, r in zip(got, refs)]
+    parity = {"ok": bool(max(errs) <= 1e-5), "rel_l2_err": max(errs),
+              "bar": "relative L2 error <= 1e-5 (tools/test_kernel.c:15)", "against": "oracle (scalar) on layer 0"}
+
+    g_qkv, _ = hip.capture(st, lambda: [qkv(l) for l in range(layers)])
+    g_wo, _ = hip.capture(st, lambda: [wo(l) for l in range(layers)])
+    g_step, _ = hip.capture(st, lambda: [(qkv(l), wo(l)) for l in range(layers)])
+    for g in (g_qkv, g_wo, g_step):
+        hip.launch_graph(g, st)
+    hip.sync()
+    reps = max(3, args.steps // layers)
+    ms_qkv = timed(hip, st, reps, lambda: hip.launch_graph(g_qkv, st)) / layers
+    ms_wo = timed(hip, st, reps, lambda: hip.launch_graph(g_wo, st)) / layers
+    ms_step = timed(hip, st, reps, lambda: hip.launch_graph(g_step, st)) / layers
+    hip.sync()
+    qkv_bytes = nbytes[0] + nbytes[1] + nbytes[2] + hidden * 4 + (qr + 2 * kr) * 4 + hidden // QK * BLOCK_BYTES
+    wo_bytes = nbytes[3] + qr * 4 + hidden * 4 + qr // QK * BLOCK_BYTES
+    achieved = qkv_bytes / (ms_qkv * 1e-3) / 1e9
+    # the launch shape the library picks for project_qkv (rows per wave, groups per pass)
+    rows_total, ng = qr + 2 * kr, (hidden // QK + 63) // 64
+    rw = 4 if rows_total >= 8192 else (2 if rows_total >= 4096 else 1)
+    gc = min(4, 8 // rw)
+    while gc > 1 and gc // 2 >= ng:
+        gc //= 2
+    line = {
+        "metric": f"Q8 projection GEMV (project_qkv + project_output) weight GB/s at {name} shape, batch 1, 1 GPU",
+        "value": layer_bytes / (ms_step * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1, "steps": reps * layers,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": (f"project_qkv ({qr}+{kr}+{kr} rows) + project_output ({hidden} rows) x "
+                                f"{hidden if hidden == qr else f'{hidden}/{qr}'} cols, Q8 weights, one token, "
+                                f"{layers} layers' weights rotated ({layers * layer_bytes / 1e6:.0f} MB), HIP graph "
+                                f"of {layers} steps"),
+                   "n_q_heads": nq, "n_kv_heads": nkv, "head_dim": hd, "hidden": hidden,
+                   "weight_bytes_per_step": layer_bytes, "layers_rotated": layers},
+        "us_project_qkv": ms_qkv * 1e3, "us_project_output": ms_wo * 1e3, "us_step": ms_step * 1e3,
+        "projection_tokens_per_s_32_layers": 1e3 / ms_step / 32,
+        "parity": parity,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": measured_traffic(f"project_{name}_qkv_pmc.txt"),
+                     "kernel": f"gemv_q8_kernel<1, {rw}, {gc}, true> (project_qkv: fused quantize + 3 matrices)",
+                     "kernel_ms": ms_qkv, "algorithmic_bytes": qkv_bytes},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_leg_project(shape, host_w, xn, attn, args.cpu_budget)
+    big.free()
+    return line
+
+
+def bench_project_8b(args, nat, hip):
+    return bench_project(args, nat, hip, shape=(32, 8, 128, 4096), name="8b")
+
+
+def bench_project_70b(args, nat, hip):
+    return bench_project(args, nat, hip, shape=(64, 8, 128, 8192), name="70b")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3200)
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--config", default="decode-8b-4k",
-                    choices=["decode-8b-4k", "decode-batched", "prefill-2k", "decode-70b-32k"])
+                    choices=["decode-8b-4k", "decode-batched", "prefill-2k", "decode-70b-32k", "project-8b",
+                             "project-70b"])
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
@@ -555,8 +744,9 @@ def main():
             line["parity"] = parity
     else:
         line = {"decode-batched": bench_decode_batched, "prefill-2k": bench_prefill_2k,
-                "decode-70b-32k": bench_decode_70b}[args.config](args, nat, hip)
-    if args.config.startswith("decode"):
+                "decode-70b-32k": bench_decode_70b, "project-8b": bench_project_8b,
+                "project-70b": bench_project_70b}[args.config](args, nat, hip)
+    if args.config.startswith(("decode", "project")):
         # the achievable read rate of this box, beside the 8 TB/s spec peak
         peak = measure_hbm_read(nat, hip)
         line["roofline"]["measured_peak"] = peak

@@ -30,9 +30,12 @@
 // sum (the reference's own SIMD kernels reorder that sum as well).
 //
 // The projections (project_qkv: wq, wk and wv in one launch over their
-// concatenated rows; project_output) quantize their fp32 input rows with
-// quantize_row_q8 into a caller-provided block_q8 workspace first, as the
-// reference does into xn_q8 / ws->xq.
+// concatenated rows; project_output) take fp32 input rows.  For one or two
+// rows the matmul launch copies them into LDS and quantizes them there
+// (bit-exact quantize_row_q8), and work-group 0 leaves the blocks in the
+// caller's workspace; for more rows quantize_row_q8 runs into the workspace
+// first, as the reference quantizes into xn_q8 / ws->xq, and the matmul
+// reads the blocks from there.
 #include "tq_common.hpp"
 
 #include <stdlib.h>
@@ -45,7 +48,10 @@ constexpr int kGemvWaves = 4;
 constexpr int kGroupBlocks = 64;
 constexpr int kGroupBytes = kGroupBlocks * kQK;   // 2048
 constexpr int kMaxSegs = 3;
-constexpr size_t kMaxStageBytes = 65536;          // activation rows in LDS per work-group
+// Activation rows in LDS per work-group: 8 rows of 8192 (73,728 bytes) fit,
+// two work-groups per CU's 160 KiB.
+constexpr size_t kMaxStageBytes = 80 * 1024;
+constexpr size_t kDefaultLdsLimit = 64 * 1024;    // beyond this a kernel must opt in
 
 int herr(hipError_t e) { return e == hipSuccess ? TQ_HIP_OK : TQ_HIP_EHIP_BASE - (int)e; }
 
@@ -108,7 +114,9 @@ struct GemvArgs {
     int seg_end[kMaxSegs];    // cumulative row ends
     int rows_total;
     int cols, nb, ng;
-    const unsigned char *xq;  // block_q8 [n_tok][nb], 16-byte aligned
+    const unsigned char *xq;  // block_q8 [n_tok][nb] (when x is null)
+    const float *x;           // fp32 [n_tok][cols], 16-byte aligned, quantized in LDS
+    unsigned char *xq_out;    // where work-group 0 leaves quantize_row_q8(x), or null
     int n_tok;                // rows of input in this launch (<= T)
 };
 
@@ -150,20 +158,40 @@ __device__ __forceinline__ void dma4(const void *src, unsigned char *dst) {
         : "memory");
 }
 
-// Activation bytes (n_tok rows of nb block_q8) into LDS, all by DMA: whole
-// 16-byte chunks when the rows are 16-byte aligned, the last bytes (and
-// everything otherwise) as dwords.  The caller's wait_vm covers the copies.
-__device__ __forceinline__ void stage_x(const GemvArgs &a, unsigned char *xs) {
+// `bytes` (a multiple of 4) from src into LDS at dst, all by DMA: whole
+// 16-byte chunks when src is 16-byte aligned, the rest (and everything
+// otherwise) as dwords.  The caller's wait_vm covers the copies.
+__device__ __forceinline__ void stage_bytes(const unsigned char *src, int bytes, unsigned char *dst) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int bytes = a.n_tok * a.nb * kBlockBytes;
-    const int chunks = ((uintptr_t)a.xq & 15) ? 0 : bytes >> 4;
+    const int chunks = ((uintptr_t)src & 15) ? 0 : bytes >> 4;
     for (int c0 = wave * 64; c0 < chunks; c0 += kThreads) {
-        if (c0 + lane < chunks) dma16(a.xq + 16 * (c0 + lane), xs + 16 * c0);
+        if (c0 + lane < chunks) dma16(src + 16 * (c0 + lane), dst + 16 * c0);
     }
     const int words = (bytes - (chunks << 4)) >> 2;
     const int base = chunks << 4;
     for (int w0 = wave * 64; w0 < words; w0 += kThreads) {
-        if (w0 + lane < words) dma4(a.xq + base + 4 * (w0 + lane), xs + base + 4 * w0);
+        if (w0 + lane < words) dma4(src + base + 4 * (w0 + lane), dst + base + 4 * w0);
+    }
+}
+
+// quantize_row_q8 (kernel/quant_x.c:12-33) of the n_tok fp32 rows staged at
+// xf into block_q8 rows at xs: 8 lanes x 4 values per block.  The task count
+// and the stride are multiples of 8, so a block's 8 lanes are active
+// together.  Work-group 0 also leaves the blocks at a.xq_out.
+__device__ __forceinline__ void quantize_lds(const GemvArgs &a, const unsigned char *xf, unsigned char *xs) {
+    const int blocks = a.n_tok * a.nb;
+    for (int k = threadIdx.x; k < blocks * 8; k += kThreads) {
+        const int e = k & 7, tb = k >> 3;
+        const float4 v = *reinterpret_cast<const float4 *>(xf + (size_t)(tb * kQK + 4 * e) * 4);
+        const float xv[4] = {v.x, v.y, v.z, v.w};
+        unsigned char *blk = xs + (size_t)tb * kBlockBytes;
+        quantize8x4(xv, reinterpret_cast<float *>(blk), blk + 4 + 4 * e, e == 0);
+    }
+    if (a.xq_out && blockIdx.x == 0) {
+        __syncthreads();
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(xs);
+        uint32_t *dst = reinterpret_cast<uint32_t *>(a.xq_out);
+        for (int w = threadIdx.x; w < blocks * (kBlockBytes / 4); w += kThreads) dst[w] = src[w];
     }
 }
 
@@ -171,7 +199,8 @@ __device__ __forceinline__ void stage_x(const GemvArgs &a, unsigned char *xs) {
 // one are clamped to real data and masked out of the sums), so no load
 // result is left unread on any path and the compiler never has to wait for
 // one in-flight load before issuing the next.
-template <int T, int RW, int GC>
+// XF: the input is fp32 rows, staged raw and quantized in LDS (T <= 2).
+template <int T, int RW, int GC, bool XF>
 __global__ __launch_bounds__(256) void gemv_q8_kernel(GemvArgs a) {
 #pragma clang fp contract(off)
     extern __shared__ __align__(16) unsigned char smem[];
@@ -179,8 +208,11 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(GemvArgs a) {
     const int wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * kGemvWaves + wave) * RW;
     const int cols = a.cols, nb = a.nb, ng = a.ng;
-    unsigned char *xs = smem;   // [T][nb] block_q8, as in global memory
-    stage_x(a, xs);
+    // xs: [T][nb] block_q8, as in global memory; with XF the fp32 rows come
+    // first in LDS and the blocks after them.
+    unsigned char *xs = XF ? smem + (size_t)T * cols * 4 : smem;
+    if (XF) stage_bytes(reinterpret_cast<const unsigned char *>(a.x), a.n_tok * cols * 4, smem);
+    else stage_bytes(a.xq, a.n_tok * nb * kBlockBytes, smem);
 
     const unsigned char *wrow[RW];
     const float *drow[RW];
@@ -228,6 +260,10 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(GemvArgs a) {
         if (g0 == 0) {
             wait_vm<3 * GC * RW>();   // the activation copies, issued first, have landed
             __syncthreads();
+            if (XF) {
+                quantize_lds(a, smem, xs);
+                __syncthreads();
+            }
         }
 #pragma unroll
         for (int u = 0; u < GC; u++) {
@@ -282,6 +318,12 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(GemvArgs a) {
     }
 }
 
+// LDS of a launch: t block_q8 rows, plus the t fp32 rows they are quantized
+// from when the input is fp32.
+size_t lds_bytes(int t, int nb, bool xf) {
+    return (size_t)t * nb * kBlockBytes + (xf ? (size_t)t * nb * kQK * 4 : 0);
+}
+
 int env_int(const char *name, int dflt) {
     const char *s = getenv(name);
     return (s && *s) ? atoi(s) : dflt;
@@ -306,52 +348,68 @@ int pick_gc(int ng, int rw) {
     return gc;
 }
 
-// Largest token count per launch whose staged rows fit the LDS budget.
-int pick_tokens(int nb) {
+// Largest token count per launch whose staged rows fit the LDS budget
+// (fp32 input: 1 or 2 rows, quantized in LDS).
+int pick_tokens(int nb, bool xf) {
     for (int t : {8, 4, 2, 1})
-        if ((size_t)t * nb * kBlockBytes <= kMaxStageBytes) return t;
+        if ((!xf || t <= 2) && lds_bytes(t, nb, xf) <= kMaxStageBytes) return t;
     return 0;
 }
 
-template <int T, int RW, int GC>
+template <int T, int RW, int GC, bool XF>
 hipError_t launch_t(const GemvArgs &a, hipStream_t s) {
     const int waves = (a.rows_total + RW - 1) / RW;
     const int grid = (waves + kGemvWaves - 1) / kGemvWaves;
-    const size_t lds = ((size_t)T * a.nb * kBlockBytes + 15) & ~(size_t)15;
-    hipLaunchKernelGGL((gemv_q8_kernel<T, RW, GC>), dim3(grid), dim3(kThreads), lds, s, a);
+    const size_t lds = (lds_bytes(T, a.nb, XF) + 15) & ~(size_t)15;
+    if (lds > kDefaultLdsLimit) {
+        static bool opted = false;   // once per instantiation (and process)
+        if (!opted) {
+            const hipError_t e = hipFuncSetAttribute((const void *)gemv_q8_kernel<T, RW, GC, XF>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     (int)kMaxStageBytes);
+            if (e != hipSuccess) return e;
+            opted = true;
+        }
+    }
+    hipLaunchKernelGGL((gemv_q8_kernel<T, RW, GC, XF>), dim3(grid), dim3(kThreads), lds, s, a);
     return hipGetLastError();
 }
 
 template <int RW, int GC>
-hipError_t launch_tok(const GemvArgs &a, int tmax, hipStream_t s) {
+hipError_t launch_tok(const GemvArgs &a, int tmax, bool xf, hipStream_t s) {
+    if (xf) return tmax == 2 ? launch_t<2, RW, GC, true>(a, s) : launch_t<1, RW, GC, true>(a, s);
     switch (tmax) {
-        case 8: return launch_t<8, RW, GC>(a, s);
-        case 4: return launch_t<4, RW, GC>(a, s);
-        case 2: return launch_t<2, RW, GC>(a, s);
-        default: return launch_t<1, RW, GC>(a, s);
+        case 8: return launch_t<8, RW, GC, false>(a, s);
+        case 4: return launch_t<4, RW, GC, false>(a, s);
+        case 2: return launch_t<2, RW, GC, false>(a, s);
+        default: return launch_t<1, RW, GC, false>(a, s);
     }
 }
 
-hipError_t launch_gemv(const GemvArgs &a, int tcap, int rw, int gc, hipStream_t s) {
+hipError_t launch_gemv(const GemvArgs &a, int tcap, bool xf, int rw, int gc, hipStream_t s) {
     switch (rw * 16 + gc) {
-        case 0x11: return launch_tok<1, 1>(a, tcap, s);
-        case 0x12: return launch_tok<1, 2>(a, tcap, s);
-        case 0x14: return launch_tok<1, 4>(a, tcap, s);
-        case 0x21: return launch_tok<2, 1>(a, tcap, s);
-        case 0x22: return launch_tok<2, 2>(a, tcap, s);
-        case 0x24: return launch_tok<2, 4>(a, tcap, s);
-        case 0x41: return launch_tok<4, 1>(a, tcap, s);
-        default: return launch_tok<4, 2>(a, tcap, s);
+        case 0x11: return launch_tok<1, 1>(a, tcap, xf, s);
+        case 0x12: return launch_tok<1, 2>(a, tcap, xf, s);
+        case 0x14: return launch_tok<1, 4>(a, tcap, xf, s);
+        case 0x21: return launch_tok<2, 1>(a, tcap, xf, s);
+        case 0x22: return launch_tok<2, 2>(a, tcap, xf, s);
+        case 0x24: return launch_tok<2, 4>(a, tcap, xf, s);
+        case 0x41: return launch_tok<4, 1>(a, tcap, xf, s);
+        default: return launch_tok<4, 2>(a, tcap, xf, s);
     }
 }
 
-// Runs the matmul over all tokens, in launches of up to tmax tokens.
+// Runs the matmul over all tokens, in launches of up to tmax tokens.  With
+// fp32 input (a.x) each launch quantizes its rows in LDS.
 int run_gemv(GemvArgs a, int n_tok, hipStream_t s) {
-    const int tmax = pick_tokens(a.nb);
+    const bool xf = a.x != nullptr;
+    const int tmax = pick_tokens(a.nb, xf);
     if (tmax == 0) return TQ_HIP_EINVAL;
     const int rw = pick_rw(a.rows_total);
     const int gc = pick_gc(a.ng, rw);
     const unsigned char *xq0 = a.xq;
+    const float *x0 = a.x;
+    unsigned char *out0 = a.xq_out;
     GemvSeg seg0[kMaxSegs];
     for (int i = 0; i < kMaxSegs; i++) seg0[i] = a.seg[i];
     for (int t0 = 0; t0 < n_tok; t0 += tmax) {
@@ -359,13 +417,23 @@ int run_gemv(GemvArgs a, int n_tok, hipStream_t s) {
         int tcap = 1;
         while (tcap < nt) tcap *= 2;
         a.n_tok = nt;
-        a.xq = xq0 + (size_t)t0 * a.nb * kBlockBytes;
+        const size_t blk_off = (size_t)t0 * a.nb * kBlockBytes;
+        a.xq = xq0 ? xq0 + blk_off : nullptr;
+        a.x = x0 ? x0 + (size_t)t0 * a.cols : nullptr;
+        a.xq_out = out0 ? out0 + blk_off : nullptr;
         for (int i = 0; i < kMaxSegs; i++)
             a.seg[i].y = seg0[i].y ? seg0[i].y + (size_t)t0 * seg0[i].rows : nullptr;
-        const hipError_t e = launch_gemv(a, tcap, rw, gc, s);
+        const hipError_t e = launch_gemv(a, tcap, xf, rw, gc, s);
         if (e != hipSuccess) return herr(e);
     }
     return TQ_HIP_OK;
+}
+
+// fp32 input is quantized inside the matmul launch for one or two rows (one
+// launch instead of two); more rows go through quantize_row_q8 into the
+// workspace first, so that a launch still covers up to 8 of them.
+bool fuse_quantize(const float *x, int n_tok, int nb) {
+    return n_tok <= 2 && ((uintptr_t)x & 15) == 0 && lds_bytes(n_tok, nb, true) <= kMaxStageBytes;
 }
 
 bool aligned(const void *p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
@@ -432,10 +500,16 @@ int tq_hip_project_qkv(const void *wq, const void *wk, const void *wv, int q_row
         !aligned(xn, 4) || !aligned(xq_ws, 4) || !aligned(q, 4) || !aligned(k, 4) || !aligned(v, 4))
         return TQ_HIP_EINVAL;
     const hipStream_t s = (hipStream_t)stream;
-    const hipError_t e = tq_launch_quantize(xn, xq_ws, n_tok * hidden, s);
-    if (e != hipSuccess) return herr(e);
     GemvArgs a;
     init_args(a, hidden);
+    if (fuse_quantize(xn, n_tok, a.nb)) {
+        a.x = xn;
+        a.xq_out = (unsigned char *)xq_ws;
+    } else {
+        const hipError_t e = tq_launch_quantize(xn, xq_ws, n_tok * hidden, s);
+        if (e != hipSuccess) return herr(e);
+        a.xq = (const unsigned char *)xq_ws;
+    }
     a.seg[0] = GemvSeg{(const unsigned char *)wq, q, q_rows};
     a.seg[1] = GemvSeg{(const unsigned char *)wk, k, kv_rows};
     a.seg[2] = GemvSeg{(const unsigned char *)wv, v, kv_rows};
@@ -443,7 +517,6 @@ int tq_hip_project_qkv(const void *wq, const void *wk, const void *wv, int q_row
     a.seg_end[1] = q_rows + kv_rows;
     a.seg_end[2] = q_rows + 2 * kv_rows;
     a.rows_total = a.seg_end[2];
-    a.xq = (const unsigned char *)xq_ws;
     return run_gemv(a, n_tok, s);
 }
 
@@ -453,14 +526,19 @@ int tq_hip_project_output(const void *wo, int rows, int cols, const float *attn,
         !aligned(attn, 4) || !aligned(xq_ws, 4) || !aligned(out, 4))
         return TQ_HIP_EINVAL;
     const hipStream_t s = (hipStream_t)stream;
-    const hipError_t e = tq_launch_quantize(attn, xq_ws, n_tok * cols, s);
-    if (e != hipSuccess) return herr(e);
     GemvArgs a;
     init_args(a, cols);
+    if (fuse_quantize(attn, n_tok, a.nb)) {
+        a.x = attn;
+        a.xq_out = (unsigned char *)xq_ws;
+    } else {
+        const hipError_t e = tq_launch_quantize(attn, xq_ws, n_tok * cols, s);
+        if (e != hipSuccess) return herr(e);
+        a.xq = (const unsigned char *)xq_ws;
+    }
     a.seg[0] = GemvSeg{(const unsigned char *)wo, out, rows};
     a.seg_end[0] = a.seg_end[1] = a.seg_end[2] = rows;
     a.rows_total = rows;
-    a.xq = (const unsigned char *)xq_ws;
     return run_gemv(a, n_tok, s);
 }
 
