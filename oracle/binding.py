@@ -78,6 +78,9 @@ class Oracle:
         L.oracle_attention_qkv.restype = _i
         L.oracle_prefill_qkv.argtypes = [_vp, _vp, _i, _i, _i, _i, _f, _i, _i, _vp, _vp, _vp, _vp, _vp]
         L.oracle_prefill_qkv.restype = _i
+        L.oracle_rmsnorm.argtypes = [_vp, _vp, _vp, _i, _f]
+        L.oracle_attention_layer.argtypes = [_vp] * 6 + [_i, _i, _i, _i, _f, _f, _vp, _vp, _i, _i, _vp, _vp, _vp]
+        L.oracle_attention_layer.restype = _i
         L.oracle_pack_matrix_q8.argtypes = [_vp, _i, _i, _vp]
         L.oracle_matmul_q8.argtypes = [_vp, _vp, _vp, _i, _i]
         L.oracle_matmul_q8_batch.argtypes = [_vp, _vp, _vp, _i, _i, _i]
@@ -143,6 +146,25 @@ class Oracle:
                                          ptr(q), ptr(k), ptr(v), ptr(scores), ptr(out))
         return rc, out
 
+    def rmsnorm(self, x, weight, eps: float) -> np.ndarray:
+        """model/rmsnorm.c on each row of x (rows of len(weight))."""
+        w = f32(weight)
+        x = f32(x).reshape(-1, w.size).copy()
+        for r in range(x.shape[0]):
+            row = x[r]
+            self.lib.oracle_rmsnorm(ptr(row), ptr(w), ptr(row), w.size, eps)
+        return x.reshape(-1)
+
+    def attention_layer(self, w, nq, nkv, hd, hidden, theta, eps, kc, vc, max_tokens, pos, xn):
+        """attention_layer for one token; w = (wq, wk, wv, wo, q_norm, k_norm); caches in place."""
+        wq, wk, wv, wo, qn, kn = (np.ascontiguousarray(a) for a in w)
+        scores = np.zeros(nq * max_tokens, np.float32)
+        out = np.zeros(hidden, np.float32)
+        rc = self.lib.oracle_attention_layer(ptr(wq), ptr(wk), ptr(wv), ptr(wo), ptr(f32(qn)), ptr(f32(kn)),
+                                             nq, nkv, hd, hidden, theta, eps, ptr(kc), ptr(vc), max_tokens,
+                                             pos, ptr(f32(xn)), ptr(scores), ptr(out))
+        return rc, out
+
     # --- weight side ---------------------------------------------------------
     def pack_matrix_q8(self, W) -> np.ndarray:
         """rows x cols floats -> rows x cols/32 block_q8 (packer/packer.c)."""
@@ -205,6 +227,7 @@ class Ref:
         L.tqref_attention_qkv.argtypes = [_i, _i, _i, _i, _f, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]
         L.tqref_attention_qkv.restype = _i
         L.tqref_isa.restype = C.c_char_p
+        L.rmsnorm.argtypes = [_vp, _vp, _vp, _i, _f]
         L.pack_matrix.argtypes = [_vp, _i, _i, _vp, C.c_char]
         L.pack_matrix.restype = _i
         simd = ("matmul_q8_avx2",) if not scalar else ()
@@ -219,6 +242,16 @@ class Ref:
 
     def isa(self) -> str:
         return self.lib.tqref_isa().decode()
+
+    def rmsnorm(self, x, weight, eps: float) -> np.ndarray:
+        w = f32(weight)
+        x = f32(x).reshape(-1, w.size)
+        out = np.zeros_like(x)
+        for r in range(x.shape[0]):
+            xr = np.ascontiguousarray(x[r])
+            o = out[r]
+            self.lib.rmsnorm(ptr(xr), ptr(w), ptr(o), w.size, eps)
+        return out.reshape(-1)
 
     def pack_matrix_q8(self, W) -> np.ndarray:
         W = f32(W)

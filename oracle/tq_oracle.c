@@ -289,3 +289,41 @@ void oracle_project_q8(const block_q8 *W, int rows, int cols, const float *x, in
         oracle_matmul_q8(W, xq, y + (size_t)t * rows, rows, cols);
     }
 }
+
+/* model/rmsnorm.c:4-19: sum of squares in one serial fp32 pass, rms =
+ * sqrtf(eps + sum / n), inverse 1/rms, out = (x * inverse) * weight.  In place
+ * (out == x) is allowed, as norm_heads uses it (model/attention_layer.c:48-53). */
+void oracle_rmsnorm(const float *x, const float *weight, float *out, int n, float eps) {
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) sum += x[i] * x[i];
+    const float inv = 1.0f / sqrtf(eps + sum / (float)n);
+    for (int i = 0; i < n; i++) out[i] = x[i] * inv * weight[i];
+}
+
+/* model/attention_layer.c:169-194 (attention_layer) on the flat Q8 cache:
+ * project_qkv (quantize_row_q8 of xn, then wq, wk, wv), per-head RMSNorm of q
+ * and k (:48-53), RoPE + store_kv + attend_q8 (oracle_attention_qkv), then
+ * project_output (quantize the attention output, then wo).  Returns -1 for a
+ * bad pos before any write. */
+int oracle_attention_layer(const block_q8 *wq, const block_q8 *wk, const block_q8 *wv,
+                           const block_q8 *wo, const float *q_norm, const float *k_norm,
+                           int n_q_heads, int n_kv_heads, int head_dim, int hidden,
+                           float rope_theta, float rms_eps, block_q8 *k_cache,
+                           block_q8 *v_cache, int max_tokens, int pos, const float *xn,
+                           float *scores, float *out) {
+    if (pos < 0 || pos >= max_tokens) return -1;
+    const int qdim = n_q_heads * head_dim, kvdim = n_kv_heads * head_dim;
+    float q[qdim], k[kvdim], v[kvdim], attn[qdim];
+    oracle_project_q8(wq, qdim, hidden, xn, 1, q);
+    oracle_project_q8(wk, kvdim, hidden, xn, 1, k);
+    oracle_project_q8(wv, kvdim, hidden, xn, 1, v);
+    for (int h = 0; h < n_q_heads; h++)
+        oracle_rmsnorm(q + (size_t)h * head_dim, q_norm, q + (size_t)h * head_dim, head_dim, rms_eps);
+    for (int h = 0; h < n_kv_heads; h++)
+        oracle_rmsnorm(k + (size_t)h * head_dim, k_norm, k + (size_t)h * head_dim, head_dim, rms_eps);
+    int rc = oracle_attention_qkv(k_cache, v_cache, n_q_heads, n_kv_heads, head_dim, max_tokens,
+                                  rope_theta, pos, q, k, v, scores, attn);
+    if (rc != 0) return rc;
+    oracle_project_q8(wo, hidden, qdim, attn, 1, out);
+    return 0;
+}

@@ -69,6 +69,18 @@ int oracle_prefill_qkv(block_q8 *k_cache, block_q8 *v_cache, int n_q_heads, int 
                        int head_dim, int max_tokens, float rope_theta, int pos0, int n,
                        float *q, float *k, const float *v, float *scores, float *out);
 
+/* model/rmsnorm.c:4-19 (in place allowed). */
+void oracle_rmsnorm(const float *x, const float *weight, float *out, int n, float eps);
+
+/* model/attention_layer.c:169-194: the whole attention layer for one token
+ * (projections, q/k RMSNorm, RoPE, store_kv, attend_q8, output projection). */
+int oracle_attention_layer(const block_q8 *wq, const block_q8 *wk, const block_q8 *wv,
+                           const block_q8 *wo, const float *q_norm, const float *k_norm,
+                           int n_q_heads, int n_kv_heads, int head_dim, int hidden,
+                           float rope_theta, float rms_eps, block_q8 *k_cache,
+                           block_q8 *v_cache, int max_tokens, int pos, const float *xn,
+                           float *scores, float *out);
+
 /* packer/packer.c:4-31 (pack_row_q8 over every row): weights -> block_q8. */
 void oracle_pack_matrix_q8(const float *W, int rows, int cols, block_q8 *out);
 
