@@ -164,6 +164,17 @@ int tq_hip_decode_step_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq,
                              const int32_t *d_pos, int max_pos, const float *d_q,
                              const float *d_k, const float *d_v, const float *d_cos,
                              const float *d_sin, float *d_out, void *stream);
+/* The same step with the per-head RMSNorm of q and of the new K in front of
+ * RoPE (norm_heads, model/attention_layer.c:48-53,183-184; model/rmsnorm.c:4-19):
+ * d_q and d_k are the projections' raw outputs, d_q_norm / d_k_norm the
+ * head_dim weights (16-byte aligned).  The norm keeps the reference's serial
+ * sum of squares, so the cached K codes equal those of attention_layer bit for
+ * bit.  Head dims 32/64/128 with groups 1..8 (the MFMA decode kernel);
+ * TQ_HIP_ETYPE otherwise. */
+int tq_hip_decode_step_norm_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_pos,
+                                  int max_pos, const float *d_q, const float *d_k, const float *d_v,
+                                  const float *d_q_norm, const float *d_k_norm, float rms_eps,
+                                  const float *d_cos, const float *d_sin, float *d_out, void *stream);
 
 /* ---- prefill: the attention loop of attention_layer_batch
  * (model/attention_layer.c:203-204,221-236): tokens pos0..pos0+n-1 of `seq`,

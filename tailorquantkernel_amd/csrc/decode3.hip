@@ -43,6 +43,13 @@
 // Step mode (k_new != null): the work-group owning position len-1 quantizes the
 // new token's K (after RoPE) and V exactly as store_kv does, writes them to the
 // cache and patches them into the staged tile: append + attend in one launch.
+//
+// With q_norm (and k_norm in step mode) the q rows and the new K row are the
+// projections' raw outputs: each wave first takes every head's RMSNorm
+// (model/rmsnorm.c:4-19, norm_heads at model/attention_layer.c:48-53,183-184)
+// in the reference's order — one lane per head sums the squares serially —
+// and applies (x * inverse) * weight before RoPE, so the K codes stay
+// bit-exact with the whole attention_layer.
 #include "tq_common.hpp"
 
 namespace {
@@ -179,6 +186,20 @@ __device__ __forceinline__ void wait_copies() {
 // memory those accesses touch).
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); }
 
+// RMSNorm's last step, out = (x * inverse) * weight, rounded as
+// model/rmsnorm.c:17 rounds it.
+__device__ __forceinline__ float norm1(float x, float inv, float w) {
+#pragma clang fp contract(off)
+    return x * inv * w;
+}
+__device__ __forceinline__ void norm8(float (&x)[8], float inv, const float *w) {
+    float ww[8];
+    *reinterpret_cast<v4f *>(&ww[0]) = *reinterpret_cast<const v4f *>(w);
+    *reinterpret_cast<v4f *>(&ww[4]) = *reinterpret_cast<const v4f *>(w + 4);
+#pragma unroll
+    for (int i = 0; i < 8; i++) x[i] = norm1(x[i], inv, ww[i]);
+}
+
 // W waves per work-group (4, or 8 when each wave has only a tile or two).
 template <int HD, int G, int W>
 __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
@@ -241,16 +262,22 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
     //      front of its second slot: q rows of the group | cos | sin | new K | new V
     //      (fp32).  These copies go first so that waiting for them lets every
     //      later K/V copy stay in flight.
+    const bool nrm = a.q_norm != nullptr;
     float *stq = reinterpret_cast<float *>(tb1);
     float *stc = stq + G * HD;
     float *sts = stc + HD / 2;
     float *stk = sts + HD / 2;
     float *stv = stk + HD;
+    float *stqn = stv + HD;          // RMSNorm weights of q | of k
+    float *stkn = stqn + HD;
+    float *stinv = stkn + HD;        // 1/rms of the G q heads, then of the new K row
+    static_assert((G + 5) * HD * 4 + 4 * (G + 1) <= L::TILE, "staged inputs fit the slot");
     {
         // 16-byte chunks per part; the cos/sin slots are always there (without
-        // RoPE they repeat q) so every part sits at a fixed offset
+        // RoPE they repeat q) so every part sits at a fixed offset; with the
+        // norm weights the K and V slots are too (without a step they repeat q)
         constexpr int QC = G * HD / 4, RC = HD / 8, NC = HD / 4;
-        const int nch = QC + 2 * RC + (step ? 2 * NC : 0);
+        const int nch = QC + 2 * RC + (nrm ? 4 * NC : (step ? 2 * NC : 0));
         const float *qg = a.q + ((size_t)qi * a.n_q_heads + (size_t)kvh * G) * HD;
         const size_t nrow = ((size_t)qi * a.n_kv_heads + kvh) * HD;
         for (int c0 = 0; c0 < nch; c0 += 64) {
@@ -261,9 +288,12 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
             } else if (c < QC + 2 * RC) {
                 const int r = c - QC;
                 if (rot) src = (r < RC ? a.cos_t : a.sin_t) + (size_t)qi * (HD / 2) + 4 * (r < RC ? r : r - RC);
-            } else if (c < nch) {
+            } else if (c < QC + 2 * RC + 2 * NC) {
                 const int r = c - QC - 2 * RC;
-                src = (r < NC ? a.k_new : a.v_new) + nrow + 4 * (r < NC ? r : r - NC);
+                if (step) src = (r < NC ? a.k_new : a.v_new) + nrow + 4 * (r < NC ? r : r - NC);
+            } else if (c < nch) {
+                const int r = c - QC - 2 * RC - 2 * NC;
+                src = r < NC ? a.q_norm + 4 * r : (step ? a.k_norm : a.q_norm) + 4 * (r - NC);
             }
             if (c0 + 64 <= nch || c < nch) dma16(src, tb1 + 16 * c0);
         }
@@ -351,6 +381,23 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
         wait_copies<CPL>();
     else
         wait_copies<0>();
+    if (nrm) {
+        // 1/rms of each q head (lanes 0..G-1) and of the new K row (lane G):
+        // the squares summed serially in element order, as model/rmsnorm.c:4-12
+        if (lane <= G) {
+#pragma clang fp contract(off)
+            const float *src = lane < G ? stq + lane * HD : stk;
+            float sum = 0.0f;
+            for (int i = 0; i < HD; i += 4) {
+                const v4f v = *reinterpret_cast<const v4f *>(src + i);
+                sum += v.x * v.x;
+                sum += v.y * v.y;
+                sum += v.z * v.z;
+                sum += v.w * v.w;
+            }
+            stinv[lane] = 1.0f / sqrtf(a.rms_eps + sum / (float)HD);
+        }
+    }
     const int pos_new = len - 1;
     const bool owns_new = step && pos_new >= t_begin && pos_new < t_end;
     // the one wave whose tiles hold pos_new appends the new token
@@ -373,6 +420,8 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
         float x[8];
         *reinterpret_cast<v4f *>(&x[0]) = *reinterpret_cast<const v4f *>(row + e0);
         *reinterpret_cast<v4f *>(&x[4]) = *reinterpret_cast<const v4f *>(row + e0 + 4);
+        const float inv_h = nrm ? stinv[min(h, G - 1)] : 1.0f;
+        if (nrm) norm8(x, inv_h, stqn + e0);
         if (rot) {
             constexpr int HALF = HD / 2;
             const bool lower = e0 < HALF;
@@ -381,6 +430,7 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
             float y[8], c[8], sn[8];
             *reinterpret_cast<v4f *>(&y[0]) = *reinterpret_cast<const v4f *>(pr);
             *reinterpret_cast<v4f *>(&y[4]) = *reinterpret_cast<const v4f *>(pr + 4);
+            if (nrm) norm8(y, inv_h, stqn + (lower ? e0 + HALF : e0 - HALF));
             *reinterpret_cast<v4f *>(&c[0]) = *reinterpret_cast<const v4f *>(stc + pi);
             *reinterpret_cast<v4f *>(&c[4]) = *reinterpret_cast<const v4f *>(stc + pi + 4);
             *reinterpret_cast<v4f *>(&sn[0]) = *reinterpret_cast<const v4f *>(sts + pi);
@@ -423,12 +473,14 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
                 const int col = 32 * b + (lane & 31);
                 const bool is_v = j >= NB;
                 const float *row = is_v ? stv : stk;
-                float x = row[col];
+                // the K row's values through its RMSNorm when there is one
+                auto kval = [&](int e) { return nrm && !is_v ? norm1(row[e], stinv[G], stkn[e]) : row[e]; };
+                float x = kval(col);
                 if (rot && !is_v) {
                     const int half = HD / 2;
                     const int pi = col < half ? col : col - half;
-                    x = col < half ? rope_lower(row[col], row[col + half], stc[pi], sts[pi])
-                                   : rope_upper(row[col - half], row[col], stc[pi], sts[pi]);
+                    x = col < half ? rope_lower(kval(col), kval(col + half), stc[pi], sts[pi])
+                                   : rope_upper(kval(col - half), kval(col), stc[pi], sts[pi]);
                 }
                 quantize_store32(x, sm.newrow + (is_v ? ROW : 0) + b * kBlockBytes);
             }

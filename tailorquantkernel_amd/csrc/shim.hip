@@ -301,10 +301,13 @@ void seq_contig(const tq_hip_kv *kv, int seq, int *first, int *n) {
 }
 
 // contig_seq: the one sequence every query of this call reads, or -1.
+// q_norm non-null: q (and the new K) are raw projections, RMSNorm'd in the
+// kernel with q_norm / k_norm and eps (MFMA kernel only).
 int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_len, int len_plus,
                   int seq_const, int seq_stride, int pos0, int max_len, const float *d_q, const float *d_cos,
                   const float *d_sin, const float *d_k, const float *d_v, float *d_out,
-                  hipStream_t s, int contig_seq) {
+                  hipStream_t s, int contig_seq, const float *q_norm = nullptr,
+                  const float *k_norm = nullptr, float rms_eps = 0.0f) {
     if (n_q <= 0) return TQ_HIP_OK;
     // queries and kv heads are grid dimensions y/z (at most 65535 each)
     if (n_q > 65535 || kv->desc.n_kv_heads > 65535) return TQ_HIP_EINVAL;
@@ -326,6 +329,9 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
     a.sin_t = d_sin;
     a.k_new = d_k;
     a.v_new = d_v;
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+    a.rms_eps = rms_eps;
     a.out = d_out;
     a.n_q = n_q;
     a.n_q_heads = D.n_q_heads;
@@ -347,6 +353,11 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
     const bool aligned = (((uintptr_t)d_q | (uintptr_t)d_cos | (uintptr_t)d_sin | (uintptr_t)d_k | (uintptr_t)d_v) &
                           15) == 0;
     const bool v3 = aligned && use_decode3(kv);
+    if (q_norm) {
+        // the norm is fused into the MFMA kernel only; it stages 16-byte pieces
+        if (((uintptr_t)q_norm | (uintptr_t)k_norm) & 15) return TQ_HIP_EINVAL;
+        if (!v3) return TQ_HIP_ETYPE;
+    }
     // four waves per work-group: for a single 4k-token sequence at the 8B
     // shape this spreads one 32-key tile per wave over all 256 CUs, which beats
     // eight waves on half of them (8.7 against 9.1 us per step)
@@ -712,6 +723,17 @@ int tq_hip_decode_step_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const
     if (!d_seq && n_q > kv->desc.max_seqs) return TQ_HIP_EINVAL;
     return decode_common(kv, n_q, d_seq, d_pos, 1, 0, 1, 0, max_pos + 1, d_q, d_cos, d_sin, d_k, d_v, d_out,
                          pick(kv, stream), (!d_seq && n_q == 1) ? 0 : -1);
+}
+
+int tq_hip_decode_step_norm_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_pos,
+                                  int max_pos, const float *d_q, const float *d_k, const float *d_v,
+                                  const float *d_q_norm, const float *d_k_norm, float rms_eps,
+                                  const float *d_cos, const float *d_sin, float *d_out, void *stream) {
+    if (!kv || n_q < 0 || max_pos < 0) return TQ_HIP_EINVAL;
+    if (n_q > 0 && (!d_pos || !d_k || !d_v || !d_q_norm || !d_k_norm)) return TQ_HIP_EINVAL;
+    if (!d_seq && n_q > kv->desc.max_seqs) return TQ_HIP_EINVAL;
+    return decode_common(kv, n_q, d_seq, d_pos, 1, 0, 1, 0, max_pos + 1, d_q, d_cos, d_sin, d_k, d_v, d_out,
+                         pick(kv, stream), (!d_seq && n_q == 1) ? 0 : -1, d_q_norm, d_k_norm, rms_eps);
 }
 
 int tq_hip_attend(tq_hip_kv *kv, int seq, int pos, const float *q, const float *cos_t, const float *sin_t,

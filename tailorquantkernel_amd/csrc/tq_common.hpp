@@ -216,6 +216,9 @@ struct TqDecodeArgs {
     const float *sin_t;
     const float *k_new;      // step mode: [n_q][n_kv_heads][hd] (pre-RoPE), else null
     const float *v_new;
+    const float *q_norm;     // [hd] RMSNorm weights applied to q (and k_norm to the new
+    const float *k_norm;     // K) before RoPE, or null: q and k are already normalized
+    float rms_eps;
     float *out;              // [n_q][n_q_heads][hd]
     float *partials;         // [n_q][n_kv][n_splits][G*(hd+2)] when n_splits > 1
     int *counters;           // [n_q][n_kv] arrival counters, zero between launches
