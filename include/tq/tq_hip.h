@@ -232,6 +232,41 @@ int tq_hip_project_qkv(const void *wq, const void *wk, const void *wv, int q_row
 int tq_hip_project_output(const void *wo, int rows, int cols, const float *attn, int n_tok,
                           block_q8 *xq_ws, float *out, void *stream);
 
+/* ---- the whole attention layer on the device --------------------------- */
+
+/* tq_attn_weights (model/model_ops.h:27-37) with device pointers: the four
+ * projection matrices in the tiled Q8 layout (tq_hip_q8_pack) and the
+ * head_dim RMSNorm weights of q and k (16-byte aligned). */
+typedef struct {
+    const void *wq;          /* n_q_heads*head_dim x hidden   */
+    const void *wk;          /* n_kv_heads*head_dim x hidden  */
+    const void *wv;          /* n_kv_heads*head_dim x hidden  */
+    const void *wo;          /* hidden x n_q_heads*head_dim   */
+    const float *q_norm;
+    const float *k_norm;
+    int hidden;
+    float rms_eps;
+} tq_hip_attn_weights;
+
+/* Device workspace bytes tq_hip_attention_layer_async needs for n_q tokens
+ * (q, k, v and attention rows plus the quantized activations, the reference's
+ * tq_batch_ws), or 0 for a bad shape. */
+size_t tq_hip_attention_layer_ws_bytes(const tq_hip_kv *kv, const tq_hip_attn_weights *w, int n_q);
+
+/* attention_layer (model/attention_layer.c:169-194) for n_q decode tokens,
+ * each of sequence d_seq[i] (NULL: sequence i) at position d_pos[i] <= max_pos,
+ * in three launches on `stream`: project_qkv over the n_q rows of d_xn
+ * [n_q][hidden]; RMSNorm + RoPE (d_cos/d_sin [n_q][head_dim/2], or NULL) +
+ * append + attend (tq_hip_decode_step_norm_async); project_output into
+ * d_out [n_q][hidden].  d_ws: tq_hip_attention_layer_ws_bytes bytes, 16-byte
+ * aligned.  Each token is the next token of its own sequence (batched
+ * decode); with n_q = 1 this is attention_layer.  Several consecutive tokens
+ * of one sequence are attention_layer_batch's work (prefill), not this call's. */
+int tq_hip_attention_layer_async(tq_hip_kv *kv, const tq_hip_attn_weights *w, int n_q,
+                                 const int32_t *d_seq, const int32_t *d_pos, int max_pos,
+                                 const float *d_xn, const float *d_cos, const float *d_sin,
+                                 float *d_out, void *d_ws, size_t ws_bytes, void *stream);
+
 /* ---- measurement: streaming-read bandwidth of device memory, the GPU
  * counterpart of the reference's host RAM probe (tools/membw.h:1-80).  Reads
  * `bytes` (a multiple of 16) of `buf` once with 16-byte loads; `sink` (device,

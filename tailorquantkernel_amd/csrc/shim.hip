@@ -848,4 +848,61 @@ int tq_hip_prefill(tq_hip_kv *kv, int seq, int pos0, int n, const float *q, cons
     return copy_out_sync(kv, out, oo, qb);
 }
 
+
+// ---- the whole attention layer -------------------------------------------
+
+static size_t layer_ws(const tq_hip_kv_desc &D, int hidden, int n_q, size_t *off_q, size_t *off_k,
+                       size_t *off_v, size_t *off_attn, size_t *off_xq) {
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t qd = (size_t)D.n_q_heads * D.head_dim, kd = (size_t)D.n_kv_heads * D.head_dim;
+    const size_t widest = (size_t)(hidden > (int)qd ? hidden : (int)qd);
+    size_t o = 0;
+    *off_q = o;
+    o += al((size_t)n_q * qd * 4);
+    *off_k = o;
+    o += al((size_t)n_q * kd * 4);
+    *off_v = o;
+    o += al((size_t)n_q * kd * 4);
+    *off_attn = o;
+    o += al((size_t)n_q * qd * 4);
+    *off_xq = o;
+    o += al((size_t)n_q * widest / QK * sizeof(block_q8));
+    return o;
+}
+
+static bool layer_shape_ok(const tq_hip_kv *kv, const tq_hip_attn_weights *w, int n_q) {
+    return kv && w && n_q > 0 && w->hidden > 0 && w->hidden % QK == 0 &&
+           (kv->desc.n_q_heads * kv->desc.head_dim) % QK == 0;
+}
+
+size_t tq_hip_attention_layer_ws_bytes(const tq_hip_kv *kv, const tq_hip_attn_weights *w, int n_q) {
+    if (!layer_shape_ok(kv, w, n_q)) return 0;
+    size_t oq, ok, ov, oa, ox;
+    return layer_ws(kv->desc, w->hidden, n_q, &oq, &ok, &ov, &oa, &ox);
+}
+
+int tq_hip_attention_layer_async(tq_hip_kv *kv, const tq_hip_attn_weights *w, int n_q,
+                                 const int32_t *d_seq, const int32_t *d_pos, int max_pos,
+                                 const float *d_xn, const float *d_cos, const float *d_sin,
+                                 float *d_out, void *d_ws, size_t ws_bytes, void *stream) {
+    if (!layer_shape_ok(kv, w, n_q) || !d_pos || !d_xn || !d_out || !d_ws || ((uintptr_t)d_ws & 15) ||
+        !w->wq || !w->wk || !w->wv || !w->wo || !w->q_norm || !w->k_norm)
+        return TQ_HIP_EINVAL;
+    const tq_hip_kv_desc &D = kv->desc;
+    size_t oq, ok, ov, oa, ox;
+    if (ws_bytes < layer_ws(D, w->hidden, n_q, &oq, &ok, &ov, &oa, &ox)) return TQ_HIP_EINVAL;
+    unsigned char *ws = (unsigned char *)d_ws;
+    float *q = (float *)(ws + oq), *k = (float *)(ws + ok), *v = (float *)(ws + ov);
+    float *attn = (float *)(ws + oa);
+    block_q8 *xq = (block_q8 *)(ws + ox);
+    const int qd = D.n_q_heads * D.head_dim, kd = D.n_kv_heads * D.head_dim;
+    void *s = (void *)pick(kv, stream);
+    int rc = tq_hip_project_qkv(w->wq, w->wk, w->wv, qd, kd, w->hidden, d_xn, n_q, xq, q, k, v, s);
+    if (rc != TQ_HIP_OK) return rc;
+    rc = tq_hip_decode_step_norm_async(kv, n_q, d_seq, d_pos, max_pos, q, k, v, w->q_norm, w->k_norm,
+                                       w->rms_eps, d_cos, d_sin, attn, s);
+    if (rc != TQ_HIP_OK) return rc;
+    return tq_hip_project_output(w->wo, w->hidden, qd, attn, n_q, xq, d_out, s);
+}
+
 }  // extern "C"

@@ -73,6 +73,8 @@ _PROTOS = {
     "tq_hip_membw_read": (_i, [_vp, _sz, _vp, C.c_uint, _vp]),
     "tq_hip_decode_step_norm_async": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp,
                                           _vp, _vp]),
+    "tq_hip_attention_layer_ws_bytes": (_sz, [_vp, _vp, _i]),
+    "tq_hip_attention_layer_async": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "tq_hip_q8_matrix_bytes": (_sz, [_i, _i]),
     "tq_hip_q8_pack": (_i, [_vp, _vp, _i, _i, _vp]),
     "tq_hip_q8_unpack": (_i, [_vp, _vp, _i, _i, _vp]),
@@ -129,6 +131,12 @@ def device_arch() -> str:
     buf = C.create_string_buffer(256)
     check(load().tq_hip_device_arch(buf, 256), "tq_hip_device_arch")
     return buf.value.decode()
+
+
+class AttnWeights(C.Structure):
+    """tq_hip_attn_weights: device projection matrices (tiled Q8) and norm weights."""
+    _fields_ = [("wq", C.c_void_p), ("wk", C.c_void_p), ("wv", C.c_void_p), ("wo", C.c_void_p),
+                ("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("hidden", C.c_int), ("rms_eps", C.c_float)]
 
 
 class DeviceBuffer:
