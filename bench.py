@@ -23,8 +23,9 @@ Other workloads: --config decode-batched (64 sequences, ragged 512..8192,
 paged), decode-70b-32k (64q/8kv, batch 16, context 32768, 1 % outliers),
 prefill-2k (causal prefill of 2048 tokens), project-8b / project-70b (the Q8
 weight GEMVs either side of attention for one token: project_qkv and
-project_output, 32 layers' weights rotated).  They print the same JSON
-fields for their own shape.
+project_output, 32 layers' weights rotated), layer-8b (the whole
+attention_layer for one token at ctx 4096: projections, q/k RMSNorm, RoPE,
+append, attend).  They print the same JSON fields for their own shape.
 
 --copy-calibration BYTES runs one device-to-device copy of BYTES first: its
 FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc give the counters' scale.
@@ -713,6 +714,167 @@ def bench_project_70b(args, nat, hip):
     return bench_project(args, nat, hip, shape=(64, 8, 128, 8192), name="70b")
 
 
+# ---------------------------------------------------------------------------
+# the whole attention layer for one token: projections + norm/RoPE/append/attend
+
+def bench_layer_8b(args, nat, hip):
+    """attention_layer (model/attention_layer.c:169-194) at the 8B shape, context 4096,
+    one token, all on the device: tq_hip_attention_layer_async per layer, `layers`
+    layers' weights and caches rotated, timed over HIP graph replays."""
+    from oracle.binding import Oracle
+    lib = nat.load()
+    nq, nkv, hd, hidden, T, theta, eps = 32, 8, 128, 4096, 4096, 500000.0, 1e-6
+    qr, kr = nq * hd, nkv * hd
+    nb = hd // QK
+    layers = args.layers
+    kv_bytes = T * nkv * 2 * nb * BLOCK_BYTES
+    rng = np.random.default_rng(21)
+    host_w = (random_q8_weights(rng, qr, hidden), random_q8_weights(rng, kr, hidden),
+              random_q8_weights(rng, kr, hidden), random_q8_weights(rng, hidden, qr))
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    dims = ((qr, hidden), (kr, hidden), (kr, hidden), (hidden, qr))
+    nbytes = [lib.tq_hip_q8_matrix_bytes(r, c) for r, c in dims]
+    layer_bytes = sum(nbytes)
+    big = nat.DeviceBuffer(layers * layer_bytes)
+    off = [0, nbytes[0], nbytes[0] + nbytes[1], nbytes[0] + nbytes[1] + nbytes[2]]
+    for w, (r, c), o in zip(host_w, dims, off):
+        src = nat.DeviceBuffer.from_numpy(w)
+        nat.check(lib.tq_hip_q8_pack(big.ptr + o, src.ptr, r, c, None), "q8_pack")
+        src.free()
+    hip.sync()
+    for l in range(1, layers):
+        nat.check(lib.tq_hip_memcpy_d2d(big.ptr + l * layer_bytes, big.ptr, layer_bytes, None), "d2d")
+    D = nat.DeviceBuffer.from_numpy
+    dqn, dkn = D(qn), D(kn)
+    weights = []
+    for l in range(layers):
+        b = big.ptr + l * layer_bytes
+        weights.append(nat.AttnWeights(b, b + off[1], b + off[2], b + off[3], dqn.ptr, dkn.ptr, hidden, eps))
+    kvs = [nat.PagedKV.single(nq, nkv, hd, T) for _ in range(layers)]
+    stream = kvs[0].stream
+    dk_rows = D(normal_rows(rng, T, nkv * hd))
+    dv_rows = D(normal_rows(rng, T, nkv * hd))
+    for kv in kvs:
+        fill_sequence(nat, kv, 0, T, dk_rows, dv_rows, T, kv.stream)
+    dk_rows.free()
+    dv_rows.free()
+    pos = T - 1
+    xn = rng.standard_normal(hidden, dtype=np.float32)
+    cos, sin = rope_tables(hd, [pos], theta)
+    dxn, dc, ds = D(xn), D(cos), D(sin)
+    dpos = D(np.array([pos], np.int32))
+    wsb = lib.tq_hip_attention_layer_ws_bytes(kvs[0].h, C.byref(weights[0]), 1)
+    ws = nat.DeviceBuffer(wsb)
+    outs = [nat.DeviceBuffer(hidden * 4) for _ in range(layers)]
+
+    def step(l):
+        nat.check(lib.tq_hip_attention_layer_async(kvs[l].h, C.byref(weights[l]), 1, None, dpos.ptr, pos, dxn.ptr,
+                                                   dc.ptr, ds.ptr, outs[l].ptr, ws.ptr, wsb, stream),
+                  "attention_layer")
+
+    # parity of layer 0: the oracle's attention_layer (bit-exact with the
+    # reference's) from the cache the GPU holds before the step
+    gk, gv = kvs[0].read(0, 0, T)
+    kc, vc = gk.reshape(-1).copy(), gv.reshape(-1).copy()
+    step(0)
+    hip.sync()
+    got = outs[0].download((hidden,), np.float32)
+    rc, ref = Oracle().attention_layer(host_w + (qn, kn), nq, nkv, hd, hidden, theta, eps, kc, vc, T, pos, xn)
+    err = rel_l2(got, ref)
+    parity = {"ok": bool(rc == 0 and err <= 1e-2), "rel_l2_err": err,
+              "bar": "relative L2 error <= 1e-2 per token (one moved activation code; median 1e-5 in the tests)",
+              "against": "oracle attention_layer (bit-exact with the reference's) on layer 0, same cache"}
+
+    for i in range(max(args.warmup, layers)):
+        step(i % layers)
+    hip.sync()
+    graph, _ = hip.capture(stream, lambda: [step(l) for l in range(layers)])
+    for _ in range(2):
+        hip.launch_graph(graph, stream)
+    hip.sync()
+    reps = max(3, args.steps // layers)
+    ms_step = timed(hip, stream, reps, lambda: hip.launch_graph(graph, stream)) / layers
+    hip.sync()
+    step_bytes = layer_bytes + kv_bytes
+    achieved = step_bytes / (ms_step * 1e-3) / 1e9
+    line = {
+        "metric": "Q8 GQA attention layer (projections + norm + RoPE + append + attend) tokens/sec at 8B shape, "
+                  "ctx 4096, batch 1, 1 GPU",
+        "value": 1e3 / ms_step, "unit": "tokens/s", "n_gpus": 1, "steps": reps * layers, "warmup": args.warmup,
+        "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": (f"attention_layer for one token: project_qkv, q/k RMSNorm + RoPE + KV append + "
+                                f"attend over 4096 cached tokens, project_output; 32q/8kv/hd128, hidden 4096; "
+                                f"{layers} layers' weights and caches rotated "
+                                f"({layers * (layer_bytes + kv_bytes) / 1e6:.0f} MB), HIP graph of {layers} steps"),
+                   "hidden": hidden, "context": T, "n_q_heads": nq, "n_kv_heads": nkv, "head_dim": hd,
+                   "bytes_per_step": step_bytes, "layers_rotated": layers},
+        "us_per_layer": ms_step * 1e3,
+        "attention_tokens_per_s_32_layers": 1e3 / ms_step / 32,
+        "parity": parity,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "gemv_q8_kernel (project_qkv) + decode3_kernel<128, 4, 4> (norm step) + "
+                               "gemv_q8_kernel (project_output): one layer step",
+                     "kernel_ms": ms_step, "algorithmic_bytes": step_bytes},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_leg_layer(nq, nkv, hd, hidden, T, theta, eps, host_w, qn, kn, xn,
+                                             args.cpu_budget)
+    for kv in kvs:
+        kv.close()
+    big.free()
+    return line
+
+
+def cpu_leg_layer(nq, nkv, hd, hidden, T, theta, eps, host_w, qn, kn, xn, budget_s: float):
+    """The reference's own attention_layer (oracle/_ref: AVX2 matmuls, OpenMP) at
+    position T-1 over a full cache, rotating 8 layers of weights and caches."""
+    from oracle.binding import Oracle, Ref, ptr
+    oracle = Oracle()
+    nb = hd // QK
+    if Ref.available():
+        kind, ref = "reference", Ref()
+        isa = ref.isa()
+
+        def fn(w, kc, vc):
+            return ref.lib.tqref_layer_run(nq, nkv, hd, hidden, theta, eps, ptr(w[0]), ptr(w[1]), ptr(w[2]),
+                                           ptr(w[3]), ptr(qn), ptr(kn), ptr(kc), ptr(vc), T, T - 1, ptr(xn),
+                                           ptr(scores), ptr(out))
+    else:
+        kind, isa = "port", "scalar"
+
+        def fn(w, kc, vc):
+            return oracle.attention_layer(w + (qn, kn), nq, nkv, hd, hidden, theta, eps, kc, vc, T, T - 1, xn)[0]
+    scores = np.zeros(nq * T, np.float32)
+    out = np.zeros(hidden, np.float32)
+    layers = 8
+    rng = np.random.default_rng(2)
+    sets = []
+    for _ in range(layers):
+        kc = oracle.quantize_row_q8(rng.standard_normal(nkv * T * hd, dtype=np.float32))
+        vc = oracle.quantize_row_q8(rng.standard_normal(nkv * T * hd, dtype=np.float32))
+        sets.append((tuple(w.copy() for w in host_w), kc, vc))
+    for l in range(2):
+        fn(*sets[l])
+    times = []
+    t_start = time.perf_counter()
+    i = 0
+    while (time.perf_counter() - t_start < budget_s and i < 100000) or i < 5:
+        t0 = time.perf_counter()
+        assert fn(*sets[i % layers]) == 0
+        times.append(time.perf_counter() - t0)
+        i += 1
+    med = float(np.median(times))
+    omp = int(os.environ.get("OMP_NUM_THREADS", str(os.cpu_count() or 1)))
+    return {"value": 1.0 / med, "unit": "tokens/s", "cores": min(omp, os.cpu_count() or 1) if kind == "reference" else 1,
+            "kind": kind,
+            "sample": (f"{len(times)} single-token attention_layer calls at position {T - 1} ({nq}q/{nkv}kv/hd{hd}, "
+                       f"hidden {hidden}) rotating {layers} layers of weights and caches, median {med * 1e3:.3f} ms; "
+                       f"{isa} matmuls, OpenMP (OMP_NUM_THREADS={omp}, nproc={os.cpu_count()})")}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -720,7 +882,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--config", default="decode-8b-4k",
                     choices=["decode-8b-4k", "decode-batched", "prefill-2k", "decode-70b-32k", "project-8b",
-                             "project-70b"])
+                             "project-70b", "layer-8b"])
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
@@ -745,8 +907,8 @@ def main():
     else:
         line = {"decode-batched": bench_decode_batched, "prefill-2k": bench_prefill_2k,
                 "decode-70b-32k": bench_decode_70b, "project-8b": bench_project_8b,
-                "project-70b": bench_project_70b}[args.config](args, nat, hip)
-    if args.config.startswith(("decode", "project")):
+                "project-70b": bench_project_70b, "layer-8b": bench_layer_8b}[args.config](args, nat, hip)
+    if args.config.startswith(("decode", "project", "layer")):
         # the achievable read rate of this box, beside the 8 TB/s spec peak
         peak = measure_hbm_read(nat, hip)
         line["roofline"]["measured_peak"] = peak
