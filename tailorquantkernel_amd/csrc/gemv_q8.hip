@@ -121,6 +121,7 @@ struct GemvArgs {
 };
 
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 // 16 bytes from each active lane's global address into LDS at dst + 16*lane
 // (global_load_lds_dwordx4; M0 holds the LDS byte address and is restored;
@@ -324,6 +325,166 @@ size_t lds_bytes(int t, int nb, bool xf) {
     return (size_t)t * nb * kBlockBytes + (xf ? (size_t)t * nb * kQK * 4 : 0);
 }
 
+// ---------------------------------------------------------------------------
+// Many tokens: int8 MFMA GEMM.  A work-group computes a 128-row x 64-token
+// tile; wave w owns rows 32w..32w+31 of it (two 16-row tiles) for all 64
+// tokens (four 16-token tiles).  The K dimension goes 4 blocks (128 codes) per
+// stage through two LDS buffers filled by direct-to-LDS copies, the next
+// stage's copies in flight while the current stage is multiplied.  Per block,
+// v_mfma_i32_16x16x32_i8 gives the exact int32 block dot for a 16 x 16 tile,
+// and each lane folds its four into fp32 with fma(s, w_d * x_d, acc): one
+// fp32 scaling per (row, token, block), the reference's per-block product
+// (kernel/q8_scalar.c:9-11) with one rounding fewer, summed over blocks in
+// order.
+//
+// LDS per stage (27,136 B):
+//   A   [4 blocks][2 halves][128 rows][16 B]   weight codes, one copy per 16 B
+//   WD  [4 blocks][128 rows] fp32             weight scales
+//   B   [64 tokens][4 blocks x 36 B]          the tokens' block_q8, as stored
+constexpr int kGemmRows = 128, kGemmToks = 64, kGemmKB = 4;
+constexpr int kGemmA = kGemmKB * 2 * kGemmRows * 16;            // 16,384
+constexpr int kGemmWD = kGemmKB * kGemmRows * 4;                // 2,048
+constexpr int kGemmBRow = kGemmKB * kBlockBytes;                // 144 bytes per token
+constexpr int kGemmB = kGemmToks * kGemmBRow;                   // 9,216
+constexpr int kGemmStage = kGemmA + kGemmWD + kGemmB;           // 27,648 (16-byte multiple)
+constexpr int kGemmBWords = kGemmB / 4;                         // 2,304 dword copies
+
+__device__ __forceinline__ long lds_pair(const unsigned char *p) {
+    const uint32_t lo = *reinterpret_cast<const uint32_t *>(p);
+    const uint32_t hi = *reinterpret_cast<const uint32_t *>(p + 4);
+    return (long)(((unsigned long)hi << 32) | lo);
+}
+
+__global__ __launch_bounds__(256) void gemm_q8_kernel(GemvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int cols = a.cols, nb = a.nb;
+    const int row0 = blockIdx.x * kGemmRows, tok0 = blockIdx.y * kGemmToks;
+    const int stages = (nb + kGemmKB - 1) / kGemmKB;
+
+    // The rows this thread copies codes and scales for (fixed over stages):
+    // A chunk c = tid + 256 j -> (block c / 256, half (c / 128) & 1, row c % 128),
+    // so row = tid % 128 and (block, half) = (j*2 + tid/128) split; WD dword
+    // c = tid + 256 j -> (block c / 128, row c % 128).
+    const int my_row = tid & 127;
+    const unsigned char *wrow;
+    const float *drow;
+    {
+        const int r = row0 + my_row < a.rows_total ? row0 + my_row : a.rows_total - 1;
+        const bool s0 = r < a.seg_end[0], s1 = !s0 && r < a.seg_end[1];
+        const unsigned char *w = s0 ? a.seg[0].w : (s1 ? a.seg[1].w : a.seg[2].w);
+        const int rows = s0 ? a.seg[0].rows : (s1 ? a.seg[1].rows : a.seg[2].rows);
+        const int lr = r - (s0 ? 0 : (s1 ? a.seg_end[0] : a.seg_end[1]));
+        wrow = w + (size_t)lr * cols;
+        drow = reinterpret_cast<const float *>(w + (size_t)rows * cols) + (size_t)lr * nb;
+    }
+
+    auto issue = [&](int st, unsigned char *buf) {
+        const int b0 = st * kGemmKB;
+        // A: 4 chunks per thread
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int c = tid + 256 * j;
+            const int blk = c >> 8, half = (c >> 7) & 1;
+            const int b = b0 + blk < nb ? b0 + blk : nb - 1;
+            dma16(wrow + tiled_offset(nb, b, 16 * half), buf + 16 * (c - lane));
+        }
+        // WD: 2 dwords per thread
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int c = tid + 256 * j;
+            const int blk = c >> 7;
+            const int b = b0 + blk < nb ? b0 + blk : nb - 1;
+            dma4(drow + b, buf + kGemmA + 4 * (c - lane));
+        }
+        // B: 9 dwords per thread, token-major, 36 dwords per token
+#pragma unroll
+        for (int j = 0; j < kGemmBWords / 256; j++) {
+            const int c = tid + 256 * j;
+            const int tk = c / (kGemmBRow / 4), w = c - tk * (kGemmBRow / 4);
+            const int blk = w / 9;
+            const int t = tok0 + tk < a.n_tok ? tok0 + tk : a.n_tok - 1;
+            const int b = b0 + blk < nb ? b0 + blk : nb - 1;
+            dma4(a.xq + ((size_t)t * nb + b) * kBlockBytes + 4 * (w - 9 * blk),
+                 buf + kGemmA + kGemmWD + 4 * (c - lane));
+        }
+    };
+
+    float acc[2][4][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[rt][tt][i] = 0.0f;
+
+    issue(0, smem);
+    for (int st = 0; st < stages; st++) {
+        unsigned char *buf = smem + (st & 1) * kGemmStage;
+        wait_vm<0>();
+        __syncthreads();   // stage st is in LDS everywhere; stage st-1's buffer is free
+        if (st + 1 < stages) issue(st + 1, smem + ((st + 1) & 1) * kGemmStage);
+        const unsigned char *A = buf, *WD = buf + kGemmA, *B = buf + kGemmA + kGemmWD;
+        // one block at a time keeps eight MFMA results live, not thirty-two
+#pragma unroll 1
+        for (int blk = 0; blk < kGemmKB; blk++) {
+            const bool valid = st * kGemmKB + blk < nb;
+            long av[2], bv[4];
+            float wd[2][4], xd[4];
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++) {
+                const int row = 32 * wave + 16 * rt;
+                av[rt] = lds_pair(A + (((blk * 2 + (lg >> 1)) * kGemmRows) + row + l16) * 16 + 8 * (lg & 1));
+                const float4 w4 = *reinterpret_cast<const float4 *>(WD + (blk * kGemmRows + row + 4 * lg) * 4);
+                wd[rt][0] = w4.x; wd[rt][1] = w4.y; wd[rt][2] = w4.z; wd[rt][3] = w4.w;
+            }
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++) {
+                const unsigned char *tb = B + (16 * tt + l16) * kGemmBRow + blk * kBlockBytes;
+                bv[tt] = lds_pair(tb + 4 + 8 * lg);
+                xd[tt] = valid ? *reinterpret_cast<const float *>(tb) : 0.0f;
+            }
+            // all eight products first, so that each one's latency hides
+            // under the others before its results are read
+            v4i c[2][4];
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++)
+                    c[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[rt], bv[tt], v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        acc[rt][tt][i] = fmaf((float)c[rt][tt][i], wd[rt][i] * xd[tt], acc[rt][tt][i]);
+        }
+    }
+
+    // y[t][r]: lane (l16, lg) holds rows 4lg..4lg+3 of each 16-row tile for
+    // token l16 of each 16-token tile.
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = row0 + 32 * wave + 16 * rt + 4 * lg + i;
+            if (r >= a.rows_total) continue;
+            const bool s0 = r < a.seg_end[0], s1 = !s0 && r < a.seg_end[1];
+            float *y = s0 ? a.seg[0].y : (s1 ? a.seg[1].y : a.seg[2].y);
+            const int rows = s0 ? a.seg[0].rows : (s1 ? a.seg[1].rows : a.seg[2].rows);
+            const int lr = r - (s0 ? 0 : (s1 ? a.seg_end[0] : a.seg_end[1]));
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++) {
+                const int t = tok0 + 16 * tt + l16;
+                if (t < a.n_tok) y[(size_t)t * rows + lr] = acc[rt][tt][i];
+            }
+        }
+    }
+}
+
 int env_int(const char *name, int dflt) {
     const char *s = getenv(name);
     return (s && *s) ? atoi(s) : dflt;
@@ -399,10 +560,30 @@ hipError_t launch_gemv(const GemvArgs &a, int tcap, bool xf, int rw, int gc, hip
     }
 }
 
-// Runs the matmul over all tokens, in launches of up to tmax tokens.  With
-// fp32 input (a.x) each launch quantizes its rows in LDS.
+// From this many tokens on (block_q8 input) the MFMA GEMM runs instead of
+// GEMV launches of up to 8 tokens (TQ_HIP_GEMM_MIN_TOKENS overrides).
+int gemm_min_tokens() {
+    const int v = env_int("TQ_HIP_GEMM_MIN_TOKENS", 0);
+    return v > 0 ? v : 16;
+}
+
+hipError_t launch_gemm(const GemvArgs &a, hipStream_t s) {
+    const dim3 grid((a.rows_total + kGemmRows - 1) / kGemmRows, (a.n_tok + kGemmToks - 1) / kGemmToks);
+    hipLaunchKernelGGL(gemm_q8_kernel, grid, dim3(kThreads), 2 * kGemmStage, s, a);
+    return hipGetLastError();
+}
+
+// Runs the matmul over all tokens: one GEMM launch for many block_q8 rows,
+// else GEMV launches of up to tmax tokens.  With fp32 input (a.x) each GEMV
+// launch quantizes its rows in LDS.
 int run_gemv(GemvArgs a, int n_tok, hipStream_t s) {
     const bool xf = a.x != nullptr;
+    if (!xf && n_tok >= gemm_min_tokens()) {
+        if ((size_t)n_tok * a.nb > (size_t)INT32_MAX / kBlockBytes || (n_tok + kGemmToks - 1) / kGemmToks > 65535)
+            return TQ_HIP_EINVAL;
+        a.n_tok = n_tok;
+        return herr(launch_gemm(a, s));
+    }
     const int tmax = pick_tokens(a.nb, xf);
     if (tmax == 0) return TQ_HIP_EINVAL;
     const int rw = pick_rw(a.rows_total);

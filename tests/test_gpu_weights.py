@@ -52,14 +52,19 @@ def rel_err(a, b) -> float:
 
 
 def abs_terms(Wq, xq, rows, cols, n_tok):
-    """sum_b |s_b * w_d * x_d| in fp64, shape [n_tok, rows]."""
+    """sum_b |s_b * w_d * x_d| in fp64, shape [n_tok, rows] (a few tokens at a time)."""
     nb = cols // QK
-    wq = Wq["q"].reshape(rows, nb, QK).astype(np.float64)
-    xqq = xq["q"].reshape(n_tok, nb, QK).astype(np.float64)
-    s = np.einsum("rbj,tbj->trb", wq, xqq)
+    wq = Wq["q"].reshape(rows, nb, QK).astype(np.float32)
+    xqq = xq["q"].reshape(n_tok, nb, QK).astype(np.float32)
     wd = np.abs(Wq["d"].reshape(rows, nb).astype(np.float64))
     xd = np.abs(xq["d"].reshape(n_tok, nb).astype(np.float64))
-    return (np.abs(s) * wd[None] * xd[:, None, :]).sum(-1)
+    out = np.empty((n_tok, rows))
+    step = max(1, (1 << 24) // (rows * nb))
+    for t0 in range(0, n_tok, step):
+        # int8 x int8 block dots are exact in fp32 (|s| <= 32 * 127^2 < 2^24)
+        s = np.einsum("rbj,tbj->trb", wq, xqq[t0:t0 + step]).astype(np.float64)
+        out[t0:t0 + step] = (np.abs(s) * wd[None] * xd[t0:t0 + step, None, :]).sum(-1)
+    return out
 
 
 def check_matmul(gpu, ref, Wq, xq, rows, cols, n_tok, what):
@@ -174,12 +179,31 @@ def test_matmul_vs_oracle(nat, oracle, rows, cols, n_tok):
     y = gpu_matmul(nat, M, xq, n_tok)
     ref = oracle.matmul_q8(Wq, xq, rows, cols, n_tok)
     check_matmul(y, ref, Wq, xq, rows, cols, n_tok, f"{rows}x{cols} n_tok={n_tok}")
-    if n_tok > 1:
+    if 1 < n_tok < 16:
         # a token's row does not depend on the rest of the batch
         nb = cols // QK
         for t in (0, n_tok - 1):
             y1 = gpu_matmul(nat, M, xq[t * nb:(t + 1) * nb], 1)
             assert y1.tobytes() == y[t:t + 1].tobytes()
+
+
+@pytest.mark.parametrize("rows,cols,n_tok", [(256, 512, 16), (1027, 96, 17), (7, 64, 64), (10, 32, 65),
+                                             (4096, 4096, 256), (100, 2080, 100), (1024, 8192, 300),
+                                             (6144, 4096, 192)])
+def test_gemm_vs_oracle(nat, oracle, rows, cols, n_tok):
+    """From 16 tokens on the MFMA GEMM runs: ragged row, token and block tails."""
+    Wq = random_weights(oracle, rows, cols, 3 * rows + cols)
+    rng = np.random.default_rng(rows + cols + n_tok)
+    x = rng.standard_normal((n_tok, cols)).astype(np.float32)
+    xq = quantize_tokens(oracle, x, n_tok, cols)
+    M = Matrix(nat, Wq, rows, cols)
+    y = gpu_matmul(nat, M, xq, n_tok)
+    ref = oracle.matmul_q8(Wq, xq, rows, cols, n_tok)
+    check_matmul(y, ref, Wq, xq, rows, cols, n_tok, f"gemm {rows}x{cols} n_tok={n_tok}")
+    # a token's row does not depend on the rest of the batch
+    nb = cols // QK
+    y16 = gpu_matmul(nat, M, xq[:16 * nb], 16)
+    assert y16.tobytes() == y[:16].tobytes()
 
 
 @pytest.mark.parametrize("rw", ["1", "2", "4"])
@@ -213,7 +237,8 @@ def test_unaligned_activation_rows(nat, oracle):
 
 @pytest.mark.parametrize("nq,nkv,hd,hidden,n_tok", [(32, 8, 128, 4096, 1), (32, 8, 128, 4096, 4),
                                                     (8, 2, 64, 256, 3), (6, 2, 32, 160, 1),
-                                                    (64, 8, 128, 8192, 1)])
+                                                    (64, 8, 128, 8192, 1), (32, 8, 128, 4096, 40),
+                                                    (8, 2, 64, 256, 130)])
 def test_project_qkv_and_output(nat, oracle, nq, nkv, hd, hidden, n_tok):
     lib = nat.load()
     qr, kr = nq * hd, nkv * hd
