@@ -326,28 +326,47 @@ size_t lds_bytes(int t, int nb, bool xf) {
 }
 
 // ---------------------------------------------------------------------------
-// Many tokens: int8 MFMA GEMM.  A work-group computes a 128-row x 64-token
-// tile; wave w owns rows 32w..32w+31 of it (two 16-row tiles) for all 64
-// tokens (four 16-token tiles).  The K dimension goes 4 blocks (128 codes) per
-// stage through two LDS buffers filled by direct-to-LDS copies, the next
-// stage's copies in flight while the current stage is multiplied.  Per block,
+// Many tokens: int8 MFMA GEMM.  A work-group of 8 waves computes a 128-row x
+// 128-token tile; wave w owns rows 32(w%4)..+31 (two 16-row tiles) of tokens
+// 64(w/4)..+63 (four 16-token tiles).  The K dimension goes 4 blocks (128
+// codes) per stage through three LDS buffers filled by direct-to-LDS copies,
+// two stages ahead of the one being multiplied.  Per block,
 // v_mfma_i32_16x16x32_i8 gives the exact int32 block dot for a 16 x 16 tile,
 // and each lane folds its four into fp32 with fma(s, w_d * x_d, acc): one
 // fp32 scaling per (row, token, block), the reference's per-block product
 // (kernel/q8_scalar.c:9-11) with one rounding fewer, summed over blocks in
 // order.
 //
-// LDS per stage (27,136 B):
+// Tile order: work-groups are dealt to the 8 XCDs round-robin, so the grid is
+// laid out so that every token tile of one row tile runs on the same XCD
+// (work-group w: XCD w % 8, row tile 8 (w/8 / n_tt) + w % 8) and the tile's
+// 128 weight rows are read from HBM once into that XCD's L2.
+//
+// LDS per stage (43,008 B):
 //   A   [4 blocks][2 halves][128 rows][16 B]   weight codes, one copy per 16 B
 //   WD  [4 blocks][128 rows] fp32             weight scales
-//   B   [64 tokens][4 blocks x 36 B]          the tokens' block_q8, as stored
-constexpr int kGemmRows = 128, kGemmToks = 64, kGemmKB = 4;
+//   B   [128 tokens][4 blocks x 36 B]         the tokens' block_q8, as stored:
+//       with 16-byte aligned rows and a block count that is a multiple of 4,
+//       a token's 144 bytes are nine 16-byte copies (three rounds of 512, the
+//       last round's surplus copies land in 6 KB of padding so every wave
+//       issues the same count); otherwise 36 dword copies per token.
+constexpr int kGemmThreads = 512;
+constexpr int kGemmRows = 128, kGemmToks = 128, kGemmKB = 4, kGemmBufs = 3;
 constexpr int kGemmA = kGemmKB * 2 * kGemmRows * 16;            // 16,384
 constexpr int kGemmWD = kGemmKB * kGemmRows * 4;                // 2,048
 constexpr int kGemmBRow = kGemmKB * kBlockBytes;                // 144 bytes per token
-constexpr int kGemmB = kGemmToks * kGemmBRow;                   // 9,216
-constexpr int kGemmStage = kGemmA + kGemmWD + kGemmB;           // 27,648 (16-byte multiple)
-constexpr int kGemmBWords = kGemmB / 4;                         // 2,304 dword copies
+constexpr int kGemmB = kGemmToks * kGemmBRow;                   // 18,432
+constexpr int kGemmBChunks = kGemmB / 16;                       // 1,152 16-byte copies
+constexpr int kGemmBRounds = (kGemmBChunks + kGemmThreads - 1) / kGemmThreads;   // 3
+constexpr int kGemmBPad = kGemmBRounds * kGemmThreads * 16;     // 24,576
+constexpr int kGemmStage = kGemmA + kGemmWD + kGemmBPad;        // 43,008 (16-byte multiple)
+constexpr int kGemmBWords = kGemmB / 4;                         // 4,608 dword copies
+// copies per thread per stage: A, WD, then B by 16 bytes or by dwords
+constexpr int kGemmCopiesX4 = kGemmA / 16 / kGemmThreads + kGemmWD / 4 / kGemmThreads + kGemmBRounds;
+constexpr int kGemmCopiesX1 = kGemmA / 16 / kGemmThreads + kGemmWD / 4 / kGemmThreads +
+                              kGemmBWords / kGemmThreads;
+static_assert(kGemmA / 16 % kGemmThreads == 0 && kGemmWD / 4 % kGemmThreads == 0 &&
+              kGemmBWords % kGemmThreads == 0, "whole copy rounds per stage");
 
 __device__ __forceinline__ long lds_pair(const unsigned char *p) {
     const uint32_t lo = *reinterpret_cast<const uint32_t *>(p);
@@ -355,19 +374,26 @@ __device__ __forceinline__ long lds_pair(const unsigned char *p) {
     return (long)(((unsigned long)hi << 32) | lo);
 }
 
-__global__ __launch_bounds__(256) void gemm_q8_kernel(GemvArgs a) {
+// BX4: the activation rows are 16-byte aligned and nb % 4 == 0.
+template <bool BX4>
+__global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
+    constexpr int kCopies = BX4 ? kGemmCopiesX4 : kGemmCopiesX1;
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, lg = lane >> 4;
     const int cols = a.cols, nb = a.nb;
-    const int row0 = blockIdx.x * kGemmRows, tok0 = blockIdx.y * kGemmToks;
+    const int n_tt = (a.n_tok + kGemmToks - 1) / kGemmToks;
+    const int n_rt = (a.rows_total + kGemmRows - 1) / kGemmRows;
+    const int k = blockIdx.x >> 3;
+    const int rt = (k / n_tt) * 8 + (blockIdx.x & 7), tt = k % n_tt;
+    if (rt >= n_rt) return;   // the padding of the last row of XCD groups
+    const int row0 = rt * kGemmRows, tok0 = tt * kGemmToks;
     const int stages = (nb + kGemmKB - 1) / kGemmKB;
+    const int wr = 32 * (wave & 3), wt = 64 * (wave >> 2);
 
-    // The rows this thread copies codes and scales for (fixed over stages):
-    // A chunk c = tid + 256 j -> (block c / 256, half (c / 128) & 1, row c % 128),
-    // so row = tid % 128 and (block, half) = (j*2 + tid/128) split; WD dword
-    // c = tid + 256 j -> (block c / 128, row c % 128).
+    // A chunk c = tid + 512 j -> (block c / 256, half (c / 128) & 1, row c % 128):
+    // row = tid % 128 for every j; WD dword c = tid -> (block c / 128, row c % 128).
     const int my_row = tid & 127;
     const unsigned char *wrow;
     const float *drow;
@@ -381,105 +407,120 @@ __global__ __launch_bounds__(256) void gemm_q8_kernel(GemvArgs a) {
         drow = reinterpret_cast<const float *>(w + (size_t)rows * cols) + (size_t)lr * nb;
     }
 
+    // kGemmCopies direct-to-LDS copies per thread per stage, nothing else
     auto issue = [&](int st, unsigned char *buf) {
         const int b0 = st * kGemmKB;
-        // A: 4 chunks per thread
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int c = tid + 256 * j;
+        for (int j = 0; j < kGemmA / 16 / kGemmThreads; j++) {
+            const int c = tid + kGemmThreads * j;
             const int blk = c >> 8, half = (c >> 7) & 1;
             const int b = b0 + blk < nb ? b0 + blk : nb - 1;
             dma16(wrow + tiled_offset(nb, b, 16 * half), buf + 16 * (c - lane));
         }
-        // WD: 2 dwords per thread
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int c = tid + 256 * j;
-            const int blk = c >> 7;
+        {
+            const int blk = tid >> 7;
             const int b = b0 + blk < nb ? b0 + blk : nb - 1;
-            dma4(drow + b, buf + kGemmA + 4 * (c - lane));
+            dma4(drow + b, buf + kGemmA + 4 * (tid - lane));
         }
-        // B: 9 dwords per thread, token-major, 36 dwords per token
+        if (BX4) {
 #pragma unroll
-        for (int j = 0; j < kGemmBWords / 256; j++) {
-            const int c = tid + 256 * j;
-            const int tk = c / (kGemmBRow / 4), w = c - tk * (kGemmBRow / 4);
-            const int blk = w / 9;
-            const int t = tok0 + tk < a.n_tok ? tok0 + tk : a.n_tok - 1;
-            const int b = b0 + blk < nb ? b0 + blk : nb - 1;
-            dma4(a.xq + ((size_t)t * nb + b) * kBlockBytes + 4 * (w - 9 * blk),
-                 buf + kGemmA + kGemmWD + 4 * (c - lane));
+            for (int j = 0; j < kGemmBRounds; j++) {
+                const int c = tid + kGemmThreads * j;
+                // copies past the tile fetch a real slice into the padding
+                const int cc = c < kGemmBChunks ? c : kGemmBChunks - 1;
+                const int tk = cc / 9, piece = cc - 9 * tk;
+                const int t = tok0 + tk < a.n_tok ? tok0 + tk : a.n_tok - 1;
+                dma16(a.xq + ((size_t)t * nb + b0) * kBlockBytes + 16 * piece,
+                      buf + kGemmA + kGemmWD + 16 * (c - lane));
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kGemmBWords / kGemmThreads; j++) {
+                const int c = tid + kGemmThreads * j;
+                const int tk = c / (kGemmBRow / 4), w = c - tk * (kGemmBRow / 4);
+                const int blk = w / 9;
+                const int t = tok0 + tk < a.n_tok ? tok0 + tk : a.n_tok - 1;
+                const int b = b0 + blk < nb ? b0 + blk : nb - 1;
+                dma4(a.xq + ((size_t)t * nb + b) * kBlockBytes + 4 * (w - 9 * blk),
+                     buf + kGemmA + kGemmWD + 4 * (c - lane));
+            }
         }
     };
 
     float acc[2][4][4];
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++)
+    for (int r2 = 0; r2 < 2; r2++)
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++)
+        for (int t4 = 0; t4 < 4; t4++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[rt][tt][i] = 0.0f;
+            for (int i = 0; i < 4; i++) acc[r2][t4][i] = 0.0f;
 
     issue(0, smem);
+    if (stages > 1) issue(1, smem + kGemmStage);
     for (int st = 0; st < stages; st++) {
-        unsigned char *buf = smem + (st & 1) * kGemmStage;
-        wait_vm<0>();
+        unsigned char *buf = smem + (st % kGemmBufs) * kGemmStage;
+        // stage st has landed once at most the next stage's copies are in flight
+        if (st + 1 < stages)
+            wait_vm<kCopies>();
+        else
+            wait_vm<0>();
         __syncthreads();   // stage st is in LDS everywhere; stage st-1's buffer is free
-        if (st + 1 < stages) issue(st + 1, smem + ((st + 1) & 1) * kGemmStage);
+        if (st + 2 < stages) issue(st + 2, smem + ((st + 2) % kGemmBufs) * kGemmStage);
         const unsigned char *A = buf, *WD = buf + kGemmA, *B = buf + kGemmA + kGemmWD;
-        // one block at a time keeps eight MFMA results live, not thirty-two
-#pragma unroll 1
+        // two blocks at a time: the second block's LDS reads and products
+        // overlap the first one's scaling
+#pragma unroll 2
         for (int blk = 0; blk < kGemmKB; blk++) {
             const bool valid = st * kGemmKB + blk < nb;
             long av[2], bv[4];
             float wd[2][4], xd[4];
 #pragma unroll
-            for (int rt = 0; rt < 2; rt++) {
-                const int row = 32 * wave + 16 * rt;
-                av[rt] = lds_pair(A + (((blk * 2 + (lg >> 1)) * kGemmRows) + row + l16) * 16 + 8 * (lg & 1));
+            for (int r2 = 0; r2 < 2; r2++) {
+                const int row = wr + 16 * r2;
+                av[r2] = lds_pair(A + (((blk * 2 + (lg >> 1)) * kGemmRows) + row + l16) * 16 + 8 * (lg & 1));
                 const float4 w4 = *reinterpret_cast<const float4 *>(WD + (blk * kGemmRows + row + 4 * lg) * 4);
-                wd[rt][0] = w4.x; wd[rt][1] = w4.y; wd[rt][2] = w4.z; wd[rt][3] = w4.w;
+                wd[r2][0] = w4.x; wd[r2][1] = w4.y; wd[r2][2] = w4.z; wd[r2][3] = w4.w;
             }
 #pragma unroll
-            for (int tt = 0; tt < 4; tt++) {
-                const unsigned char *tb = B + (16 * tt + l16) * kGemmBRow + blk * kBlockBytes;
-                bv[tt] = lds_pair(tb + 4 + 8 * lg);
-                xd[tt] = valid ? *reinterpret_cast<const float *>(tb) : 0.0f;
+            for (int t4 = 0; t4 < 4; t4++) {
+                const unsigned char *tb = B + (wt + 16 * t4 + l16) * kGemmBRow + blk * kBlockBytes;
+                bv[t4] = lds_pair(tb + 4 + 8 * lg);
+                xd[t4] = valid ? *reinterpret_cast<const float *>(tb) : 0.0f;
             }
             // all eight products first, so that each one's latency hides
             // under the others before its results are read
             v4i c[2][4];
 #pragma unroll
-            for (int rt = 0; rt < 2; rt++)
+            for (int r2 = 0; r2 < 2; r2++)
 #pragma unroll
-                for (int tt = 0; tt < 4; tt++)
-                    c[rt][tt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[rt], bv[tt], v4i{0, 0, 0, 0}, 0, 0, 0);
+                for (int t4 = 0; t4 < 4; t4++)
+                    c[r2][t4] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[r2], bv[t4], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-            for (int rt = 0; rt < 2; rt++)
+            for (int r2 = 0; r2 < 2; r2++)
 #pragma unroll
-                for (int tt = 0; tt < 4; tt++)
+                for (int t4 = 0; t4 < 4; t4++)
 #pragma unroll
                     for (int i = 0; i < 4; i++)
-                        acc[rt][tt][i] = fmaf((float)c[rt][tt][i], wd[rt][i] * xd[tt], acc[rt][tt][i]);
+                        acc[r2][t4][i] = fmaf((float)c[r2][t4][i], wd[r2][i] * xd[t4], acc[r2][t4][i]);
         }
     }
 
     // y[t][r]: lane (l16, lg) holds rows 4lg..4lg+3 of each 16-row tile for
     // token l16 of each 16-token tile.
 #pragma unroll
-    for (int rt = 0; rt < 2; rt++) {
+    for (int r2 = 0; r2 < 2; r2++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int r = row0 + 32 * wave + 16 * rt + 4 * lg + i;
+            const int r = row0 + wr + 16 * r2 + 4 * lg + i;
             if (r >= a.rows_total) continue;
             const bool s0 = r < a.seg_end[0], s1 = !s0 && r < a.seg_end[1];
             float *y = s0 ? a.seg[0].y : (s1 ? a.seg[1].y : a.seg[2].y);
             const int rows = s0 ? a.seg[0].rows : (s1 ? a.seg[1].rows : a.seg[2].rows);
             const int lr = r - (s0 ? 0 : (s1 ? a.seg_end[0] : a.seg_end[1]));
 #pragma unroll
-            for (int tt = 0; tt < 4; tt++) {
-                const int t = tok0 + 16 * tt + l16;
-                if (t < a.n_tok) y[(size_t)t * rows + lr] = acc[rt][tt][i];
+            for (int t4 = 0; t4 < 4; t4++) {
+                const int t = tok0 + wt + 16 * t4 + l16;
+                if (t < a.n_tok) y[(size_t)t * rows + lr] = acc[r2][t4][i];
             }
         }
     }
@@ -568,8 +609,24 @@ int gemm_min_tokens() {
 }
 
 hipError_t launch_gemm(const GemvArgs &a, hipStream_t s) {
-    const dim3 grid((a.rows_total + kGemmRows - 1) / kGemmRows, (a.n_tok + kGemmToks - 1) / kGemmToks);
-    hipLaunchKernelGGL(gemm_q8_kernel, grid, dim3(kThreads), 2 * kGemmStage, s, a);
+    const int n_rt = (a.rows_total + kGemmRows - 1) / kGemmRows;
+    const int n_tt = (a.n_tok + kGemmToks - 1) / kGemmToks;
+    const long groups = ((long)n_rt + 7) / 8;   // row tiles per XCD, rounded up
+    const long grid = groups * 8 * n_tt;
+    if (grid > INT32_MAX) return hipErrorInvalidValue;
+    const size_t lds = (size_t)kGemmBufs * kGemmStage;
+    static bool opted = false;
+    if (!opted) {
+        for (const void *f : {(const void *)gemm_q8_kernel<true>, (const void *)gemm_q8_kernel<false>}) {
+            const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
+        opted = true;
+    }
+    if ((((uintptr_t)a.xq & 15) == 0) && a.nb % kGemmKB == 0)
+        hipLaunchKernelGGL(gemm_q8_kernel<true>, dim3((unsigned)grid), dim3(kGemmThreads), lds, s, a);
+    else
+        hipLaunchKernelGGL(gemm_q8_kernel<false>, dim3((unsigned)grid), dim3(kGemmThreads), lds, s, a);
     return hipGetLastError();
 }
 
@@ -579,8 +636,7 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t s) {
 int run_gemv(GemvArgs a, int n_tok, hipStream_t s) {
     const bool xf = a.x != nullptr;
     if (!xf && n_tok >= gemm_min_tokens()) {
-        if ((size_t)n_tok * a.nb > (size_t)INT32_MAX / kBlockBytes || (n_tok + kGemmToks - 1) / kGemmToks > 65535)
-            return TQ_HIP_EINVAL;
+        if ((size_t)n_tok * a.nb > (size_t)INT32_MAX / kBlockBytes) return TQ_HIP_EINVAL;
         a.n_tok = n_tok;
         return herr(launch_gemm(a, s));
     }

@@ -218,9 +218,10 @@ def test_rows_per_wave_identical(nat, oracle, rw, monkeypatch):
     assert gpu_matmul(nat, M, xq, n_tok).tobytes() == base.tobytes()
 
 
-def test_unaligned_activation_rows(nat, oracle):
-    """block_q8 activations at a 4-byte (not 16-byte) aligned address."""
-    rows, cols, n_tok = 300, 96, 3
+@pytest.mark.parametrize("cols,n_tok", [(96, 3), (128, 20), (4096, 40)])
+def test_unaligned_activation_rows(nat, oracle, cols, n_tok):
+    """block_q8 activations at a 4-byte (not 16-byte) aligned address (GEMV and GEMM)."""
+    rows = 300
     Wq = random_weights(oracle, rows, cols, 77)
     xq = quantize_tokens(oracle, fill_random(n_tok * cols, 78, 1.0), n_tok, cols)
     M = Matrix(nat, Wq, rows, cols)
