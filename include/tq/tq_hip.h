@@ -80,6 +80,13 @@ int tq_hip_attn_accum_q8(const float *w, size_t w_stride, int g, const block_q8 
 /* model/softmax.c:4-23 softmax on `rows` rows of n values, row r at x + r*stride. */
 int tq_hip_softmax(float *x, int n, int rows, size_t stride, void *stream);
 
+/* rmsnorm (model/rmsnorm.c:4-19) of n_rows rows of n floats with one weight
+ * row, as norm_heads applies it per head (model/attention_layer.c:48-53);
+ * the squares are summed serially in element order, so the result is the
+ * reference's bit for bit.  out may equal x.  n <= 8191. */
+int tq_hip_rmsnorm_rows(const float *x, const float *weight, float *out, int n_rows, int n, float eps,
+                        void *stream);
+
 /* model/attn_q8.c:78-90 attention_head_q8: writes q_q8 (head_dim/32 blocks),
  * scores[n] (the softmax weights) and out[head_dim]. */
 int tq_hip_attention_head_q8(const float *q, block_q8 *q_q8, const block_q8 *k_cache,
@@ -219,7 +226,7 @@ int tq_hip_matmul_q8_batch(const void *W, const block_q8 *xq, float *y, int rows
                            int n_tok, void *stream);
 
 /* project_qkv for n_tok rows of xn [n_tok][hidden] (model/attention_layer.c:38-46,
- * batched :210-218): quantize_row_q8 of every row into xq_ws (n_tok*hidden/32
+ * batched :213-218): quantize_row_q8 of every row into xq_ws (n_tok*hidden/32
  * block_q8, the reference's xn_q8 / ws->xq), then q = wq.xq, k = wk.xq,
  * v = wv.xq in one launch over the concatenated rows; q [n_tok][q_rows],
  * k and v [n_tok][kv_rows].  wq is q_rows x hidden, wk and wv kv_rows x hidden. */
@@ -266,6 +273,19 @@ int tq_hip_attention_layer_async(tq_hip_kv *kv, const tq_hip_attn_weights *w, in
                                  const int32_t *d_seq, const int32_t *d_pos, int max_pos,
                                  const float *d_xn, const float *d_cos, const float *d_sin,
                                  float *d_out, void *d_ws, size_t ws_bytes, void *stream);
+
+/* attention_layer_batch (model/attention_layer.c:200-243) for tokens
+ * pos0..pos0+n-1 of sequence `seq`, all on the device: project_qkv over the n
+ * rows of d_xn [n][hidden] (the MFMA GEMM from 16 rows on), the per-head
+ * RMSNorm of q and k (tq_hip_rmsnorm_rows), RoPE + KV append + causal
+ * attention (tq_hip_prefill_async; d_cos/d_sin [n][head_dim/2] or NULL),
+ * project_output into d_out [n][hidden].  d_ws: tq_hip_attention_layer_ws_bytes
+ * bytes for n tokens, 16-byte aligned.  Returns -1 (TQ_HIP_EINVAL) for n <= 0
+ * or a range past the sequence's pages before any launch, as
+ * attention_layer_batch does (:203-204). */
+int tq_hip_attention_layer_batch_async(tq_hip_kv *kv, const tq_hip_attn_weights *w, int seq, int pos0,
+                                       int n, const float *d_xn, const float *d_cos, const float *d_sin,
+                                       float *d_out, void *d_ws, size_t ws_bytes, void *stream);
 
 /* ---- measurement: streaming-read bandwidth of device memory, the GPU
  * counterpart of the reference's host RAM probe (tools/membw.h:1-80).  Reads

@@ -278,7 +278,7 @@ void oracle_matmul_q8_batch(const block_q8 *W, const block_q8 *xq, float *y, int
 /* A projection as attention_layer makes it: quantize_row_q8 of each input
  * row, then the Q8 matmul (project_qkv for one matrix,
  * model/attention_layer.c:38-46; project_output, :161-167; the batched
- * versions quantize every token row first, :210-218 and :238-241).
+ * versions quantize every token row first, :213-218 and :238-241).
  * x: n_tok rows of cols floats; y: n_tok rows of rows floats. */
 void oracle_project_q8(const block_q8 *W, int rows, int cols, const float *x, int n_tok,
                        float *y) {

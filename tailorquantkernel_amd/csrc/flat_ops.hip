@@ -172,6 +172,50 @@ hipError_t tq_launch_accum(const float *w, size_t w_stride, int g, const block_q
     return hipGetLastError();
 }
 
+// RMSNorm of rows of n floats (model/rmsnorm.c:4-19; norm_heads,
+// model/attention_layer.c:48-53): a work-group copies R rows into LDS with
+// coalesced loads (row stride n+1, so the lanes' serial walks below fall in
+// distinct banks); lane r sums row r's squares serially in element order, as
+// the reference does; then every thread writes (x * inverse) * weight.  out
+// may be x.
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float *__restrict__ x,
+                                                           const float *__restrict__ w, float *out,
+                                                           int n_rows, int n, int rows_per_wg, float eps) {
+#pragma clang fp contract(off)
+    extern __shared__ float rows_s[];
+    const int r0 = blockIdx.x * rows_per_wg;
+    const int nr = min(rows_per_wg, n_rows - r0);
+    const int stride = n + 1;
+    float *inv_s = rows_s + rows_per_wg * stride;
+    for (int e = threadIdx.x; e < nr * n; e += 256) {
+        const int r = e / n, j = e - r * n;
+        rows_s[r * stride + j] = x[(size_t)r0 * n + e];
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < nr) {
+        const float *row = rows_s + threadIdx.x * stride;
+        float sum = 0.0f;
+        for (int j = 0; j < n; j++) sum += row[j] * row[j];
+        inv_s[threadIdx.x] = 1.0f / sqrtf(eps + sum / (float)n);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < nr * n; e += 256) {
+        const int r = e / n, j = e - r * n;
+        out[(size_t)r0 * n + e] = rows_s[r * stride + j] * inv_s[r] * w[j];
+    }
+}
+
+hipError_t tq_launch_rmsnorm_rows(const float *x, const float *w, float *out, int n_rows, int n, float eps,
+                                  hipStream_t s) {
+    if (n_rows <= 0) return hipSuccess;
+    int per = 8192 / (n + 1);
+    per = per < 1 ? 1 : (per > 64 ? 64 : per);
+    const size_t lds = ((size_t)per * (n + 1) + per) * sizeof(float);
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)((n_rows + per - 1) / per)), dim3(256), lds, s, x, w,
+                       out, n_rows, n, per, eps);
+    return hipGetLastError();
+}
+
 hipError_t tq_launch_softmax(float *x, int n, int rows, size_t stride, hipStream_t s) {
     if (n <= 0 || rows <= 0) return hipSuccess;
     hipLaunchKernelGGL(softmax_kernel, dim3(rows), dim3(256), 0, s, x, n, stride);

@@ -2,7 +2,7 @@
 // weight x Q8-activation matmul (kernel/q8_scalar.c:3-30, kernel/kernel.h:13-20)
 // and the projections around attention that use it (project_qkv and
 // project_output, model/attention_layer.c:38-46,161-167, and their batched
-// forms, :210-218,238-241).
+// forms, :213-218,238-241).
 //
 // Device weight layout ("tiled Q8"), exactly the byte count of the
 // reference's rows x cols/32 block_q8 array:

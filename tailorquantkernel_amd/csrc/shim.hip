@@ -492,6 +492,12 @@ int tq_hip_attn_accum_q8(const float *w, size_t w_stride, int g, const block_q8 
     return herr(tq_launch_accum(w, w_stride, g, v, n, nb, out, out_stride, (hipStream_t)stream));
 }
 
+int tq_hip_rmsnorm_rows(const float *x, const float *weight, float *out, int n_rows, int n, float eps,
+                        void *stream) {
+    if (n_rows < 0 || n <= 0 || n > 8191 || (n_rows > 0 && (!x || !weight || !out))) return TQ_HIP_EINVAL;
+    return herr(tq_launch_rmsnorm_rows(x, weight, out, n_rows, n, eps, (hipStream_t)stream));
+}
+
 int tq_hip_softmax(float *x, int n, int rows, size_t stride, void *stream) {
     if (n < 0 || rows < 0 || (rows > 1 && stride < (size_t)n) || (n > 0 && rows > 0 && !x))
         return TQ_HIP_EINVAL;
@@ -903,6 +909,38 @@ int tq_hip_attention_layer_async(tq_hip_kv *kv, const tq_hip_attn_weights *w, in
                                        w->rms_eps, d_cos, d_sin, attn, s);
     if (rc != TQ_HIP_OK) return rc;
     return tq_hip_project_output(w->wo, w->hidden, qd, attn, n_q, xq, d_out, s);
+}
+
+int tq_hip_attention_layer_batch_async(tq_hip_kv *kv, const tq_hip_attn_weights *w, int seq, int pos0,
+                                       int n, const float *d_xn, const float *d_cos, const float *d_sin,
+                                       float *d_out, void *d_ws, size_t ws_bytes, void *stream) {
+    if (!layer_shape_ok(kv, w, n) || !seq_ok(kv, seq) || !d_xn || !d_out || !d_ws || ((uintptr_t)d_ws & 15) ||
+        !w->wq || !w->wk || !w->wv || !w->wo || !w->q_norm || !w->k_norm ||
+        ((d_cos == nullptr) != (d_sin == nullptr)))
+        return TQ_HIP_EINVAL;
+    // model/attention_layer.c:203-204
+    if (pos0 < 0 || pos0 + n > capacity_of(kv, seq)) return TQ_HIP_EINVAL;
+    const tq_hip_kv_desc &D = kv->desc;
+    size_t oq, ok, ov, oa, ox;
+    if (ws_bytes < layer_ws(D, w->hidden, n, &oq, &ok, &ov, &oa, &ox)) return TQ_HIP_EINVAL;
+    unsigned char *ws = (unsigned char *)d_ws;
+    float *q = (float *)(ws + oq), *k = (float *)(ws + ok), *v = (float *)(ws + ov);
+    float *attn = (float *)(ws + oa);
+    block_q8 *xq = (block_q8 *)(ws + ox);
+    const int qd = D.n_q_heads * D.head_dim, kd = D.n_kv_heads * D.head_dim;
+    const hipStream_t hs = pick(kv, stream);
+    void *s = (void *)hs;
+    // :213-218 quantize every row, then the batched q/k/v projections
+    int rc = tq_hip_project_qkv(w->wq, w->wk, w->wv, qd, kd, w->hidden, d_xn, n, xq, q, k, v, s);
+    if (rc != TQ_HIP_OK) return rc;
+    // :227-228 norm_heads on every token's q and k rows
+    TQ_TRY(tq_launch_rmsnorm_rows(q, w->q_norm, q, n * D.n_q_heads, D.head_dim, w->rms_eps, hs));
+    TQ_TRY(tq_launch_rmsnorm_rows(k, w->k_norm, k, n * D.n_kv_heads, D.head_dim, w->rms_eps, hs));
+    // :230-235 RoPE, store_kv and causal attention for the n tokens
+    rc = tq_hip_prefill_async(kv, seq, pos0, n, q, k, v, d_cos, d_sin, attn, s);
+    if (rc != TQ_HIP_OK) return rc;
+    // :238-241 quantize the attention rows, then the batched output projection
+    return tq_hip_project_output(w->wo, w->hidden, qd, attn, n, xq, d_out, s);
 }
 
 }  // extern "C"

@@ -75,6 +75,8 @@ _PROTOS = {
                                           _vp, _vp]),
     "tq_hip_attention_layer_ws_bytes": (_sz, [_vp, _vp, _i]),
     "tq_hip_attention_layer_async": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "tq_hip_rmsnorm_rows": (_i, [_vp, _vp, _vp, _i, _i, C.c_float, _vp]),
+    "tq_hip_attention_layer_batch_async": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "tq_hip_q8_matrix_bytes": (_sz, [_i, _i]),
     "tq_hip_q8_pack": (_i, [_vp, _vp, _i, _i, _vp]),
     "tq_hip_q8_unpack": (_i, [_vp, _vp, _i, _i, _vp]),
