@@ -25,7 +25,8 @@ prefill-2k (causal prefill of 2048 tokens), project-8b / project-70b (the Q8
 weight GEMVs either side of attention for one token: project_qkv and
 project_output, 32 layers' weights rotated), layer-8b (the whole
 attention_layer for one token at ctx 4096: projections, q/k RMSNorm, RoPE,
-append, attend).  They print the same JSON fields for their own shape.
+append, attend), layer-prefill-8b (attention_layer_batch for 2048 tokens).
+They print the same JSON fields for their own shape.
 
 --copy-calibration BYTES runs one device-to-device copy of BYTES first: its
 FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc give the counters' scale.
@@ -828,6 +829,116 @@ def bench_layer_8b(args, nat, hip):
     return line
 
 
+def bench_layer_prefill_8b(args, nat, hip):
+    """attention_layer_batch (model/attention_layer.c:200-243) for 2048 new tokens at
+    the 8B shape on an empty cache, all on the device: GEMM projections, q/k
+    RMSNorm, RoPE + append + causal attention, GEMM output projection."""
+    from oracle.binding import Oracle
+    lib = nat.load()
+    nq, nkv, hd, hidden, n, theta, eps = 32, 8, 128, 4096, 2048, 500000.0, 1e-6
+    qr, kr = nq * hd, nkv * hd
+    rng = np.random.default_rng(23)
+    host_w = (random_q8_weights(rng, qr, hidden), random_q8_weights(rng, kr, hidden),
+              random_q8_weights(rng, kr, hidden), random_q8_weights(rng, hidden, qr))
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    dims = ((qr, hidden), (kr, hidden), (kr, hidden), (hidden, qr))
+    mats = []
+    for w, (r, c) in zip(host_w, dims):
+        src = nat.DeviceBuffer.from_numpy(w)
+        m = nat.DeviceBuffer(lib.tq_hip_q8_matrix_bytes(r, c))
+        nat.check(lib.tq_hip_q8_pack(m.ptr, src.ptr, r, c, None), "q8_pack")
+        mats.append(m)
+        src.free()
+    D = nat.DeviceBuffer.from_numpy
+    dqn, dkn = D(qn), D(kn)
+    weights = nat.AttnWeights(mats[0].ptr, mats[1].ptr, mats[2].ptr, mats[3].ptr, dqn.ptr, dkn.ptr, hidden, eps)
+    kv = nat.PagedKV.single(nq, nkv, hd, n)
+    stream = kv.stream
+    xn = rng.standard_normal(n * hidden, dtype=np.float32)
+    cos, sin = rope_tables(hd, range(n), theta)
+    dxn, dc, ds = D(xn), D(cos), D(sin)
+    wsb = lib.tq_hip_attention_layer_ws_bytes(kv.h, C.byref(weights), n)
+    ws = nat.DeviceBuffer(wsb)
+    out = nat.DeviceBuffer(n * hidden * 4)
+
+    def step():
+        nat.check(lib.tq_hip_attention_layer_batch_async(kv.h, C.byref(weights), 0, 0, n, dxn.ptr, dc.ptr, ds.ptr,
+                                                         out.ptr, ws.ptr, wsb, stream), "attention_layer_batch")
+
+    step()
+    hip.sync()
+    got = out.download((n, hidden), np.float32)
+    # parity: the first 64 tokens against the oracle's attention_layer, token by token
+    oracle = Oracle()
+    nb = hd // QK
+    from oracle.binding import blocks
+    kc, vc = blocks(nkv * n * nb), blocks(nkv * n * nb)
+    errs = []
+    for i in range(64):
+        rc, r = oracle.attention_layer(host_w + (qn, kn), nq, nkv, hd, hidden, theta, eps, kc, vc, n, i,
+                                       xn[i * hidden:(i + 1) * hidden])
+        errs.append(rel_l2(got[i], r))
+    parity = {"ok": bool(max(errs) <= 1e-2 and float(np.median(errs)) <= 1e-3), "median_rel_l2": float(np.median(errs)),
+              "max_rel_l2": float(max(errs)), "bar": "per-token relative L2 <= 1e-2, median <= 1e-3",
+              "against": "oracle attention_layer (bit-exact with the reference's), first 64 tokens"}
+    steps = max(3, args.steps // 400)
+    ms = timed(hip, stream, steps, step)
+    hip.sync()
+    weight_bytes = sum(m.nbytes for m in mats)
+    # int8 products of the four projections plus the useful attention products
+    proj_ops = 2.0 * n * hidden * (qr + 2 * kr) + 2.0 * n * qr * hidden
+    attn_ops = 2.0 * nq * (n * (n + 1) / 2) * hd * 2
+    line = {
+        "metric": "Q8 GQA attention layer prefill tokens/sec (attention_layer_batch, 2048 tokens) at 8B shape, 1 GPU",
+        "value": n * 1e3 / ms, "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": 1, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": ("attention_layer_batch for 2048 new tokens on an empty cache: GEMM q/k/v "
+                                "projections, q/k RMSNorm, RoPE + KV append + causal attention, GEMM output "
+                                "projection; 32q/8kv/hd128, hidden 4096"),
+                   "tokens": n, "hidden": hidden, "weight_bytes": weight_bytes,
+                   "projection_ops": proj_ops, "attention_useful_ops": attn_ops},
+        "parity": parity,
+        "roofline": {"bound": "mfma", "achieved": proj_ops / (ms * 1e-3) / 1e12, "peak": 5000.0,
+                     "unit": "TOP/s", "frac": proj_ops / (ms * 1e-3) / 1e12 / 5000.0, "traffic": None,
+                     "kernel": "gemm_q8_kernel (projections) + rmsnorm_rows + prefill kernels: one layer step; "
+                               "achieved = projection int8 ops over the whole step",
+                     "kernel_ms": ms},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_leg_layer_batch(nq, nkv, hd, hidden, n, theta, eps, host_w, qn, kn, xn,
+                                                   args.cpu_budget)
+    kv.close()
+    return line
+
+
+def cpu_leg_layer_batch(nq, nkv, hd, hidden, n, theta, eps, host_w, qn, kn, xn, budget_s: float):
+    """The reference's own attention_layer_batch (oracle/_ref: AVX2 token-tiled matmuls,
+    OpenMP) for the same 2048 tokens on an empty cache; whole calls until the budget."""
+    from oracle.binding import Ref, blocks, ptr
+    if not Ref.available():
+        return None
+    ref = Ref()
+    nb = hd // QK
+    scores = np.zeros(nq * n, np.float32)
+    out = np.zeros(n * hidden, np.float32)
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s or len(times) < 2:
+        kc, vc = blocks(nkv * n * nb), blocks(nkv * n * nb)
+        t0 = time.perf_counter()
+        rc = ref.lib.tqref_layer_batch_run(nq, nkv, hd, hidden, theta, eps, ptr(host_w[0]), ptr(host_w[1]),
+                                           ptr(host_w[2]), ptr(host_w[3]), ptr(qn), ptr(kn), ptr(kc), ptr(vc), n, 0,
+                                           n, ptr(xn), ptr(scores), ptr(out))
+        times.append(time.perf_counter() - t0)
+        assert rc == 0
+    med = float(np.median(times))
+    omp = int(os.environ.get("OMP_NUM_THREADS", str(os.cpu_count() or 1)))
+    return {"value": n / med, "unit": "tokens/s", "cores": min(omp, os.cpu_count() or 1), "kind": "reference",
+            "sample": (f"{len(times)} attention_layer_batch calls of {n} tokens, median {med:.3f} s; {ref.isa()} "
+                       f"matmuls, OpenMP (OMP_NUM_THREADS={omp}, nproc={os.cpu_count()})")}
+
+
 def cpu_leg_layer(nq, nkv, hd, hidden, T, theta, eps, host_w, qn, kn, xn, budget_s: float):
     """The reference's own attention_layer (oracle/_ref: AVX2 matmuls, OpenMP) at
     position T-1 over a full cache, rotating 8 layers of weights and caches."""
@@ -882,7 +993,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--config", default="decode-8b-4k",
                     choices=["decode-8b-4k", "decode-batched", "prefill-2k", "decode-70b-32k", "project-8b",
-                             "project-70b", "layer-8b"])
+                             "project-70b", "layer-8b", "layer-prefill-8b"])
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
@@ -907,8 +1018,9 @@ def main():
     else:
         line = {"decode-batched": bench_decode_batched, "prefill-2k": bench_prefill_2k,
                 "decode-70b-32k": bench_decode_70b, "project-8b": bench_project_8b,
-                "project-70b": bench_project_70b, "layer-8b": bench_layer_8b}[args.config](args, nat, hip)
-    if args.config.startswith(("decode", "project", "layer")):
+                "project-70b": bench_project_70b, "layer-8b": bench_layer_8b,
+                "layer-prefill-8b": bench_layer_prefill_8b}[args.config](args, nat, hip)
+    if args.config.startswith(("decode", "project")) or args.config == "layer-8b":
         # the achievable read rate of this box, beside the 8 TB/s spec peak
         peak = measure_hbm_read(nat, hip)
         line["roofline"]["measured_peak"] = peak
