@@ -81,6 +81,15 @@ class Oracle:
         L.oracle_rmsnorm.argtypes = [_vp, _vp, _vp, _i, _f]
         L.oracle_attention_layer.argtypes = [_vp] * 6 + [_i, _i, _i, _i, _f, _f, _vp, _vp, _i, _i, _vp, _vp, _vp]
         L.oracle_attention_layer.restype = _i
+        L.oracle_silu_mul.argtypes = [_vp, _vp, _vp, _i]
+        L.oracle_mlp_layer.argtypes = [_vp, _vp, _vp, _i, _i, _vp, _vp]
+        L.oracle_mlp_layer.restype = _i
+        L.oracle_embed_lookup_q8.argtypes = [_vp, _i, _i, _i, _vp]
+        L.oracle_embed_lookup_q8.restype = _i
+        L.oracle_sample_greedy.argtypes = [_vp, _i]
+        L.oracle_sample_greedy.restype = _i
+        L.oracle_forward_token.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
+        L.oracle_forward_token.restype = _i
         L.oracle_pack_matrix_q8.argtypes = [_vp, _i, _i, _vp]
         L.oracle_matmul_q8.argtypes = [_vp, _vp, _vp, _i, _i]
         L.oracle_matmul_q8_batch.argtypes = [_vp, _vp, _vp, _i, _i, _i]
@@ -165,6 +174,34 @@ class Oracle:
                                              pos, ptr(f32(xn)), ptr(scores), ptr(out))
         return rc, out
 
+    # --- the rest of the block ----------------------------------------------
+    def silu_mul(self, g, u) -> np.ndarray:
+        g, u = f32(g), f32(u)
+        out = np.zeros_like(g)
+        self.lib.oracle_silu_mul(ptr(g), ptr(u), ptr(out), g.size)
+        return out
+
+    def mlp_layer(self, wgate, wup, wdown, hidden, inter, xn) -> np.ndarray:
+        out = np.zeros(hidden, np.float32)
+        rc = self.lib.oracle_mlp_layer(ptr(np.ascontiguousarray(wgate)), ptr(np.ascontiguousarray(wup)),
+                                       ptr(np.ascontiguousarray(wdown)), hidden, inter, ptr(f32(xn)), ptr(out))
+        assert rc == 0
+        return out
+
+    def forward(self, model, tokens, max_tokens):
+        """tq_forward_token over `tokens` on fresh caches; logits [len(tokens)][vocab]."""
+        nb = model.hd // QK
+        kc = [blocks(model.nkv * max_tokens * nb) for _ in range(model.n_layers)]
+        vc = [blocks(model.nkv * max_tokens * nb) for _ in range(model.n_layers)]
+        karr = (C.c_void_p * model.n_layers)(*[ptr(c) for c in kc])
+        varr = (C.c_void_p * model.n_layers)(*[ptr(c) for c in vc])
+        st, keep = model.struct()
+        out = np.zeros((len(tokens), model.vocab), np.float32)
+        for i, t in enumerate(tokens):
+            rc = self.lib.oracle_forward_token(C.byref(st), karr, varr, max_tokens, i, int(t), ptr(out[i]))
+            assert rc == 0, rc
+        return out, kc, vc
+
     # --- weight side ---------------------------------------------------------
     def pack_matrix_q8(self, W) -> np.ndarray:
         """rows x cols floats -> rows x cols/32 block_q8 (packer/packer.c)."""
@@ -200,6 +237,54 @@ class Oracle:
         return rc, out
 
 
+class OracleModel(C.Structure):
+    """struct oracle_model (oracle/tq_oracle.h): a Q8 model as flat per-layer pointer arrays."""
+    _fields_ = [("n_layers", _i), ("n_q_heads", _i), ("n_kv_heads", _i), ("head_dim", _i), ("hidden", _i),
+                ("inter", _i), ("vocab", _i), ("rope_theta", _f), ("rms_eps", _f), ("embed", _vp),
+                ("final_norm", _vp), ("input_norm", _vp), ("post_norm", _vp), ("wq", _vp), ("wk", _vp),
+                ("wv", _vp), ("wo", _vp), ("q_norm", _vp), ("k_norm", _vp), ("wgate", _vp), ("wup", _vp),
+                ("wdown", _vp)]
+
+
+class Model:
+    """A random Q8 model held as numpy arrays, in the shapes tq_model uses."""
+
+    def __init__(self, oracle, n_layers, nq, nkv, hd, hidden, inter, vocab, theta=5e5, eps=1e-6, seed=0):
+        rng = np.random.default_rng(seed)
+        self.n_layers, self.nq, self.nkv, self.hd = n_layers, nq, nkv, hd
+        self.hidden, self.inter, self.vocab, self.theta, self.eps = hidden, inter, vocab, theta, eps
+
+        def mat(r, c, scale):
+            return oracle.pack_matrix_q8((rng.standard_normal((r, c)) * scale).astype(np.float32)).reshape(-1)
+
+        def norm(n):
+            return rng.uniform(0.6, 1.4, n).astype(np.float32)
+
+        self.embed = mat(vocab, hidden, 1.0)
+        self.final_norm = norm(hidden)
+        self.layers = []
+        for _ in range(n_layers):
+            self.layers.append(dict(
+                input_norm=norm(hidden), post_norm=norm(hidden),
+                wq=mat(nq * hd, hidden, 0.05), wk=mat(nkv * hd, hidden, 0.05), wv=mat(nkv * hd, hidden, 0.05),
+                wo=mat(hidden, nq * hd, 0.05), q_norm=norm(hd), k_norm=norm(hd),
+                wgate=mat(inter, hidden, 0.05), wup=mat(inter, hidden, 0.05), wdown=mat(hidden, inter, 0.05)))
+
+    def ptr_array(self, key):
+        arr = (C.c_void_p * self.n_layers)(*[ptr(l[key]) for l in self.layers])
+        return arr
+
+    def struct(self):
+        keep = {k: self.ptr_array(k) for k in ("input_norm", "post_norm", "wq", "wk", "wv", "wo", "q_norm",
+                                              "k_norm", "wgate", "wup", "wdown")}
+        st = OracleModel(self.n_layers, self.nq, self.nkv, self.hd, self.hidden, self.inter, self.vocab,
+                         self.theta, self.eps, ptr(self.embed), ptr(self.final_norm),
+                         *[C.cast(keep[k], C.c_void_p) for k in ("input_norm", "post_norm", "wq", "wk", "wv",
+                                                                  "wo", "q_norm", "k_norm", "wgate", "wup",
+                                                                  "wdown")])
+        return st, keep
+
+
 class Ref:
     """The reference compiled from its own sources (oracle/_ref)."""
 
@@ -228,6 +313,13 @@ class Ref:
         L.tqref_attention_qkv.restype = _i
         L.tqref_isa.restype = C.c_char_p
         L.rmsnorm.argtypes = [_vp, _vp, _vp, _i, _f]
+        L.silu_mul.argtypes = [_vp, _vp, _vp, _i]
+        L.sample_greedy.argtypes = [_vp, _i]
+        L.sample_greedy.restype = _i
+        L.tqref_mlp_run.argtypes = [_i, _i, _vp, _vp, _vp, _vp, _vp]
+        L.tqref_mlp_run.restype = _i
+        L.tqref_forward_run.argtypes = [_i] * 7 + [_f, _f] + [_vp] * 13 + [_i, _i, _vp, _vp]
+        L.tqref_forward_run.restype = _i
         L.pack_matrix.argtypes = [_vp, _i, _i, _vp, C.c_char]
         L.pack_matrix.restype = _i
         simd = ("matmul_q8_avx2",) if not scalar else ()
@@ -242,6 +334,19 @@ class Ref:
 
     def isa(self) -> str:
         return self.lib.tqref_isa().decode()
+
+    def forward(self, model, tokens, max_tokens):
+        """The reference's tq_forward_token over `tokens` (tq_ctx with TQ_KV_Q8 caches)."""
+        st, keep = model.struct()
+        toks = np.ascontiguousarray(tokens, np.int32)
+        out = np.zeros((len(toks), model.vocab), np.float32)
+        rc = self.lib.tqref_forward_run(model.n_layers, model.nq, model.nkv, model.hd, model.hidden, model.inter,
+                                        model.vocab, model.theta, model.eps, ptr(model.embed),
+                                        ptr(model.final_norm), *[keep[k] for k in (
+                                            "input_norm", "post_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm",
+                                            "wgate", "wup", "wdown")], max_tokens, len(toks), ptr(toks), ptr(out))
+        assert rc == 0, rc
+        return out
 
     def rmsnorm(self, x, weight, eps: float) -> np.ndarray:
         w = f32(weight)

@@ -188,5 +188,63 @@ int tqref_attention_qkv(int nq, int nkv, int hd, int max_tokens, float theta,
     return 0;
 }
 
+/* The reference's own mlp_layer (model/mlp.c:3-17) on Q8 matrices. */
+int tqref_mlp_run(int hidden, int inter, const block_q8 *wgate, const block_q8 *wup,
+                  const block_q8 *wdown, const float *xn, float *out) {
+    tq_mlp_weights w;
+    bind(&w.wgate, wgate, inter, hidden);
+    bind(&w.wup, wup, inter, hidden);
+    bind(&w.wdown, wdown, hidden, inter);
+    block_q8 *xq = malloc((size_t)hidden / QK * sizeof(block_q8));
+    block_q8 *hq = malloc((size_t)inter / QK * sizeof(block_q8));
+    float *gate = malloc((size_t)inter * sizeof(float)), *up = malloc((size_t)inter * sizeof(float));
+    int rc = (xq && hq && gate && up) ? mlp_layer(&w, xn, xq, gate, up, hq, out) : -100;
+    free(xq); free(hq); free(gate); free(up);
+    return rc;
+}
+
+/* The reference's own tq_ctx_init + tq_forward_token (model/context.c:6-52,
+ * 128-153) over n_tok tokens on a Q8 model given as flat per-layer pointer
+ * arrays, with TQ_KV_Q8 caches; logits [n_tok][vocab].  Returns the first
+ * nonzero code, or 0. */
+int tqref_forward_run(int n_layers, int nq, int nkv, int hd, int hidden, int inter, int vocab,
+                      float theta, float eps, const block_q8 *embed, const float *final_norm,
+                      const float *const *input_norm, const float *const *post_norm,
+                      const block_q8 *const *wq, const block_q8 *const *wk,
+                      const block_q8 *const *wv, const block_q8 *const *wo,
+                      const float *const *qn, const float *const *kn,
+                      const block_q8 *const *wgate, const block_q8 *const *wup,
+                      const block_q8 *const *wdown, int max_tokens, int n_tok, const int *tokens,
+                      float *logits) {
+    tq_layer_weights *layers = calloc((size_t)n_layers, sizeof *layers);
+    if (!layers) return -100;
+    tq_model m;
+    memset(&m, 0, sizeof m);
+    for (int l = 0; l < n_layers; l++) {
+        make_layer(&layers[l].attn, &m.cfg.attn, nq, nkv, hd, hidden, theta, eps, wq[l], wk[l], wv[l],
+                   wo[l], qn[l], kn[l]);
+        layers[l].input_norm = input_norm[l];
+        layers[l].post_norm = post_norm[l];
+        bind(&layers[l].mlp.wgate, wgate[l], inter, hidden);
+        bind(&layers[l].mlp.wup, wup[l], inter, hidden);
+        bind(&layers[l].mlp.wdown, wdown[l], hidden, inter);
+    }
+    m.cfg.n_layers = n_layers;
+    m.cfg.intermediate_size = inter;
+    m.cfg.vocab_size = vocab;
+    bind(&m.w.embed, embed, vocab, hidden);
+    m.w.final_norm = final_norm;
+    m.w.layers = layers;
+    tq_ctx ctx;
+    int rc = tq_ctx_init(&ctx, &m, TQ_KV_Q8, max_tokens);
+    for (int i = 0; rc == 0 && i < n_tok; i++) {
+        rc = tq_forward_token(&ctx, tokens[i]);
+        if (rc == 0) memcpy(logits + (size_t)i * vocab, ctx.logits, (size_t)vocab * sizeof(float));
+    }
+    tq_ctx_free(&ctx);
+    free(layers);
+    return rc;
+}
+
 /* Which matmul/attention ISA the build dispatches to ("AVX2" or "scalar"). */
 const char *tqref_isa(void) { return kernel_isa_name(); }

@@ -17,6 +17,7 @@
 
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* kernel/quant_x.c:5-10.  Adding 1.5*2^23 moves v into the binade where the
@@ -326,4 +327,96 @@ int oracle_attention_layer(const block_q8 *wq, const block_q8 *wk, const block_q
     if (rc != 0) return rc;
     oracle_project_q8(wo, hidden, qdim, attn, 1, out);
     return 0;
+}
+
+/* ---- the rest of the block: MLP, embedding, lm_head, sampler, forward ---- */
+
+/* model/silu.c:6-18: out = silu(g) * u, silu(x) = x * (1 / (1 + expf(-x))). */
+void oracle_silu_mul(const float *gate, const float *up, float *out, int n) {
+    for (int i = 0; i < n; i++) {
+        const float g = gate[i];
+        const float sig = 1.0f / (1.0f + expf(-g));
+        out[i] = g * sig * up[i];
+    }
+}
+
+/* model/mlp.c:3-17 (mlp_layer): quantize xn, gate and up matmuls, silu_mul,
+ * quantize, down matmul.  wgate/wup: inter x hidden; wdown: hidden x inter. */
+int oracle_mlp_layer(const block_q8 *wgate, const block_q8 *wup, const block_q8 *wdown, int hidden,
+                     int inter, const float *xn, float *out) {
+    if (hidden % QK != 0 || inter % QK != 0) return -1;
+    float *gate = (float *)malloc((size_t)inter * sizeof(float));
+    float *up = (float *)malloc((size_t)inter * sizeof(float));
+    block_q8 *q = (block_q8 *)malloc((size_t)(inter > hidden ? inter : hidden) / QK * sizeof(block_q8));
+    if (!gate || !up || !q) {
+        free(gate); free(up); free(q);
+        return -100;
+    }
+    oracle_quantize_row_q8(xn, q, hidden);
+    oracle_matmul_q8(wgate, q, gate, inter, hidden);
+    oracle_matmul_q8(wup, q, up, inter, hidden);
+    oracle_silu_mul(gate, up, gate, inter);
+    oracle_quantize_row_q8(gate, q, inter);
+    oracle_matmul_q8(wdown, q, out, hidden, inter);
+    free(gate); free(up); free(q);
+    return 0;
+}
+
+/* model/embedding.c:4-17, Q8 branch: out[b*32+j] = d * q[j] of row `token`. */
+int oracle_embed_lookup_q8(const block_q8 *embed, int rows, int cols, int token, float *out) {
+    if (token < 0 || token >= rows || cols % QK != 0) return -1;
+    const int nb = cols / QK;
+    const block_q8 *row = embed + (size_t)token * nb;
+    for (int b = 0; b < nb; b++)
+        for (int j = 0; j < QK; j++) out[b * QK + j] = row[b].d * (float)row[b].q[j];
+    return 0;
+}
+
+/* model/sampler.c:3-13: the first index of the largest logit (strict >). */
+int oracle_sample_greedy(const float *logits, int n) {
+    if (n <= 0) return -1;
+    float m = logits[0];
+    int idx = 0;
+    for (int i = 1; i < n; i++)
+        if (logits[i] > m) {
+            m = logits[i];
+            idx = i;
+        }
+    return idx;
+}
+
+/* model/context.c:128-153 (tq_forward_token) with Q8 weights and the flat Q8
+ * caches: embed_lookup, per layer rmsnorm(input_norm) -> attention_layer ->
+ * x += attn (vec_add, model/vec.c:3-6) -> rmsnorm(post_norm) -> mlp_layer ->
+ * x += mlp, then rmsnorm(final_norm) and lm_head (model/embedding.c:34-38:
+ * quantize + matmul against the embedding).  Per-layer pointers come in arrays
+ * of n_layers; caches[l] are [n_kv][max_tokens][nb] K then V arrays. */
+int oracle_forward_token(const struct oracle_model *m, block_q8 *const *k_caches,
+                         block_q8 *const *v_caches, int max_tokens, int pos, int token, float *logits) {
+    const int hidden = m->hidden;
+    if (pos < 0 || pos >= max_tokens || token < 0 || token >= m->vocab) return -1;
+    float *x = (float *)malloc((size_t)hidden * sizeof(float));
+    float *xn = (float *)malloc((size_t)hidden * sizeof(float));
+    float *y = (float *)malloc((size_t)hidden * sizeof(float));
+    float *scores = (float *)malloc((size_t)m->n_q_heads * max_tokens * sizeof(float));
+    int rc = (x && xn && y && scores) ? 0 : -100;
+    if (rc == 0) rc = oracle_embed_lookup_q8(m->embed, m->vocab, hidden, token, x);
+    for (int l = 0; rc == 0 && l < m->n_layers; l++) {
+        oracle_rmsnorm(x, m->input_norm[l], xn, hidden, m->rms_eps);
+        rc = oracle_attention_layer(m->wq[l], m->wk[l], m->wv[l], m->wo[l], m->q_norm[l], m->k_norm[l],
+                                    m->n_q_heads, m->n_kv_heads, m->head_dim, hidden, m->rope_theta,
+                                    m->rms_eps, k_caches[l], v_caches[l], max_tokens, pos, xn, scores, y);
+        if (rc != 0) break;
+        for (int i = 0; i < hidden; i++) x[i] += y[i];
+        oracle_rmsnorm(x, m->post_norm[l], xn, hidden, m->rms_eps);
+        rc = oracle_mlp_layer(m->wgate[l], m->wup[l], m->wdown[l], hidden, m->inter, xn, y);
+        if (rc != 0) break;
+        for (int i = 0; i < hidden; i++) x[i] += y[i];
+    }
+    if (rc == 0) {
+        oracle_rmsnorm(x, m->final_norm, xn, hidden, m->rms_eps);
+        oracle_project_q8(m->embed, m->vocab, hidden, xn, 1, logits);
+    }
+    free(x); free(xn); free(y); free(scores);
+    return rc;
 }

@@ -81,6 +81,37 @@ int oracle_attention_layer(const block_q8 *wq, const block_q8 *wk, const block_q
                            block_q8 *v_cache, int max_tokens, int pos, const float *xn,
                            float *scores, float *out);
 
+/* model/silu.c:6-18 */
+void oracle_silu_mul(const float *gate, const float *up, float *out, int n);
+
+/* model/mlp.c:3-17 */
+int oracle_mlp_layer(const block_q8 *wgate, const block_q8 *wup, const block_q8 *wdown, int hidden,
+                     int inter, const float *xn, float *out);
+
+/* model/embedding.c:4-17 (Q8) */
+int oracle_embed_lookup_q8(const block_q8 *embed, int rows, int cols, int token, float *out);
+
+/* model/sampler.c:3-13 */
+int oracle_sample_greedy(const float *logits, int n);
+
+/* A Q8 model as tq_model holds it (model/model_ops.h:50-73), per-layer
+ * pointers in arrays of n_layers; embed is vocab x hidden (tied lm_head). */
+struct oracle_model {
+    int n_layers, n_q_heads, n_kv_heads, head_dim, hidden, inter, vocab;
+    float rope_theta, rms_eps;
+    const block_q8 *embed;
+    const float *final_norm;
+    const float *const *input_norm;
+    const float *const *post_norm;
+    const block_q8 *const *wq, *const *wk, *const *wv, *const *wo;
+    const float *const *q_norm, *const *k_norm;
+    const block_q8 *const *wgate, *const *wup, *const *wdown;
+};
+
+/* model/context.c:128-153 (tq_forward_token) on flat Q8 caches. */
+int oracle_forward_token(const struct oracle_model *m, block_q8 *const *k_caches,
+                         block_q8 *const *v_caches, int max_tokens, int pos, int token, float *logits);
+
 /* packer/packer.c:4-31 (pack_row_q8 over every row): weights -> block_q8. */
 void oracle_pack_matrix_q8(const float *W, int rows, int cols, block_q8 *out);
 
