@@ -239,6 +239,46 @@ int tq_hip_project_qkv(const void *wq, const void *wk, const void *wv, int q_row
 int tq_hip_project_output(const void *wo, int rows, int cols, const float *attn, int n_tok,
                           block_q8 *xq_ws, float *out, void *stream);
 
+/* ---- the rest of the block: MLP, residual norm, embedding, sampler ------- */
+
+/* tq_mlp_weights (model/model_ops.h:29-31) with device pointers: wgate and wup
+ * inter x hidden, wdown hidden x inter, all tiled Q8 (tq_hip_q8_pack). */
+typedef struct {
+    const void *wgate;
+    const void *wup;
+    const void *wdown;
+    int hidden;
+    int inter;
+} tq_hip_mlp_weights;
+
+/* Device workspace bytes for tq_hip_mlp_layer_async over n rows (gate, up and
+ * the quantized rows), or 0 for a bad shape. */
+size_t tq_hip_mlp_ws_bytes(const tq_hip_mlp_weights *w, int n);
+/* mlp_layer / mlp_layer_batch (model/mlp.c:3-43) for n rows of d_xn
+ * [n][hidden] into d_out [n][hidden]: quantize_row_q8, the gate and up
+ * matmuls in one launch, silu_mul (model/silu.c:6-18, device expf) fused with
+ * the quantization of the hidden rows, the down matmul.  d_ws 16-byte aligned. */
+int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn, float *d_out, void *d_ws,
+                           size_t ws_bytes, void *stream);
+
+/* The residual add and RMSNorm of model/context.c:83-105 for n_rows rows of n:
+ * x += y (model/vec.c:3-6; y may be NULL), then xn = rmsnorm(x, weight)
+ * (model/rmsnorm.c:4-19) with the sum of squares taken in parallel (within
+ * fp32 rounding of the reference's serial sum; the per-head norms in front
+ * of the cache keep the serial order, tq_hip_rmsnorm_rows). */
+int tq_hip_add_rmsnorm(float *x, const float *y, const float *weight, float *xn, int n_rows, int n, float eps,
+                       void *stream);
+
+/* embed_lookup, Q8 (model/embedding.c:4-17): row `token` of a tiled Q8
+ * rows x cols matrix, dequantized into out[cols].  TQ_HIP_EINVAL for a token
+ * outside [0, rows), as the reference returns -1. */
+int tq_hip_embed_lookup_q8(const void *embed, int rows, int cols, int token, float *out, void *stream);
+
+/* sample_greedy (model/sampler.c:3-13): the first index of the largest of n
+ * logits (strict >, so NaN never wins and ties keep the lower index), written
+ * to out[0] on the device. */
+int tq_hip_sample_greedy(const float *logits, int n, int32_t *out, void *stream);
+
 /* ---- the whole attention layer on the device --------------------------- */
 
 /* tq_attn_weights (model/model_ops.h:27-37) with device pointers: the four

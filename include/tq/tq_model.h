@@ -1,0 +1,80 @@
+/* tq_model.h — a Q8 model's token forward on one MI355X: the device
+ * counterpart of tq_ctx_init / tq_forward_token (model/context.c:6-52,
+ * 128-153), in libtqattn.so over libtqhip.so.
+ *
+ * Weights live on the device (tiled Q8 matrices made by tq_hip_q8_pack, fp32
+ * norm rows); the context owns one TQ_KV_Q8_DEVICE cache per layer, the
+ * activations, a RoPE table for every position (computed on the host with the
+ * reference's rope_table arithmetic) and one workspace.  tq_dev_forward_token
+ * only enqueues work on the context's stream; tq_dev_logits and
+ * tq_dev_sample_greedy wait for it.
+ */
+#ifndef TQ_MODEL_H
+#define TQ_MODEL_H
+
+#include "tq_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* tq_layer_weights (model/model_ops.h:57-62), device pointers. */
+typedef struct {
+    const float *input_norm;      /* [hidden] */
+    tq_hip_attn_weights attn;     /* wq, wk, wv, wo, q_norm, k_norm, hidden, rms_eps */
+    const float *post_norm;       /* [hidden] */
+    tq_hip_mlp_weights mlp;       /* wgate, wup, wdown, hidden, inter */
+} tq_dev_layer_weights;
+
+/* tq_model (model/model_ops.h:50-73), device pointers; `layers` is a host
+ * array of n_layers.  embed (vocab x hidden, tiled Q8) is also the lm_head
+ * (model/embedding.c:34-38). */
+typedef struct {
+    tq_attn_config attn;
+    int n_layers;
+    int intermediate_size;
+    int vocab_size;
+    const void *embed;
+    const float *final_norm;
+    const tq_dev_layer_weights *layers;
+} tq_dev_model;
+
+/* tq_ctx (model/model_ops.h:75-95) for the device. */
+typedef struct {
+    const tq_dev_model *model;
+    tq_kv_cache *caches;          /* n_layers TQ_KV_Q8_DEVICE caches */
+    int pos;
+    int max_tokens;
+    void *stream;                 /* every launch goes here */
+    float *x, *xn, *y, *logits;   /* device: residual, normalized, block output, [vocab] */
+    float *cos_t, *sin_t;         /* device [max_tokens][head_dim/2] */
+    int32_t *positions;           /* device [max_tokens]: 0, 1, 2, ... */
+    void *ws;                     /* device workspace of the attention and MLP calls */
+    size_t ws_bytes;
+    int32_t *sampled;             /* device: tq_dev_sample_greedy's result */
+} tq_dev_ctx;
+
+/* model/context.c:6-52: -1 for a NULL model, max_tokens <= 0, hidden or
+ * intermediate size not a multiple of 32, n_layers or vocab_size <= 0, a
+ * missing weight pointer, or a device or allocation failure (everything
+ * allocated so far is freed). */
+int tq_dev_ctx_init(tq_dev_ctx *ctx, const tq_dev_model *m, int max_tokens);
+/* model/context.c:55-77; idempotent. */
+void tq_dev_ctx_free(tq_dev_ctx *ctx);
+
+/* model/context.c:128-153: embed_lookup, per layer rmsnorm -> attention_layer
+ * -> residual add -> rmsnorm -> mlp_layer -> residual add, then the final
+ * rmsnorm and lm_head into ctx->logits; pos advances.  -1 for pos >=
+ * max_tokens or a token outside [0, vocab_size) before any launch. */
+int tq_dev_forward_token(tq_dev_ctx *ctx, int token);
+/* Wait for the stream and copy the last token's logits to host[vocab]. */
+int tq_dev_logits(tq_dev_ctx *ctx, float *host);
+/* sample_greedy (model/sampler.c:3-13) of the last token's logits on the
+ * device; waits and returns the token (or < 0 on failure). */
+int tq_dev_sample_greedy(tq_dev_ctx *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TQ_MODEL_H */

@@ -1,4 +1,4 @@
-"""ctypes binding of libtqattn.so (include/tq/tq_attn.h), the C host interface.
+"""ctypes binding of libtqattn.so (include/tq/tq_attn.h, tq_model.h), the C host interface.
 
 Mirrors the reference's kv_cache / attention entry points for the device Q8
 cache (model/model_ops.h:95-97,124; model/attention_layer.c:66-90,125-150,
@@ -34,7 +34,26 @@ class KVCache(C.Structure):
                 ("max_tokens", _i), ("dev", _vp)]
 
 
+class DevLayerWeights(C.Structure):
+    """tq_dev_layer_weights (include/tq/tq_model.h): tq_layer_weights with device pointers."""
+    _fields_ = [("input_norm", _vp), ("attn", native.AttnWeights), ("post_norm", _vp), ("mlp", native.MlpWeights)]
+
+
+class DevModel(C.Structure):
+    """tq_dev_model: tq_model (model/model_ops.h:50-73) with device weights."""
+    _fields_ = [("attn", AttnConfig), ("n_layers", _i), ("intermediate_size", _i), ("vocab_size", _i),
+                ("embed", _vp), ("final_norm", _vp), ("layers", C.POINTER(DevLayerWeights))]
+
+
+class DevCtx(C.Structure):
+    """tq_dev_ctx: tq_ctx (model/model_ops.h:75-95) for the device."""
+    _fields_ = [("model", _vp), ("caches", _vp), ("pos", _i), ("max_tokens", _i), ("stream", _vp),
+                ("x", _vp), ("xn", _vp), ("y", _vp), ("logits", _vp), ("cos_t", _vp), ("sin_t", _vp),
+                ("positions", _vp), ("ws", _vp), ("ws_bytes", C.c_size_t), ("sampled", _vp)]
+
+
 _PC, _PK = C.POINTER(AttnConfig), C.POINTER(KVCache)
+_PM, _PX = C.POINTER(DevModel), C.POINTER(DevCtx)
 
 _PROTOS = {
     "tq_kv_cache_init": (_i, [_PK, _i, _PC, _i]),
@@ -47,6 +66,11 @@ _PROTOS = {
     "tq_attention_core_batch": (_i, [_PC, _PK, _i, _i, _vp, _vp, _vp, _vp]),
     "tq_kv_cache_upload": (_i, [_PK, _vp, _vp]),
     "tq_kv_cache_download": (_i, [_PK, _vp, _vp]),
+    "tq_dev_ctx_init": (_i, [_PX, _PM, _i]),
+    "tq_dev_ctx_free": (None, [_PX]),
+    "tq_dev_forward_token": (_i, [_PX, _i]),
+    "tq_dev_logits": (_i, [_PX, _vp]),
+    "tq_dev_sample_greedy": (_i, [_PX]),
 }
 
 EXPORTS = tuple(_PROTOS)

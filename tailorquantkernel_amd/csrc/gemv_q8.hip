@@ -779,4 +779,69 @@ int tq_hip_project_output(const void *wo, int rows, int cols, const float *attn,
     return run_gemv(a, n_tok, s);
 }
 
+static size_t mlp_ws(int hidden, int inter, int n, size_t *off_gate, size_t *off_up, size_t *off_xq) {
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    size_t o = 0;
+    *off_gate = o;
+    o += al((size_t)n * inter * 4);
+    *off_up = o;
+    o += al((size_t)n * inter * 4);
+    *off_xq = o;
+    o += al((size_t)n * (size_t)(hidden > inter ? hidden : inter) / kQK * kBlockBytes);
+    return o;
+}
+
+static bool mlp_ok(const tq_hip_mlp_weights *w, int n) {
+    return w && n > 0 && w->wgate && w->wup && w->wdown && shape_ok(w->inter, w->hidden) &&
+           shape_ok(w->hidden, w->inter) && aligned(w->wgate, 16) && aligned(w->wup, 16) && aligned(w->wdown, 16);
+}
+
+size_t tq_hip_mlp_ws_bytes(const tq_hip_mlp_weights *w, int n) {
+    if (!mlp_ok(w, n)) return 0;
+    size_t a, b, c;
+    return mlp_ws(w->hidden, w->inter, n, &a, &b, &c);
+}
+
+int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn, float *d_out, void *d_ws,
+                           size_t ws_bytes, void *stream) {
+    if (!mlp_ok(w, n) || !d_xn || !d_out || !d_ws || !aligned(d_ws, 16) || !aligned(d_xn, 4) ||
+        !aligned(d_out, 4))
+        return TQ_HIP_EINVAL;
+    size_t og, ou, ox;
+    if (ws_bytes < mlp_ws(w->hidden, w->inter, n, &og, &ou, &ox)) return TQ_HIP_EINVAL;
+    unsigned char *ws = (unsigned char *)d_ws;
+    float *gate = (float *)(ws + og), *up = (float *)(ws + ou);
+    block_q8 *xq = (block_q8 *)(ws + ox);
+    const hipStream_t s = (hipStream_t)stream;
+    // model/mlp.c:9-11: quantize xn, then the gate and up matmuls in one launch
+    GemvArgs a;
+    init_args(a, w->hidden);
+    if (fuse_quantize(d_xn, n, a.nb)) {
+        a.x = d_xn;
+        a.xq_out = (unsigned char *)xq;
+    } else {
+        const hipError_t e = tq_launch_quantize(d_xn, xq, n * w->hidden, s);
+        if (e != hipSuccess) return herr(e);
+        a.xq = (const unsigned char *)xq;
+    }
+    a.seg[0] = GemvSeg{(const unsigned char *)w->wgate, gate, w->inter};
+    a.seg[1] = GemvSeg{(const unsigned char *)w->wup, up, w->inter};
+    a.seg_end[0] = w->inter;
+    a.seg_end[1] = a.seg_end[2] = 2 * w->inter;
+    a.rows_total = 2 * w->inter;
+    int rc = run_gemv(a, n, s);
+    if (rc != TQ_HIP_OK) return rc;
+    // :12-13 silu_mul, then quantize the hidden rows (fused)
+    hipError_t e = tq_launch_silu_quant(gate, up, xq, (long)n * w->inter, s);
+    if (e != hipSuccess) return herr(e);
+    // :14 the down matmul
+    GemvArgs d;
+    init_args(d, w->inter);
+    d.seg[0] = GemvSeg{(const unsigned char *)w->wdown, d_out, w->hidden};
+    d.seg_end[0] = d.seg_end[1] = d.seg_end[2] = w->hidden;
+    d.rows_total = w->hidden;
+    d.xq = (const unsigned char *)xq;
+    return run_gemv(d, n, s);
+}
+
 }  // extern "C"

@@ -245,6 +245,8 @@ hipError_t tq_launch_scores(const block_q8 *q, int g, const block_q8 *k, int n, 
 hipError_t tq_launch_accum(const float *w, size_t w_stride, int g, const block_q8 *v, int n,
                            int nb, float *out, size_t out_stride, hipStream_t s);
 hipError_t tq_launch_softmax(float *x, int n, int rows, size_t stride, hipStream_t s);
+// h = silu(g) * u of n floats (rows of whole blocks), quantized to hq.
+hipError_t tq_launch_silu_quant(const float *gate, const float *up, block_q8 *hq, long n, hipStream_t s);
 // In place allowed (out == x); n <= 8191.
 hipError_t tq_launch_rmsnorm_rows(const float *x, const float *w, float *out, int n_rows, int n, float eps,
                                   hipStream_t s);

@@ -1,0 +1,154 @@
+/* tq_model.c — tq_ctx_init / tq_forward_token for a Q8 model on the device
+ * (model/context.c:6-153), composed from libtqhip's kernels.  See
+ * include/tq/tq_model.h.  Built with -ffp-contract=off: the RoPE table is
+ * tq_attn_rope_table, the reference's rope_table arithmetic. */
+#include "tq/tq_model.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+static int check_model(const tq_dev_model *m) {
+    if (!m || !m->embed || !m->final_norm || !m->layers) return -1;
+    const tq_attn_config *a = &m->attn;
+    if (a->hidden_size <= 0 || a->hidden_size % QK != 0 || m->intermediate_size <= 0 ||
+        m->intermediate_size % QK != 0)
+        return -1;
+    if (m->n_layers <= 0 || m->vocab_size <= 0) return -1;
+    if (a->n_q_heads <= 0 || a->n_kv_heads <= 0 || a->head_dim <= 0 || a->head_dim % 2 != 0) return -1;
+    for (int l = 0; l < m->n_layers; l++) {
+        const tq_dev_layer_weights *L = &m->layers[l];
+        if (!L->input_norm || !L->post_norm || !L->attn.wq || !L->attn.wk || !L->attn.wv || !L->attn.wo ||
+            !L->attn.q_norm || !L->attn.k_norm || !L->mlp.wgate || !L->mlp.wup || !L->mlp.wdown)
+            return -1;
+        if (L->attn.hidden != a->hidden_size || L->mlp.hidden != a->hidden_size ||
+            L->mlp.inter != m->intermediate_size)
+            return -1;
+    }
+    return 0;
+}
+
+static int dmalloc(void **p, size_t bytes) { return tq_hip_malloc(p, bytes) == TQ_HIP_OK ? 0 : -1; }
+
+int tq_dev_ctx_init(tq_dev_ctx *ctx, const tq_dev_model *m, int max_tokens) {
+    memset(ctx, 0, sizeof *ctx);
+    if (check_model(m) != 0 || max_tokens <= 0) return -1;
+    const tq_attn_config *a = &m->attn;
+    const int hidden = a->hidden_size, vocab = m->vocab_size, half = a->head_dim / 2;
+    ctx->model = m;
+    ctx->max_tokens = max_tokens;
+    ctx->caches = calloc((size_t)m->n_layers, sizeof(tq_kv_cache));
+    if (!ctx->caches) return -1;
+    for (int l = 0; l < m->n_layers; l++) {
+        if (tq_kv_cache_init(&ctx->caches[l], TQ_KV_Q8_DEVICE, a, max_tokens) != 0) {
+            tq_dev_ctx_free(ctx);
+            return -1;
+        }
+    }
+    ctx->stream = tq_hip_kv_stream(ctx->caches[0].dev);
+    size_t ws = tq_hip_attention_layer_ws_bytes(ctx->caches[0].dev, &m->layers[0].attn, 1);
+    const size_t ws_mlp = tq_hip_mlp_ws_bytes(&m->layers[0].mlp, 1);
+    if (ws_mlp > ws) ws = ws_mlp;
+    if (ws == 0) {
+        tq_dev_ctx_free(ctx);
+        return -1;
+    }
+    ctx->ws_bytes = ws;
+    const size_t tb = (size_t)max_tokens * half * sizeof(float);
+    if (dmalloc((void **)&ctx->x, (size_t)hidden * 4) || dmalloc((void **)&ctx->xn, (size_t)hidden * 4) ||
+        dmalloc((void **)&ctx->y, (size_t)hidden * 4) || dmalloc((void **)&ctx->logits, (size_t)vocab * 4) ||
+        dmalloc((void **)&ctx->cos_t, tb) || dmalloc((void **)&ctx->sin_t, tb) ||
+        dmalloc((void **)&ctx->positions, (size_t)max_tokens * sizeof(int32_t)) || dmalloc(&ctx->ws, ws) ||
+        dmalloc((void **)&ctx->sampled, sizeof(int32_t))) {
+        tq_dev_ctx_free(ctx);
+        return -1;
+    }
+    /* RoPE table for every position and the position list, once */
+    float *hc = malloc(tb), *hs = malloc(tb);
+    int32_t *hp = malloc((size_t)max_tokens * sizeof(int32_t));
+    int rc = (hc && hs && hp) ? 0 : -1;
+    for (int p = 0; rc == 0 && p < max_tokens; p++) {
+        tq_attn_rope_table(hc + (size_t)p * half, hs + (size_t)p * half, a->head_dim, p, a->rope_theta);
+        hp[p] = p;
+    }
+    if (rc == 0 && (tq_hip_memcpy_h2d(ctx->cos_t, hc, tb, NULL) != TQ_HIP_OK ||
+                    tq_hip_memcpy_h2d(ctx->sin_t, hs, tb, NULL) != TQ_HIP_OK ||
+                    tq_hip_memcpy_h2d(ctx->positions, hp, (size_t)max_tokens * sizeof(int32_t), NULL) !=
+                        TQ_HIP_OK))
+        rc = -1;
+    free(hc);
+    free(hs);
+    free(hp);
+    if (rc != 0) tq_dev_ctx_free(ctx);
+    return rc;
+}
+
+void tq_dev_ctx_free(tq_dev_ctx *ctx) {
+    if (!ctx) return;
+    if (ctx->stream) tq_hip_stream_synchronize(ctx->stream);
+    if (ctx->caches && ctx->model)
+        for (int l = 0; l < ctx->model->n_layers; l++) tq_kv_cache_free(&ctx->caches[l]);
+    free(ctx->caches);
+    tq_hip_free(ctx->x);
+    tq_hip_free(ctx->xn);
+    tq_hip_free(ctx->y);
+    tq_hip_free(ctx->logits);
+    tq_hip_free(ctx->cos_t);
+    tq_hip_free(ctx->sin_t);
+    tq_hip_free(ctx->positions);
+    tq_hip_free(ctx->ws);
+    tq_hip_free(ctx->sampled);
+    memset(ctx, 0, sizeof *ctx);
+}
+
+#define TRY(expr)                      \
+    do {                               \
+        const int rc_ = (expr);        \
+        if (rc_ != TQ_HIP_OK) return rc_; \
+    } while (0)
+
+int tq_dev_forward_token(tq_dev_ctx *ctx, int token) {
+    if (!ctx || !ctx->model) return -1;
+    if (ctx->pos >= ctx->max_tokens) return -1;
+    const tq_dev_model *m = ctx->model;
+    const tq_attn_config *a = &m->attn;
+    const int hidden = a->hidden_size, half = a->head_dim / 2, pos = ctx->pos;
+    void *s = ctx->stream;
+    if (token < 0 || token >= m->vocab_size) return -1;
+    /* :134 embed_lookup */
+    TRY(tq_hip_embed_lookup_q8(m->embed, m->vocab_size, hidden, token, ctx->x, s));
+    const float *pending = NULL;   /* the previous block's output, added in the next norm */
+    for (int l = 0; l < m->n_layers; l++) {
+        const tq_dev_layer_weights *L = &m->layers[l];
+        /* :84,89 (x += mlp of the previous layer) rmsnorm(input_norm) */
+        TRY(tq_hip_add_rmsnorm(ctx->x, pending, L->input_norm, ctx->xn, 1, hidden, a->rms_eps, s));
+        /* :86-87 attention_layer */
+        TRY(tq_hip_attention_layer_async(ctx->caches[l].dev, &L->attn, 1, NULL, ctx->positions + pos, pos,
+                                         ctx->xn, ctx->cos_t + (size_t)pos * half,
+                                         ctx->sin_t + (size_t)pos * half, ctx->y, ctx->ws, ctx->ws_bytes, s));
+        /* :89 x += attn, :96 rmsnorm(post_norm) */
+        TRY(tq_hip_add_rmsnorm(ctx->x, ctx->y, L->post_norm, ctx->xn, 1, hidden, a->rms_eps, s));
+        /* :98-99 mlp_layer */
+        TRY(tq_hip_mlp_layer_async(&L->mlp, 1, ctx->xn, ctx->y, ctx->ws, ctx->ws_bytes, s));
+        pending = ctx->y;
+    }
+    /* :101 x += mlp, :147 rmsnorm(final_norm), :148 lm_head */
+    TRY(tq_hip_add_rmsnorm(ctx->x, pending, m->final_norm, ctx->xn, 1, hidden, a->rms_eps, s));
+    TRY(tq_hip_project_output(m->embed, m->vocab_size, hidden, ctx->xn, 1, (block_q8 *)ctx->ws, ctx->logits, s));
+    ctx->pos++;
+    return 0;
+}
+
+int tq_dev_logits(tq_dev_ctx *ctx, float *host) {
+    if (!ctx || !ctx->model || !host) return -1;
+    TRY(tq_hip_memcpy_d2h(host, ctx->logits, (size_t)ctx->model->vocab_size * sizeof(float), ctx->stream));
+    return tq_hip_stream_synchronize(ctx->stream);
+}
+
+int tq_dev_sample_greedy(tq_dev_ctx *ctx) {
+    if (!ctx || !ctx->model) return -1;
+    TRY(tq_hip_sample_greedy(ctx->logits, ctx->model->vocab_size, ctx->sampled, ctx->stream));
+    int32_t tok = -1;
+    TRY(tq_hip_memcpy_d2h(&tok, ctx->sampled, sizeof tok, ctx->stream));
+    TRY(tq_hip_stream_synchronize(ctx->stream));
+    return tok;
+}

@@ -77,6 +77,11 @@ _PROTOS = {
     "tq_hip_attention_layer_async": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "tq_hip_rmsnorm_rows": (_i, [_vp, _vp, _vp, _i, _i, C.c_float, _vp]),
     "tq_hip_attention_layer_batch_async": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "tq_hip_mlp_ws_bytes": (_sz, [_vp, _i]),
+    "tq_hip_mlp_layer_async": (_i, [_vp, _i, _vp, _vp, _vp, _sz, _vp]),
+    "tq_hip_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, C.c_float, _vp]),
+    "tq_hip_embed_lookup_q8": (_i, [_vp, _i, _i, _i, _vp, _vp]),
+    "tq_hip_sample_greedy": (_i, [_vp, _i, _vp, _vp]),
     "tq_hip_q8_matrix_bytes": (_sz, [_i, _i]),
     "tq_hip_q8_pack": (_i, [_vp, _vp, _i, _i, _vp]),
     "tq_hip_q8_unpack": (_i, [_vp, _vp, _i, _i, _vp]),
@@ -133,6 +138,12 @@ def device_arch() -> str:
     buf = C.create_string_buffer(256)
     check(load().tq_hip_device_arch(buf, 256), "tq_hip_device_arch")
     return buf.value.decode()
+
+
+class MlpWeights(C.Structure):
+    """tq_hip_mlp_weights: device gate/up/down matrices (tiled Q8)."""
+    _fields_ = [("wgate", C.c_void_p), ("wup", C.c_void_p), ("wdown", C.c_void_p), ("hidden", C.c_int),
+                ("inter", C.c_int)]
 
 
 class AttnWeights(C.Structure):

@@ -30,10 +30,10 @@ def cfg_of(attn, nq=8, nkv=2, hd=64, theta=10000.0):
 
 
 def test_exports_every_declared_symbol(attn):
-    names = declared("tq_attn.h", "tq_")
+    names = declared("tq_attn.h", "tq_") | declared("tq_model.h", "tq_")
     names = {n for n in names if not n.startswith("tq_hip_")}
-    assert len(names) == 10
-    assert names == set(attn.EXPORTS), "ctypes prototypes out of step with tq_attn.h"
+    assert len(names) == 15
+    assert names == set(attn.EXPORTS), "ctypes prototypes out of step with tq_attn.h / tq_model.h"
     for n in names:
         assert hasattr(attn.load(), n)
 
@@ -56,6 +56,31 @@ def test_struct_layout_matches_header(attn, tmp_path):
     want = [C.sizeof(K), K.k_q8.offset, K.max_tokens.offset, K.dev.offset,
             C.sizeof(attn.AttnConfig), C.sizeof(C.c_int)]
     assert [int(x) for x in got] == want
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs gcc")
+def test_model_struct_layout_matches_header(attn, tmp_path):
+    """tq_dev_layer_weights / tq_dev_model / tq_dev_ctx and the tq_hip weight
+    structs: the binding's layout is the header's."""
+    src = tmp_path / "layout2.c"
+    fields = [("tq_hip_attn_weights", "rms_eps"), ("tq_hip_mlp_weights", "inter"),
+              ("tq_dev_layer_weights", "post_norm"), ("tq_dev_layer_weights", "mlp"),
+              ("tq_dev_model", "vocab_size"), ("tq_dev_model", "layers"), ("tq_dev_ctx", "ws_bytes"),
+              ("tq_dev_ctx", "sampled")]
+    body = " ".join(f'printf("%zu %zu ", sizeof({t}), offsetof({t}, {f}));' for t, f in fields)
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "tq/tq_model.h"\n'
+                   f"int main(void){{{body} return 0;}}\n")
+    exe = tmp_path / "layout2"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    from tailorquantkernel_amd import native
+    py = {"tq_hip_attn_weights": native.AttnWeights, "tq_hip_mlp_weights": native.MlpWeights,
+          "tq_dev_layer_weights": attn.DevLayerWeights, "tq_dev_model": attn.DevModel, "tq_dev_ctx": attn.DevCtx}
+    want = []
+    for t, f in fields:
+        want += [C.sizeof(py[t]), getattr(py[t], f).offset]
+    assert got == want
 
 
 @pytest.mark.parametrize("kv_type", [0, 1])
