@@ -986,6 +986,257 @@ def cpu_leg_layer(nq, nkv, hd, hidden, T, theta, eps, host_w, qn, kn, xn, budget
                        f"{isa} matmuls, OpenMP (OMP_NUM_THREADS={omp}, nproc={os.cpu_count()})")}
 
 
+class HostModel:
+    """Host copies of a Q8 model in the reference's block_q8 layout, in the shape
+    the oracle's and the reference's forward take; `layers` is a list of dicts
+    of the layer's arrays."""
+
+    def __init__(self, nq, nkv, hd, hidden, inter, vocab, theta, eps, embed, final_norm, layers):
+        self.n_layers, self.nq, self.nkv, self.hd = len(layers), nq, nkv, hd
+        self.hidden, self.inter, self.vocab, self.theta, self.eps = hidden, inter, vocab, theta, eps
+        self.embed, self.final_norm = embed, final_norm
+        self.layers = list(layers)
+
+    def struct(self):
+        from oracle.binding import Model
+        return Model.struct(self)
+
+    def ptr_array(self, key):
+        from oracle.binding import Model
+        return Model.ptr_array(self, key)
+
+
+def bench_forward_8b(args, nat, hip):
+    """tq_forward_token (model/context.c:104-126) for a Llama-3-8B-shaped Q8 model on
+    the device: embedding, 32 x (residual RMSNorm, attention_layer over a 4096-token
+    cache, residual RMSNorm, mlp_layer), final RMSNorm and the lm_head GEMV over
+    128256 rows.  One token per step; a HIP graph of one whole token forward,
+    replayed at the same position so every step attends over 4096 keys."""
+    from tailorquantkernel_amd import attn
+    lib = nat.load()
+    A = attn.load()
+    nl, nq, nkv, hd, hidden, inter, vocab = 32, 32, 8, 128, 4096, 14336, 128256
+    theta, eps, T = 500000.0, 1e-5, 4096
+    qr, kr = nq * hd, nkv * hd
+    nb = hd // QK
+    rng = np.random.default_rng(29)
+    names = ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")
+    dims = dict(wq=(qr, hidden), wk=(kr, hidden), wv=(kr, hidden), wo=(hidden, qr), wgate=(inter, hidden),
+                wup=(inter, hidden), wdown=(hidden, inter))
+    host = {k: random_q8_weights(rng, *dims[k]) for k in names}
+
+    def norm(n):
+        return rng.uniform(0.6, 1.4, n).astype(np.float32)
+
+    for k in ("input_norm", "post_norm"):
+        host[k] = norm(hidden)
+    host["q_norm"], host["k_norm"] = norm(hd), norm(hd)
+    embed = random_q8_weights(rng, vocab, hidden)
+    final_norm = norm(hidden)
+
+    # one layer packed on the device, copied to every layer's own memory
+    nbytes = {k: lib.tq_hip_q8_matrix_bytes(*dims[k]) for k in names}
+    off, o = {}, 0
+    for k in names:
+        off[k] = o
+        o += nbytes[k]
+    layer_bytes = o
+    big = nat.DeviceBuffer(nl * layer_bytes)
+    for k in names:
+        src = nat.DeviceBuffer.from_numpy(host[k])
+        nat.check(lib.tq_hip_q8_pack(big.ptr + off[k], src.ptr, *dims[k], None), "q8_pack")
+        src.free()
+    hip.sync()
+    for l in range(1, nl):
+        nat.check(lib.tq_hip_memcpy_d2d(big.ptr + l * layer_bytes, big.ptr, layer_bytes, None), "d2d")
+    embed_bytes = lib.tq_hip_q8_matrix_bytes(vocab, hidden)
+    dembed = nat.DeviceBuffer(embed_bytes)
+    src = nat.DeviceBuffer.from_numpy(embed)
+    nat.check(lib.tq_hip_q8_pack(dembed.ptr, src.ptr, vocab, hidden, None), "q8_pack")
+    src.free()
+    hip.sync()
+    D = nat.DeviceBuffer.from_numpy
+    dvec = {k: D(host[k]) for k in ("input_norm", "post_norm", "q_norm", "k_norm")}
+    dfinal = D(final_norm)
+    layers = (attn.DevLayerWeights * nl)()
+    for l in range(nl):
+        b = big.ptr + l * layer_bytes
+        layers[l].input_norm = dvec["input_norm"].ptr
+        layers[l].post_norm = dvec["post_norm"].ptr
+        layers[l].attn = nat.AttnWeights(b + off["wq"], b + off["wk"], b + off["wv"], b + off["wo"],
+                                         dvec["q_norm"].ptr, dvec["k_norm"].ptr, hidden, eps)
+        layers[l].mlp = nat.MlpWeights(b + off["wgate"], b + off["wup"], b + off["wdown"], hidden, inter)
+    cfg = attn.AttnConfig(nq, nkv, hd, hidden, theta, eps)
+
+    def dev_model(n_layers):
+        return attn.DevModel(cfg, n_layers, inter, vocab, dembed.ptr, dfinal.ptr, layers)
+
+    # parity: two layers of the same weights, three tokens from empty caches,
+    # against the reference's own tq_forward_token on the host copies (the
+    # oracle's restatement where the reference is not built)
+    from oracle.binding import Oracle, Ref
+    tokens = [17, 90001, 4242]
+    small = dev_model(2)
+    ctx = attn.DevCtx()
+    assert A.tq_dev_ctx_init(C.byref(ctx), C.byref(small), 8) == 0
+    got = []
+    for t in tokens:
+        assert A.tq_dev_forward_token(C.byref(ctx), t) == 0
+        g = np.zeros(vocab, np.float32)
+        assert A.tq_dev_logits(C.byref(ctx), g.ctypes.data) == 0
+        got.append(g)
+    dev_tok = A.tq_dev_sample_greedy(C.byref(ctx))
+    A.tq_dev_ctx_free(C.byref(ctx))
+    hm = HostModel(nq, nkv, hd, hidden, inter, vocab, theta, eps, embed, final_norm, [host, host])
+    if Ref.available():
+        against, ref = "reference tq_forward_token (oracle/_ref), 2 layers, 3 tokens", Ref().forward(hm, tokens, 8)
+    else:
+        against, ref = "oracle forward, 2 layers, 3 tokens", Oracle().forward(hm, tokens, 8)[0]
+    errs = [rel_l2(g, r) for g, r in zip(got, ref)]
+    parity = {"ok": bool(errs[0] <= 1e-4 and max(errs) <= 3e-2 and dev_tok == int(np.argmax(ref[-1]))),
+              "rel_l2_per_token": errs, "greedy_token_equal": dev_tok == int(np.argmax(ref[-1])),
+              "bar": "first token relative L2 <= 1e-4, every token <= 3e-2, greedy token equal",
+              "against": against}
+
+    # the timed model: 32 layers, caches holding 4095 tokens; each step appends
+    # position 4095 and attends over 4096 keys
+    model = dev_model(nl)
+    ctx = attn.DevCtx()
+    assert A.tq_dev_ctx_init(C.byref(ctx), C.byref(model), T) == 0
+    caches = C.cast(ctx.caches, C.POINTER(attn.KVCache))
+    dk_rows = D(normal_rows(rng, 512, nkv * hd))
+    dv_rows = D(normal_rows(rng, 512, nkv * hd))
+
+    class _Handle:
+        def __init__(self, h):
+            self.h = h
+
+    for l in range(nl):
+        fill_sequence(nat, _Handle(caches[l].dev), 0, T - 1, dk_rows, dv_rows, 512, ctx.stream)
+    dk_rows.free()
+    dv_rows.free()
+    stream = ctx.stream
+
+    def step():
+        ctx.pos = T - 1
+        rc = A.tq_dev_forward_token(C.byref(ctx), 1234)
+        if rc != 0:
+            raise RuntimeError(f"tq_dev_forward_token: {rc}")
+
+    for _ in range(max(3, args.warmup // 16)):
+        step()
+    hip.sync()
+    graph, _ = hip.capture(stream, step)
+    for _ in range(2):
+        hip.launch_graph(graph, stream)
+    hip.sync()
+    reps = max(5, args.steps // 64)
+    ms = timed(hip, stream, reps, lambda: hip.launch_graph(graph, stream))
+    hip.sync()
+
+    # the two halves of a layer on their own, over the same 32 layers
+    ws = ctx.ws
+    wsb = ctx.ws_bytes
+    dpos = ctx.positions + 4 * (T - 1)
+    half = hd // 2
+    cos_p, sin_p = ctx.cos_t + 4 * (T - 1) * half, ctx.sin_t + 4 * (T - 1) * half
+
+    def attn_all():
+        for l in range(nl):
+            nat.check(lib.tq_hip_attention_layer_async(caches[l].dev, C.byref(layers[l].attn), 1, None, dpos, T - 1,
+                                                       ctx.xn, cos_p, sin_p, ctx.y, ws, wsb, stream), "attention")
+
+    def mlp_all():
+        for l in range(nl):
+            nat.check(lib.tq_hip_mlp_layer_async(C.byref(layers[l].mlp), 1, ctx.xn, ctx.y, ws, wsb, stream), "mlp")
+
+    parts = {}
+    for name, fn in (("attention", attn_all), ("mlp", mlp_all)):
+        fn()
+        hip.sync()
+        g, _ = hip.capture(stream, fn)
+        hip.launch_graph(g, stream)
+        hip.sync()
+        parts[name] = timed(hip, stream, reps, lambda: hip.launch_graph(g, stream))
+    hip.sync()
+
+    kv_bytes = nl * T * nkv * 2 * nb * BLOCK_BYTES
+    step_bytes = nl * layer_bytes + embed_bytes + kv_bytes + hidden * BLOCK_BYTES // QK
+    achieved = step_bytes / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "Q8 model decode tokens/sec (tq_forward_token, Llama-3-8B shape, ctx 4096, batch 1), 1 GPU",
+        "value": 1e3 / ms, "unit": "tokens/s", "n_gpus": 1, "steps": reps, "warmup": max(3, args.warmup // 16),
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": ("tq_forward_token of one token at position 4095: Q8 embedding, 32 x (residual "
+                                "RMSNorm, attention_layer 32q/8kv/hd128 over 4096 keys, residual RMSNorm, "
+                                "mlp_layer 4096->14336->4096), final RMSNorm, lm_head 128256 x 4096; all 32 "
+                                "layers' weights distinct in memory (one random layer copied), one HIP graph "
+                                "per token"),
+                   "n_layers": nl, "hidden": hidden, "intermediate": inter, "vocab": vocab, "context": T,
+                   "weight_bytes": nl * layer_bytes + embed_bytes, "kv_bytes": kv_bytes,
+                   "bytes_per_step": step_bytes},
+        "ms_attention_32_layers": parts["attention"], "ms_mlp_32_layers": parts["mlp"],
+        "parity": parity,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "whole token forward (gemv_q8_kernel projections, MLP and lm_head, decode3_kernel, "
+                               "norms): weight + KV bytes over the step",
+                     "kernel_ms": ms, "algorithmic_bytes": step_bytes},
+    }
+    A.tq_dev_ctx_free(C.byref(ctx))
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_leg_forward(host, embed, final_norm, (nq, nkv, hd, hidden, inter, vocab, theta,
+                                                                         eps), args.cpu_budget)
+    big.free()
+    dembed.free()
+    return line
+
+
+def cpu_leg_forward(host, embed, final_norm, shape, budget_s: float):
+    """The reference's own tq_forward_token (oracle/_ref: AVX2 matmuls, OpenMP) on
+    1- and 3-layer models (distinct weights in memory), 8 tokens from empty caches per call;
+    the 32-layer rate is t(1 layer) + 31 x (t(3 layers) - t(1 layer)) / 2 per token.
+    The short context makes the sample's attention cheaper than at 4096 keys,
+    which favours the CPU."""
+    from oracle.binding import Oracle, Ref
+    nq, nkv, hd, hidden, inter, vocab, theta, eps = shape
+    if Ref.available():
+        kind, ref = "reference", Ref()
+        isa = ref.isa()
+
+        def fwd(m, toks):
+            return ref.forward(m, toks, len(toks))
+    else:
+        kind, isa, o = "port", "scalar", Oracle()
+
+        def fwd(m, toks):
+            return o.forward(m, toks, len(toks))[0]
+    toks = [t % vocab for t in (5, 77, 1234, 99, 100000, 3, 42, 4096)]
+    per = {}
+    t_start = time.perf_counter()
+    # the later layers are copies in their own memory, as in a real model
+    stack = [host] + [{k: v.copy() for k, v in host.items()} for _ in range(2)]
+    for n_layers in (1, 3):
+        m = HostModel(nq, nkv, hd, hidden, inter, vocab, theta, eps, embed, final_norm, stack[:n_layers])
+        fwd(m, toks[:2])
+        times = []
+        t0s = time.perf_counter()
+        while (time.perf_counter() - t0s < budget_s / 2 and len(times) < 1000) or len(times) < 2:
+            t0 = time.perf_counter()
+            fwd(m, toks)
+            times.append((time.perf_counter() - t0) / len(toks))
+        per[n_layers] = float(np.median(times))
+    t32 = per[1] + 31 * max(per[3] - per[1], 0.0) / 2
+    omp = int(os.environ.get("OMP_NUM_THREADS", str(os.cpu_count() or 1)))
+    return {"value": 1.0 / t32, "unit": "tokens/s", "cores": min(omp, os.cpu_count() or 1) if kind == "reference"
+            else 1, "kind": kind,
+            "sample": (f"tq_forward_token over 8 tokens from empty caches, 1-layer model {per[1] * 1e3:.2f} ms/token, "
+                       f"3-layer {per[3] * 1e3:.2f} ms/token (Llama-3-8B layer and vocab shapes), extrapolated to "
+                       f"32 layers; {isa} matmuls, OpenMP (OMP_NUM_THREADS={omp}, nproc={os.cpu_count()}); "
+                       f"{time.perf_counter() - t_start:.0f} s of sampling")}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -993,7 +1244,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--config", default="decode-8b-4k",
                     choices=["decode-8b-4k", "decode-batched", "prefill-2k", "decode-70b-32k", "project-8b",
-                             "project-70b", "layer-8b", "layer-prefill-8b"])
+                             "project-70b", "layer-8b", "layer-prefill-8b", "forward-8b"])
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline sampling")
     ap.add_argument("--no-cpu", action="store_true")
@@ -1019,8 +1270,9 @@ def main():
         line = {"decode-batched": bench_decode_batched, "prefill-2k": bench_prefill_2k,
                 "decode-70b-32k": bench_decode_70b, "project-8b": bench_project_8b,
                 "project-70b": bench_project_70b, "layer-8b": bench_layer_8b,
-                "layer-prefill-8b": bench_layer_prefill_8b}[args.config](args, nat, hip)
-    if args.config.startswith(("decode", "project")) or args.config == "layer-8b":
+                "layer-prefill-8b": bench_layer_prefill_8b,
+                "forward-8b": bench_forward_8b}[args.config](args, nat, hip)
+    if args.config.startswith(("decode", "project")) or args.config in ("layer-8b", "forward-8b"):
         # the achievable read rate of this box, beside the 8 TB/s spec peak
         peak = measure_hbm_read(nat, hip)
         line["roofline"]["measured_peak"] = peak

@@ -261,7 +261,7 @@ size_t tq_hip_mlp_ws_bytes(const tq_hip_mlp_weights *w, int n);
 int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn, float *d_out, void *d_ws,
                            size_t ws_bytes, void *stream);
 
-/* The residual add and RMSNorm of model/context.c:83-105 for n_rows rows of n:
+/* The residual add and RMSNorm of model/context.c:80-102 for n_rows rows of n:
  * x += y (model/vec.c:3-6; y may be NULL), then xn = rmsnorm(x, weight)
  * (model/rmsnorm.c:4-19) with the sum of squares taken in parallel (within
  * fp32 rounding of the reference's serial sum; the per-head norms in front
@@ -273,6 +273,13 @@ int tq_hip_add_rmsnorm(float *x, const float *y, const float *weight, float *xn,
  * rows x cols matrix, dequantized into out[cols].  TQ_HIP_EINVAL for a token
  * outside [0, rows), as the reference returns -1. */
 int tq_hip_embed_lookup_q8(const void *embed, int rows, int cols, int token, float *out, void *stream);
+/* The embed_lookup loop of tq_forward_batch (model/context.c:184-187) for n
+ * tokens held on the device: row i of out[n][cols] <- row d_tokens[i].  The
+ * caller checks the tokens (the reference returns -1 for one outside [0,
+ * rows)); the kernel writes zeros for such a row rather than read outside the
+ * matrix.  n at most 65535. */
+int tq_hip_embed_lookup_q8_batch(const void *embed, int rows, int cols, const int32_t *d_tokens, int n, float *out,
+                                 void *stream);
 
 /* sample_greedy (model/sampler.c:3-13): the first index of the largest of n
  * logits (strict >, so NaN never wins and ties keep the lower index), written

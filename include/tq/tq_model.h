@@ -1,6 +1,6 @@
 /* tq_model.h — a Q8 model's token forward on one MI355X: the device
  * counterpart of tq_ctx_init / tq_forward_token (model/context.c:6-52,
- * 128-153), in libtqattn.so over libtqhip.so.
+ * 104-126), in libtqattn.so over libtqhip.so.
  *
  * Weights live on the device (tiled Q8 matrices made by tq_hip_q8_pack, fp32
  * norm rows); the context owns one TQ_KV_Q8_DEVICE cache per layer, the
@@ -28,7 +28,7 @@ typedef struct {
 
 /* tq_model (model/model_ops.h:50-73), device pointers; `layers` is a host
  * array of n_layers.  embed (vocab x hidden, tiled Q8) is also the lm_head
- * (model/embedding.c:34-38). */
+ * (model/embedding.c:35-40). */
 typedef struct {
     tq_attn_config attn;
     int n_layers;
@@ -62,11 +62,50 @@ int tq_dev_ctx_init(tq_dev_ctx *ctx, const tq_dev_model *m, int max_tokens);
 /* model/context.c:55-77; idempotent. */
 void tq_dev_ctx_free(tq_dev_ctx *ctx);
 
-/* model/context.c:128-153: embed_lookup, per layer rmsnorm -> attention_layer
+/* model/context.c:104-126: embed_lookup, per layer rmsnorm -> attention_layer
  * -> residual add -> rmsnorm -> mlp_layer -> residual add, then the final
  * rmsnorm and lm_head into ctx->logits; pos advances.  -1 for pos >=
  * max_tokens or a token outside [0, vocab_size) before any launch. */
 int tq_dev_forward_token(tq_dev_ctx *ctx, int token);
+/* tq_batch_ws (model/model_ops.h:146-154) for the device: activations of up
+ * to cap tokens, their token ids, and the workspace of the batched attention
+ * and MLP calls (sized on the first tq_dev_forward_batch, which knows the
+ * cache). */
+typedef struct {
+    int cap;
+    float *x, *xn, *y;            /* device [cap][hidden] */
+    int32_t *tokens;              /* device [cap] */
+    void *ws;
+    size_t ws_bytes;
+} tq_dev_batch_ws;
+
+/* model/context.c:141-172: -1 for a NULL model or cap <= 0 or an allocation
+ * failure (everything allocated so far is freed). */
+int tq_dev_batch_ws_init(tq_dev_batch_ws *ws, const tq_dev_model *m, int cap);
+/* model/context.c:131-139; idempotent. */
+void tq_dev_batch_ws_free(tq_dev_batch_ws *ws);
+
+/* model/context.c:174-213: n tokens at positions pos .. pos+n-1 in one pass:
+ * embed_lookup of each, then per layer the rows' rmsnorm ->
+ * attention_layer_batch -> residual add -> rmsnorm -> mlp_layer_batch ->
+ * residual add; with want_logits the last token's final rmsnorm and lm_head
+ * into ctx->logits.  pos advances by n.  -1, before any launch, for n <= 0, n
+ * > ws->cap, pos + n > max_tokens or a token outside [0, vocab_size).  The
+ * token ids are copied to the device through the stream, which is waited for
+ * once after that copy; everything else is only enqueued. */
+int tq_dev_forward_batch(tq_dev_ctx *ctx, tq_dev_batch_ws *ws, const int *tokens, int n, int want_logits);
+
+/* Tokens per tq_dev_forward_batch call of tq_dev_prefill.  The reference
+ * uses 16 (model/model_ops.h:144), sized for its CPU; the device's batched
+ * matmuls and causal attention want hundreds of tokens per call.  The chunk
+ * changes only rounding: every token attends to all tokens before it. */
+#define TQ_DEV_PREFILL_BATCH 512
+
+/* model/context.c:215-229: the whole prompt in chunks of
+ * TQ_DEV_PREFILL_BATCH, logits of the last token in ctx->logits.  -1 for n
+ * <= 0 or pos + n > max_tokens. */
+int tq_dev_prefill(tq_dev_ctx *ctx, const int *tokens, int n);
+
 /* Wait for the stream and copy the last token's logits to host[vocab]. */
 int tq_dev_logits(tq_dev_ctx *ctx, float *host);
 /* sample_greedy (model/sampler.c:3-13) of the last token's logits on the

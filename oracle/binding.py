@@ -320,6 +320,8 @@ class Ref:
         L.tqref_mlp_run.restype = _i
         L.tqref_forward_run.argtypes = [_i] * 7 + [_f, _f] + [_vp] * 13 + [_i, _i, _vp, _vp]
         L.tqref_forward_run.restype = _i
+        L.tqref_prefill_run.argtypes = [_i] * 7 + [_f, _f] + [_vp] * 13 + [_i, _i, _vp, _vp, _vp, _vp]
+        L.tqref_prefill_run.restype = _i
         L.pack_matrix.argtypes = [_vp, _i, _i, _vp, C.c_char]
         L.pack_matrix.restype = _i
         simd = ("matmul_q8_avx2",) if not scalar else ()
@@ -347,6 +349,26 @@ class Ref:
                                             "wgate", "wup", "wdown")], max_tokens, len(toks), ptr(toks), ptr(out))
         assert rc == 0, rc
         return out
+
+    def prefill(self, model, tokens, max_tokens):
+        """The reference's tq_prefill over `tokens` on fresh TQ_KV_Q8 caches: the last
+        token's logits [vocab] and per-layer K and V caches."""
+        st, keep = model.struct()
+        toks = np.ascontiguousarray(tokens, np.int32)
+        out = np.zeros(model.vocab, np.float32)
+        nb = model.hd // QK
+        kc = [blocks(model.nkv * max_tokens * nb) for _ in range(model.n_layers)]
+        vc = [blocks(model.nkv * max_tokens * nb) for _ in range(model.n_layers)]
+        karr = (C.c_void_p * model.n_layers)(*[ptr(c) for c in kc])
+        varr = (C.c_void_p * model.n_layers)(*[ptr(c) for c in vc])
+        rc = self.lib.tqref_prefill_run(model.n_layers, model.nq, model.nkv, model.hd, model.hidden, model.inter,
+                                        model.vocab, model.theta, model.eps, ptr(model.embed),
+                                        ptr(model.final_norm), *[keep[k] for k in (
+                                            "input_norm", "post_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm",
+                                            "wgate", "wup", "wdown")], max_tokens, len(toks), ptr(toks), ptr(out),
+                                        karr, varr)
+        assert rc == 0, rc
+        return out, kc, vc
 
     def rmsnorm(self, x, weight, eps: float) -> np.ndarray:
         w = f32(weight)

@@ -203,25 +203,22 @@ int tqref_mlp_run(int hidden, int inter, const block_q8 *wgate, const block_q8 *
     return rc;
 }
 
-/* The reference's own tq_ctx_init + tq_forward_token (model/context.c:6-52,
- * 128-153) over n_tok tokens on a Q8 model given as flat per-layer pointer
- * arrays, with TQ_KV_Q8 caches; logits [n_tok][vocab].  Returns the first
- * nonzero code, or 0. */
-int tqref_forward_run(int n_layers, int nq, int nkv, int hd, int hidden, int inter, int vocab,
-                      float theta, float eps, const block_q8 *embed, const float *final_norm,
-                      const float *const *input_norm, const float *const *post_norm,
-                      const block_q8 *const *wq, const block_q8 *const *wk,
-                      const block_q8 *const *wv, const block_q8 *const *wo,
-                      const float *const *qn, const float *const *kn,
-                      const block_q8 *const *wgate, const block_q8 *const *wup,
-                      const block_q8 *const *wdown, int max_tokens, int n_tok, const int *tokens,
-                      float *logits) {
+/* A tq_model over flat per-layer pointer arrays; *layers_out is the layer
+ * array to free. */
+#define TQREF_MODEL_ARGS                                                                                 \
+    int n_layers, int nq, int nkv, int hd, int hidden, int inter, int vocab, float theta, float eps,     \
+        const block_q8 *embed, const float *final_norm, const float *const *input_norm,                  \
+        const float *const *post_norm, const block_q8 *const *wq, const block_q8 *const *wk,             \
+        const block_q8 *const *wv, const block_q8 *const *wo, const float *const *qn,                   \
+        const float *const *kn, const block_q8 *const *wgate, const block_q8 *const *wup,                \
+        const block_q8 *const *wdown
+
+static int build_model(tq_model *m, tq_layer_weights **layers_out, TQREF_MODEL_ARGS) {
     tq_layer_weights *layers = calloc((size_t)n_layers, sizeof *layers);
     if (!layers) return -100;
-    tq_model m;
-    memset(&m, 0, sizeof m);
+    memset(m, 0, sizeof *m);
     for (int l = 0; l < n_layers; l++) {
-        make_layer(&layers[l].attn, &m.cfg.attn, nq, nkv, hd, hidden, theta, eps, wq[l], wk[l], wv[l],
+        make_layer(&layers[l].attn, &m->cfg.attn, nq, nkv, hd, hidden, theta, eps, wq[l], wk[l], wv[l],
                    wo[l], qn[l], kn[l]);
         layers[l].input_norm = input_norm[l];
         layers[l].post_norm = post_norm[l];
@@ -229,17 +226,60 @@ int tqref_forward_run(int n_layers, int nq, int nkv, int hd, int hidden, int int
         bind(&layers[l].mlp.wup, wup[l], inter, hidden);
         bind(&layers[l].mlp.wdown, wdown[l], hidden, inter);
     }
-    m.cfg.n_layers = n_layers;
-    m.cfg.intermediate_size = inter;
-    m.cfg.vocab_size = vocab;
-    bind(&m.w.embed, embed, vocab, hidden);
-    m.w.final_norm = final_norm;
-    m.w.layers = layers;
+    m->cfg.n_layers = n_layers;
+    m->cfg.intermediate_size = inter;
+    m->cfg.vocab_size = vocab;
+    bind(&m->w.embed, embed, vocab, hidden);
+    m->w.final_norm = final_norm;
+    m->w.layers = layers;
+    *layers_out = layers;
+    return 0;
+}
+
+#define TQREF_MODEL_PASS                                                                                \
+    n_layers, nq, nkv, hd, hidden, inter, vocab, theta, eps, embed, final_norm, input_norm, post_norm, wq, \
+        wk, wv, wo, qn, kn, wgate, wup, wdown
+
+/* The reference's own tq_ctx_init + tq_forward_token (model/context.c:6-52,
+ * 104-126) over n_tok tokens on a Q8 model given as flat per-layer pointer
+ * arrays, with TQ_KV_Q8 caches; logits [n_tok][vocab].  Returns the first
+ * nonzero code, or 0. */
+int tqref_forward_run(TQREF_MODEL_ARGS, int max_tokens, int n_tok, const int *tokens, float *logits) {
+    tq_model m;
+    tq_layer_weights *layers = NULL;
+    int rc = build_model(&m, &layers, TQREF_MODEL_PASS);
+    if (rc != 0) return rc;
     tq_ctx ctx;
-    int rc = tq_ctx_init(&ctx, &m, TQ_KV_Q8, max_tokens);
+    rc = tq_ctx_init(&ctx, &m, TQ_KV_Q8, max_tokens);
     for (int i = 0; rc == 0 && i < n_tok; i++) {
         rc = tq_forward_token(&ctx, tokens[i]);
         if (rc == 0) memcpy(logits + (size_t)i * vocab, ctx.logits, (size_t)vocab * sizeof(float));
+    }
+    tq_ctx_free(&ctx);
+    free(layers);
+    return rc;
+}
+
+/* The reference's own tq_prefill (model/context.c:215-229: tq_forward_batch
+ * in chunks of TQ_PREFILL_BATCH) over n_tok tokens on fresh TQ_KV_Q8 caches:
+ * the last token's logits [vocab], and each layer's K and V caches
+ * ([n_kv][max_tokens][hd/32] block_q8) into k_out[l] / v_out[l] when given. */
+int tqref_prefill_run(TQREF_MODEL_ARGS, int max_tokens, int n_tok, const int *tokens, float *logits,
+                      block_q8 *const *k_out, block_q8 *const *v_out) {
+    tq_model m;
+    tq_layer_weights *layers = NULL;
+    int rc = build_model(&m, &layers, TQREF_MODEL_PASS);
+    if (rc != 0) return rc;
+    tq_ctx ctx;
+    rc = tq_ctx_init(&ctx, &m, TQ_KV_Q8, max_tokens);
+    if (rc == 0) rc = tq_prefill(&ctx, tokens, n_tok);
+    if (rc == 0) {
+        memcpy(logits, ctx.logits, (size_t)vocab * sizeof(float));
+        const size_t cache = (size_t)nkv * max_tokens * (hd / QK) * sizeof(block_q8);
+        for (int l = 0; k_out && v_out && l < n_layers; l++) {
+            memcpy(k_out[l], ctx.caches[l].k_q8, cache);
+            memcpy(v_out[l], ctx.caches[l].v_q8, cache);
+        }
     }
     tq_ctx_free(&ctx);
     free(layers);

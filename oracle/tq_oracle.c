@@ -385,10 +385,10 @@ int oracle_sample_greedy(const float *logits, int n) {
     return idx;
 }
 
-/* model/context.c:128-153 (tq_forward_token) with Q8 weights and the flat Q8
+/* model/context.c:104-126 (tq_forward_token) with Q8 weights and the flat Q8
  * caches: embed_lookup, per layer rmsnorm(input_norm) -> attention_layer ->
  * x += attn (vec_add, model/vec.c:3-6) -> rmsnorm(post_norm) -> mlp_layer ->
- * x += mlp, then rmsnorm(final_norm) and lm_head (model/embedding.c:34-38:
+ * x += mlp, then rmsnorm(final_norm) and lm_head (model/embedding.c:35-40:
  * quantize + matmul against the embedding).  Per-layer pointers come in arrays
  * of n_layers; caches[l] are [n_kv][max_tokens][nb] K then V arrays. */
 int oracle_forward_token(const struct oracle_model *m, block_q8 *const *k_caches,

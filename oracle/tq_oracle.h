@@ -108,7 +108,7 @@ struct oracle_model {
     const block_q8 *const *wgate, *const *wup, *const *wdown;
 };
 
-/* model/context.c:128-153 (tq_forward_token) on flat Q8 caches. */
+/* model/context.c:104-126 (tq_forward_token) on flat Q8 caches. */
 int oracle_forward_token(const struct oracle_model *m, block_q8 *const *k_caches,
                          block_q8 *const *v_caches, int max_tokens, int pos, int token, float *logits);
 

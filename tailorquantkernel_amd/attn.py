@@ -45,6 +45,12 @@ class DevModel(C.Structure):
                 ("embed", _vp), ("final_norm", _vp), ("layers", C.POINTER(DevLayerWeights))]
 
 
+class DevBatchWs(C.Structure):
+    """tq_dev_batch_ws: tq_batch_ws (model/model_ops.h:146-154) for the device."""
+    _fields_ = [("cap", _i), ("x", _vp), ("xn", _vp), ("y", _vp), ("tokens", _vp), ("ws", _vp),
+                ("ws_bytes", C.c_size_t)]
+
+
 class DevCtx(C.Structure):
     """tq_dev_ctx: tq_ctx (model/model_ops.h:75-95) for the device."""
     _fields_ = [("model", _vp), ("caches", _vp), ("pos", _i), ("max_tokens", _i), ("stream", _vp),
@@ -54,6 +60,7 @@ class DevCtx(C.Structure):
 
 _PC, _PK = C.POINTER(AttnConfig), C.POINTER(KVCache)
 _PM, _PX = C.POINTER(DevModel), C.POINTER(DevCtx)
+_PB = C.POINTER(DevBatchWs)
 
 _PROTOS = {
     "tq_kv_cache_init": (_i, [_PK, _i, _PC, _i]),
@@ -69,6 +76,10 @@ _PROTOS = {
     "tq_dev_ctx_init": (_i, [_PX, _PM, _i]),
     "tq_dev_ctx_free": (None, [_PX]),
     "tq_dev_forward_token": (_i, [_PX, _i]),
+    "tq_dev_batch_ws_init": (_i, [_PB, _PM, _i]),
+    "tq_dev_batch_ws_free": (None, [_PB]),
+    "tq_dev_forward_batch": (_i, [_PX, _PB, _vp, _i, _i]),
+    "tq_dev_prefill": (_i, [_PX, _vp, _i]),
     "tq_dev_logits": (_i, [_PX, _vp]),
     "tq_dev_sample_greedy": (_i, [_PX]),
 }

@@ -1,7 +1,7 @@
 // block_ops.hip — the rest of a transformer block on gfx950, around the
 // attention layer and the projections: the MLP's silu_mul + quantize
 // (model/silu.c:6-18, model/mlp.c:3-17), the residual add + RMSNorm
-// (model/vec.c:3-6, model/rmsnorm.c:4-19, model/context.c:83-105), the Q8
+// (model/vec.c:3-6, model/rmsnorm.c:4-19, model/context.c:80-102), the Q8
 // embedding lookup (model/embedding.c:4-17) and the greedy sampler
 // (model/sampler.c:3-13).
 #include "tq_common.hpp"
@@ -9,6 +9,8 @@
 namespace {
 
 using namespace tq;
+
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 // h = silu(g) * u (silu(x) = x * (1 / (1 + expf(-x)))), then quantize_row_q8
 // of h: one 32-lane group per block, 8 blocks per work-group.  Rows are
@@ -54,11 +56,84 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *__restrict__ x,
     for (int i = threadIdx.x; i < n; i += 256) xnr[i] = xr[i] * inv * w[i];
 }
 
-// One row of a tiled Q8 matrix to fp32: out[b*32 + j] = d_b * code_j.
+// The same with 16-byte accesses and every load of a row issued up front:
+// 1024 threads, K float4 of the row per thread held in registers, so the row
+// costs one round trip to memory instead of one per strided slice.  The sum
+// of squares is per thread (its K float4 in order), then a wave tree, then the
+// 16 waves in order.
+template <int K>
+__global__ __launch_bounds__(1024) void add_rmsnorm4_kernel(float *__restrict__ x, const float *__restrict__ y,
+                                                            const float *__restrict__ w, float *__restrict__ xn,
+                                                            int n, float eps) {
+#pragma clang fp contract(off)
+    __shared__ float part[16];
+    const int n4 = n >> 2;
+    v4f *xr = reinterpret_cast<v4f *>(x + (size_t)blockIdx.x * n);
+    const v4f *yr = y ? reinterpret_cast<const v4f *>(y + (size_t)blockIdx.x * n) : nullptr;
+    const v4f *wr = reinterpret_cast<const v4f *>(w);
+    v4f *xnr = reinterpret_cast<v4f *>(xn + (size_t)blockIdx.x * n);
+    v4f v[K], wv[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = threadIdx.x + 1024 * k;
+        const int ic = i < n4 ? i : n4 - 1;   // clamped: every load is issued unconditionally
+        v[k] = xr[ic];
+        wv[k] = wr[ic];
+    }
+    if (yr) {
+        v4f yv[K];
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int i = threadIdx.x + 1024 * k;
+            yv[k] = yr[i < n4 ? i : n4 - 1];
+        }
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int i = threadIdx.x + 1024 * k;
+            v[k] += yv[k];
+            if (i < n4) xr[i] = v[k];
+        }
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        if (threadIdx.x + 1024 * k < n4) {
+            sum += v[k].x * v[k].x;
+            sum += v[k].y * v[k].y;
+            sum += v[k].z * v[k].z;
+            sum += v[k].w * v[k].w;
+        }
+    }
+    sum = wave_sum(sum);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) total += part[i];
+    const float inv = 1.0f / sqrtf(eps + total / (float)n);
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = threadIdx.x + 1024 * k;
+        if (i < n4) xnr[i] = v[k] * inv * wv[k];
+    }
+}
+
+// One row of a tiled Q8 matrix to fp32: out[b*32 + j] = d_b * code_j.  With
+// `tokens`, grid row y looks up tokens[y] into out + y*cols (a token outside
+// [0, rows) writes zeros).
 __global__ __launch_bounds__(256) void embed_q8_kernel(const unsigned char *__restrict__ E, int rows, int cols,
-                                                       int token, float *__restrict__ out) {
+                                                       int token, const int32_t *__restrict__ tokens,
+                                                       float *__restrict__ out) {
     const int e = blockIdx.x * 256 + threadIdx.x;
     if (e >= cols) return;
+    if (tokens) {
+        token = tokens[blockIdx.y];
+        out += (size_t)blockIdx.y * cols;
+        if (token < 0 || token >= rows) {
+            out[e] = 0.0f;
+            return;
+        }
+    }
     const int nb = cols / kQK;
     const int b = e / kQK, j = e - b * kQK;
     const int g = b / 64, rest = nb - 64 * g, n = rest < 64 ? rest : 64, i = b - 64 * g;
@@ -69,36 +144,77 @@ __global__ __launch_bounds__(256) void embed_q8_kernel(const unsigned char *__re
 }
 
 // The first index of the largest logit, as the serial scan with a strict ">"
-// finds it (NaN never wins; a NaN at index 0 keeps index 0): thread t scans
-// its contiguous slice in order (slice 0 from logits[0], the others from
-// -inf with no index), then thread 0 merges the 256 slices in order.
-__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int n,
-                                                     int32_t *__restrict__ out) {
-    __shared__ float sm[256];
-    __shared__ int si[256];
-    const int per = (n + 255) / 256;
-    const int i0 = threadIdx.x * per, i1 = min(n, i0 + per);
-    float m = threadIdx.x == 0 ? logits[0] : -__builtin_inff();
-    int idx = threadIdx.x == 0 ? 0 : -1;
-    for (int i = (threadIdx.x == 0 ? 1 : i0); i < i1; i++) {
-        const float v = logits[i];
-        if (v > m) {
-            m = v;
-            idx = i;
+// from logits[0] finds it: NaN never wins, and a NaN at index 0 keeps index 0.
+// Every other NaN is skipped, so the answer is the smallest index holding the
+// largest non-NaN value — an order-free reduction of (value, index) pairs with
+// "larger value, then smaller index" wins.  1024 threads; each loads its
+// share in batches of 8 independent float4 (or float) loads.
+__device__ __forceinline__ void arg_better(float v, int i, float &bv, int &bi) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ logits, int n,
+                                                      int32_t *__restrict__ out) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    float bv = -__builtin_inff();
+    int bi = n;   // none yet
+    constexpr int B = 8;
+    if constexpr (VEC) {
+        const v4f *l4 = reinterpret_cast<const v4f *>(logits);
+        const int n4 = n >> 2;
+        for (int u0 = 0; u0 < n4; u0 += 1024 * B) {
+            v4f x[B];
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const int u = u0 + 1024 * b + (int)threadIdx.x;
+                x[b] = l4[u < n4 ? u : n4 - 1];
+            }
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const int u = u0 + 1024 * b + (int)threadIdx.x;
+                if (u < n4) {
+                    arg_better(x[b].x, 4 * u, bv, bi);
+                    arg_better(x[b].y, 4 * u + 1, bv, bi);
+                    arg_better(x[b].z, 4 * u + 2, bv, bi);
+                    arg_better(x[b].w, 4 * u + 3, bv, bi);
+                }
+            }
+        }
+    } else {
+        for (int e0 = 0; e0 < n; e0 += 1024 * B) {
+            float x[B];
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const int e = e0 + 1024 * b + (int)threadIdx.x;
+                x[b] = logits[e < n ? e : n - 1];
+            }
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                const int e = e0 + 1024 * b + (int)threadIdx.x;
+                if (e < n) arg_better(x[b], e, bv, bi);
+            }
         }
     }
-    sm[threadIdx.x] = m;
-    si[threadIdx.x] = idx;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        arg_better(ov, oi, bv, bi);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
-        float bm = sm[0];
-        int bi = si[0];
-        for (int t = 1; t < 256; t++)
-            if (si[t] >= 0 && sm[t] > bm) {
-                bm = sm[t];
-                bi = si[t];
-            }
-        *out = bi;
+        for (int w = 1; w < 16; w++) arg_better(sv[w], si[w], bv, bi);
+        const float first = logits[0];
+        *out = (first != first || bi >= n) ? 0 : bi;
     }
 }
 
@@ -120,8 +236,20 @@ int tq_hip_add_rmsnorm(float *x, const float *y, const float *weight, float *xn,
                        void *stream) {
     if (n_rows < 0 || n <= 0 || (n_rows > 0 && (!x || !weight || !xn))) return TQ_HIP_EINVAL;
     if (n_rows == 0) return TQ_HIP_OK;
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)n_rows), dim3(256), 0, (hipStream_t)stream, x, y, weight,
-                       xn, n, eps);
+    const hipStream_t s = (hipStream_t)stream;
+    const bool vec = n % 4 == 0 && (((uintptr_t)x | (uintptr_t)y | (uintptr_t)weight | (uintptr_t)xn) & 15) == 0;
+    const int k = (n / 4 + 1023) / 1024;
+    const dim3 grid((unsigned)n_rows);
+    if (vec && k == 1)
+        hipLaunchKernelGGL(add_rmsnorm4_kernel<1>, grid, dim3(1024), 0, s, x, y, weight, xn, n, eps);
+    else if (vec && k == 2)
+        hipLaunchKernelGGL(add_rmsnorm4_kernel<2>, grid, dim3(1024), 0, s, x, y, weight, xn, n, eps);
+    else if (vec && k <= 4)
+        hipLaunchKernelGGL(add_rmsnorm4_kernel<4>, grid, dim3(1024), 0, s, x, y, weight, xn, n, eps);
+    else if (vec && k <= 8)
+        hipLaunchKernelGGL(add_rmsnorm4_kernel<8>, grid, dim3(1024), 0, s, x, y, weight, xn, n, eps);
+    else
+        hipLaunchKernelGGL(add_rmsnorm_kernel, grid, dim3(256), 0, s, x, y, weight, xn, n, eps);
     return herr(hipGetLastError());
 }
 
@@ -129,13 +257,27 @@ int tq_hip_embed_lookup_q8(const void *embed, int rows, int cols, int token, flo
     if (!embed || !out || rows <= 0 || cols <= 0 || cols % kQK != 0 || ((uintptr_t)embed & 15)) return TQ_HIP_EINVAL;
     if (token < 0 || token >= rows) return TQ_HIP_EINVAL;   // model/embedding.c:5
     hipLaunchKernelGGL(embed_q8_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                       (const unsigned char *)embed, rows, cols, token, out);
+                       (const unsigned char *)embed, rows, cols, token, nullptr, out);
+    return herr(hipGetLastError());
+}
+
+int tq_hip_embed_lookup_q8_batch(const void *embed, int rows, int cols, const int32_t *d_tokens, int n, float *out,
+                                 void *stream) {
+    if (!embed || !out || !d_tokens || rows <= 0 || cols <= 0 || cols % kQK != 0 || ((uintptr_t)embed & 15) ||
+        n < 0 || n > 65535)
+        return TQ_HIP_EINVAL;
+    if (n == 0) return TQ_HIP_OK;
+    hipLaunchKernelGGL(embed_q8_kernel, dim3((unsigned)((cols + 255) / 256), (unsigned)n), dim3(256), 0,
+                       (hipStream_t)stream, (const unsigned char *)embed, rows, cols, 0, d_tokens, out);
     return herr(hipGetLastError());
 }
 
 int tq_hip_sample_greedy(const float *logits, int n, int32_t *out, void *stream) {
     if (n <= 0 || !logits || !out) return TQ_HIP_EINVAL;   // model/sampler.c:4
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, logits, n, out);
+    if (n % 4 == 0 && ((uintptr_t)logits & 15) == 0)
+        hipLaunchKernelGGL(argmax_kernel<true>, dim3(1), dim3(1024), 0, (hipStream_t)stream, logits, n, out);
+    else
+        hipLaunchKernelGGL(argmax_kernel<false>, dim3(1), dim3(1024), 0, (hipStream_t)stream, logits, n, out);
     return herr(hipGetLastError());
 }
 

@@ -1,5 +1,5 @@
 /* tq_model.c — tq_ctx_init / tq_forward_token for a Q8 model on the device
- * (model/context.c:6-153), composed from libtqhip's kernels.  See
+ * (model/context.c:6-126), composed from libtqhip's kernels.  See
  * include/tq/tq_model.h.  Built with -ffp-contract=off: the RoPE table is
  * tq_attn_rope_table, the reference's rope_table arithmetic. */
 #include "tq/tq_model.h"
@@ -114,28 +114,120 @@ int tq_dev_forward_token(tq_dev_ctx *ctx, int token) {
     const int hidden = a->hidden_size, half = a->head_dim / 2, pos = ctx->pos;
     void *s = ctx->stream;
     if (token < 0 || token >= m->vocab_size) return -1;
-    /* :134 embed_lookup */
+    /* :113 embed_lookup */
     TRY(tq_hip_embed_lookup_q8(m->embed, m->vocab_size, hidden, token, ctx->x, s));
     const float *pending = NULL;   /* the previous block's output, added in the next norm */
     for (int l = 0; l < m->n_layers; l++) {
         const tq_dev_layer_weights *L = &m->layers[l];
-        /* :84,89 (x += mlp of the previous layer) rmsnorm(input_norm) */
+        /* :100 (x += mlp of the previous layer), :83 rmsnorm(input_norm) */
         TRY(tq_hip_add_rmsnorm(ctx->x, pending, L->input_norm, ctx->xn, 1, hidden, a->rms_eps, s));
-        /* :86-87 attention_layer */
+        /* :85-86 attention_layer */
         TRY(tq_hip_attention_layer_async(ctx->caches[l].dev, &L->attn, 1, NULL, ctx->positions + pos, pos,
                                          ctx->xn, ctx->cos_t + (size_t)pos * half,
                                          ctx->sin_t + (size_t)pos * half, ctx->y, ctx->ws, ctx->ws_bytes, s));
-        /* :89 x += attn, :96 rmsnorm(post_norm) */
+        /* :88 x += attn, :95 rmsnorm(post_norm) */
         TRY(tq_hip_add_rmsnorm(ctx->x, ctx->y, L->post_norm, ctx->xn, 1, hidden, a->rms_eps, s));
-        /* :98-99 mlp_layer */
+        /* :97-98 mlp_layer */
         TRY(tq_hip_mlp_layer_async(&L->mlp, 1, ctx->xn, ctx->y, ctx->ws, ctx->ws_bytes, s));
         pending = ctx->y;
     }
-    /* :101 x += mlp, :147 rmsnorm(final_norm), :148 lm_head */
+    /* :100 x += mlp, :121 rmsnorm(final_norm), :122 lm_head */
     TRY(tq_hip_add_rmsnorm(ctx->x, pending, m->final_norm, ctx->xn, 1, hidden, a->rms_eps, s));
     TRY(tq_hip_project_output(m->embed, m->vocab_size, hidden, ctx->xn, 1, (block_q8 *)ctx->ws, ctx->logits, s));
     ctx->pos++;
     return 0;
+}
+
+int tq_dev_batch_ws_init(tq_dev_batch_ws *ws, const tq_dev_model *m, int cap) {
+    memset(ws, 0, sizeof *ws);
+    if (check_model(m) != 0 || cap <= 0) return -1;
+    const size_t rows = (size_t)cap * m->attn.hidden_size * sizeof(float);
+    ws->cap = cap;
+    if (dmalloc((void **)&ws->x, rows) || dmalloc((void **)&ws->xn, rows) || dmalloc((void **)&ws->y, rows) ||
+        dmalloc((void **)&ws->tokens, (size_t)cap * sizeof(int32_t))) {
+        tq_dev_batch_ws_free(ws);
+        return -1;
+    }
+    return 0;
+}
+
+void tq_dev_batch_ws_free(tq_dev_batch_ws *ws) {
+    if (!ws) return;
+    tq_hip_free(ws->x);
+    tq_hip_free(ws->xn);
+    tq_hip_free(ws->y);
+    tq_hip_free(ws->tokens);
+    tq_hip_free(ws->ws);
+    memset(ws, 0, sizeof *ws);
+}
+
+int tq_dev_forward_batch(tq_dev_ctx *ctx, tq_dev_batch_ws *ws, const int *tokens, int n, int want_logits) {
+    /* :175-177 */
+    if (!ctx || !ctx->model || !ws || !tokens) return -1;
+    if (n <= 0 || n > ws->cap) return -1;
+    if (ctx->pos + n > ctx->max_tokens) return -1;
+    const tq_dev_model *m = ctx->model;
+    const tq_attn_config *a = &m->attn;
+    const int hidden = a->hidden_size, half = a->head_dim / 2, pos0 = ctx->pos;
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->vocab_size) return -1;   /* :185 */
+    if (!ws->ws) {
+        /* the workspace of the widest call, for cap tokens */
+        size_t b = tq_hip_attention_layer_ws_bytes(ctx->caches[0].dev, &m->layers[0].attn, ws->cap);
+        const size_t bm = tq_hip_mlp_ws_bytes(&m->layers[0].mlp, ws->cap);
+        if (bm > b) b = bm;
+        if (b == 0 || dmalloc(&ws->ws, b)) return -1;
+        ws->ws_bytes = b;
+    }
+    void *s = ctx->stream;
+    /* the ids go through the stream; waiting once here lets the caller reuse
+     * `tokens` on return whatever the copy path */
+    TRY(tq_hip_memcpy_h2d(ws->tokens, tokens, (size_t)n * sizeof(int32_t), s));
+    TRY(tq_hip_stream_synchronize(s));
+    /* :184-187 embed_lookup of every token */
+    TRY(tq_hip_embed_lookup_q8_batch(m->embed, m->vocab_size, hidden, ws->tokens, n, ws->x, s));
+    const float *pending = NULL;   /* the previous block's rows, added in the next norm */
+    for (int l = 0; l < m->n_layers; l++) {
+        const tq_dev_layer_weights *L = &m->layers[l];
+        /* :202 (x += mlp of the previous layer), :192-194 rmsnorm of every row */
+        TRY(tq_hip_add_rmsnorm(ws->x, pending, L->input_norm, ws->xn, n, hidden, a->rms_eps, s));
+        /* :195-196 attention_layer_batch */
+        TRY(tq_hip_attention_layer_batch_async(ctx->caches[l].dev, &L->attn, 0, pos0, n, ws->xn,
+                                               ctx->cos_t + (size_t)pos0 * half, ctx->sin_t + (size_t)pos0 * half,
+                                               ws->y, ws->ws, ws->ws_bytes, s));
+        /* :197 x += attn, :199-201 rmsnorm(post_norm) of every row */
+        TRY(tq_hip_add_rmsnorm(ws->x, ws->y, L->post_norm, ws->xn, n, hidden, a->rms_eps, s));
+        /* :202 mlp_layer_batch */
+        TRY(tq_hip_mlp_layer_async(&L->mlp, n, ws->xn, ws->y, ws->ws, ws->ws_bytes, s));
+        pending = ws->y;
+    }
+    if (want_logits) {
+        /* :203 x += mlp (the last row is the one read), :206-208 rmsnorm(final_norm) + lm_head */
+        const size_t last = (size_t)(n - 1) * hidden;
+        TRY(tq_hip_add_rmsnorm(ws->x + last, pending + last, m->final_norm, ctx->xn, 1, hidden, a->rms_eps, s));
+        TRY(tq_hip_project_output(m->embed, m->vocab_size, hidden, ctx->xn, 1, (block_q8 *)ctx->ws, ctx->logits,
+                                  s));
+    }
+    ctx->pos += n;
+    return 0;
+}
+
+int tq_dev_prefill(tq_dev_ctx *ctx, const int *tokens, int n) {
+    /* :216-217 */
+    if (!ctx || !ctx->model || !tokens || n <= 0) return -1;
+    if (ctx->pos + n > ctx->max_tokens) return -1;
+    const int cap = n < TQ_DEV_PREFILL_BATCH ? n : TQ_DEV_PREFILL_BATCH;
+    tq_dev_batch_ws ws;
+    if (tq_dev_batch_ws_init(&ws, ctx->model, cap) != 0) return -1;
+    int rc = 0;
+    for (int i = 0; i < n && rc == 0; i += cap) {
+        const int c = n - i < cap ? n - i : cap;
+        rc = tq_dev_forward_batch(ctx, &ws, tokens + i, c, i + c == n);
+    }
+    /* the workspace is freed only after the stream has used it */
+    if (ctx->stream) tq_hip_stream_synchronize(ctx->stream);
+    tq_dev_batch_ws_free(&ws);
+    return rc;
 }
 
 int tq_dev_logits(tq_dev_ctx *ctx, float *host) {

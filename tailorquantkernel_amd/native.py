@@ -81,6 +81,7 @@ _PROTOS = {
     "tq_hip_mlp_layer_async": (_i, [_vp, _i, _vp, _vp, _vp, _sz, _vp]),
     "tq_hip_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, C.c_float, _vp]),
     "tq_hip_embed_lookup_q8": (_i, [_vp, _i, _i, _i, _vp, _vp]),
+    "tq_hip_embed_lookup_q8_batch": (_i, [_vp, _i, _i, _vp, _i, _vp, _vp]),
     "tq_hip_sample_greedy": (_i, [_vp, _i, _vp, _vp]),
     "tq_hip_q8_matrix_bytes": (_sz, [_i, _i]),
     "tq_hip_q8_pack": (_i, [_vp, _vp, _i, _i, _vp]),

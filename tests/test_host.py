@@ -32,7 +32,7 @@ def cfg_of(attn, nq=8, nkv=2, hd=64, theta=10000.0):
 def test_exports_every_declared_symbol(attn):
     names = declared("tq_attn.h", "tq_") | declared("tq_model.h", "tq_")
     names = {n for n in names if not n.startswith("tq_hip_")}
-    assert len(names) == 15
+    assert len(names) == 19
     assert names == set(attn.EXPORTS), "ctypes prototypes out of step with tq_attn.h / tq_model.h"
     for n in names:
         assert hasattr(attn.load(), n)
@@ -66,7 +66,7 @@ def test_model_struct_layout_matches_header(attn, tmp_path):
     fields = [("tq_hip_attn_weights", "rms_eps"), ("tq_hip_mlp_weights", "inter"),
               ("tq_dev_layer_weights", "post_norm"), ("tq_dev_layer_weights", "mlp"),
               ("tq_dev_model", "vocab_size"), ("tq_dev_model", "layers"), ("tq_dev_ctx", "ws_bytes"),
-              ("tq_dev_ctx", "sampled")]
+              ("tq_dev_ctx", "sampled"), ("tq_dev_batch_ws", "tokens"), ("tq_dev_batch_ws", "ws_bytes")]
     body = " ".join(f'printf("%zu %zu ", sizeof({t}), offsetof({t}, {f}));' for t, f in fields)
     src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "tq/tq_model.h"\n'
                    f"int main(void){{{body} return 0;}}\n")
@@ -76,7 +76,8 @@ def test_model_struct_layout_matches_header(attn, tmp_path):
     got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
     from tailorquantkernel_amd import native
     py = {"tq_hip_attn_weights": native.AttnWeights, "tq_hip_mlp_weights": native.MlpWeights,
-          "tq_dev_layer_weights": attn.DevLayerWeights, "tq_dev_model": attn.DevModel, "tq_dev_ctx": attn.DevCtx}
+          "tq_dev_layer_weights": attn.DevLayerWeights, "tq_dev_model": attn.DevModel, "tq_dev_ctx": attn.DevCtx,
+          "tq_dev_batch_ws": attn.DevBatchWs}
     want = []
     for t, f in fields:
         want += [C.sizeof(py[t]), getattr(py[t], f).offset]

@@ -1,7 +1,7 @@
 """Pins the oracle's rest of the transformer block and the token forward:
 oracle_silu_mul (model/silu.c:6-18), oracle_mlp_layer (model/mlp.c:3-17),
 oracle_embed_lookup_q8 (model/embedding.c:4-17), oracle_sample_greedy
-(model/sampler.c:3-13) and oracle_forward_token (model/context.c:128-153).
+(model/sampler.c:3-13) and oracle_forward_token (model/context.c:104-126).
 
 Anchors: bit-exact against the compiled reference (its silu_mul, mlp_layer,
 sample_greedy, and tq_ctx_init + tq_forward_token through oracle/_ref's
