@@ -1,4 +1,5 @@
-/* block_q8.h — the Q8 block: 32 int8 codes sharing one fp32 scale.
+/* block_q8.h — the Q8 block: 32 int8 codes sharing one fp32 scale (and the
+ * Q4 weight block beside it).
  *
  * Byte layout (36 bytes, no padding): float d at offset 0, int8 q[32] at
  * offset 4.  This is the layout of packer/packer.h:7-11 in the reference, so a
@@ -20,12 +21,21 @@ typedef struct {
     float  d;
     int8_t q[QK];
 } block_q8;
+/* The Q4 weight block (packer/packer.h:9): 32 codes in [-7, 7] stored as
+ * code + 8 in nibbles, byte j holding code j in its low nibble and code
+ * j + 16 in its high nibble; 20 bytes. */
+typedef struct {
+    float   d;
+    uint8_t q[QK / 2];
+} block_q4;
 #endif
 
 #ifdef __cplusplus
 static_assert(sizeof(block_q8) == 36, "block_q8 must be 36 bytes with no padding");
+static_assert(sizeof(block_q4) == 20, "block_q4 must be 20 bytes with no padding");
 #else
 _Static_assert(sizeof(block_q8) == 36, "block_q8 must be 36 bytes with no padding");
+_Static_assert(sizeof(block_q4) == 20, "block_q4 must be 20 bytes with no padding");
 #endif
 
 #endif /* TQ_BLOCK_Q8_H */

@@ -239,16 +239,53 @@ int tq_hip_project_qkv(const void *wq, const void *wk, const void *wv, int q_row
 int tq_hip_project_output(const void *wo, int rows, int cols, const float *attn, int n_tok,
                           block_q8 *xq_ws, float *out, void *stream);
 
+/* ---- Q4 weight matrices (packer/packer.h:9, kernel/q4_scalar.c,
+ * kernel/q4_avx2.c) --------------------------------------------------------
+ *
+ * The "tiled Q4" layout, the same byte count as the reference's rows x
+ * cols/32 block_q4 array (packer/packer.c:63-75):
+ *   codes  [rows][cols/2]: each block's 16 nibble bytes exactly as block_q4.q
+ *          holds them (code j + 8 in the low nibble of byte j, code j + 24 in
+ *          the high nibble), blocks in row order;
+ *   scales [rows][cols/32] fp32 at byte offset rows*cols/2.
+ * The matmuls take the same block_q8 activations as the Q8 ones and compute
+ * each block's exact int32 dot sum_j (nibble_j - 8) * x_j, then
+ * ((float)s * w.d) * x.d (kernel/q4_scalar.c:3-15). */
+
+/* The matrix format of a weight struct (tq_format, kernel/kernel.h:6-9). */
+#define TQ_HIP_FORMAT_Q8 0
+#define TQ_HIP_FORMAT_Q4 1
+
+/* Bytes of a tiled Q4 rows x cols matrix (0 for a bad shape). */
+size_t tq_hip_q4_matrix_bytes(int rows, int cols);
+/* The reference's block_q4 rows (pack_matrix with bit_type '4',
+ * packer/packer.c:40-52,77-89, on the device) -> tiled Q4; and back. */
+int tq_hip_q4_pack(void *dst, const block_q4 *src, int rows, int cols, void *stream);
+int tq_hip_q4_unpack(block_q4 *dst, const void *src, int rows, int cols, void *stream);
+/* The Q4 MatmulFn / MatmulBatchFn (kernel/q4_scalar.c:17-32,
+ * kernel/q4_avx2.c:27-36). */
+int tq_hip_matmul_q4(const void *W, const block_q8 *xq, float *y, int rows, int cols, void *stream);
+int tq_hip_matmul_q4_batch(const void *W, const block_q8 *xq, float *y, int rows, int cols,
+                           int n_tok, void *stream);
+/* tq_hip_project_qkv / tq_hip_project_output with tiled Q4 matrices. */
+int tq_hip_project_qkv_q4(const void *wq, const void *wk, const void *wv, int q_rows, int kv_rows,
+                          int hidden, const float *xn, int n_tok, block_q8 *xq_ws, float *q, float *k,
+                          float *v, void *stream);
+int tq_hip_project_output_q4(const void *wo, int rows, int cols, const float *attn, int n_tok,
+                             block_q8 *xq_ws, float *out, void *stream);
+
 /* ---- the rest of the block: MLP, residual norm, embedding, sampler ------- */
 
 /* tq_mlp_weights (model/model_ops.h:29-31) with device pointers: wgate and wup
- * inter x hidden, wdown hidden x inter, all tiled Q8 (tq_hip_q8_pack). */
+ * inter x hidden, wdown hidden x inter, all tiled Q8 (tq_hip_q8_pack) or, with
+ * format TQ_HIP_FORMAT_Q4, all tiled Q4 (tq_hip_q4_pack). */
 typedef struct {
     const void *wgate;
     const void *wup;
     const void *wdown;
     int hidden;
     int inter;
+    int format;              /* TQ_HIP_FORMAT_Q8 (0) or TQ_HIP_FORMAT_Q4 */
 } tq_hip_mlp_weights;
 
 /* Device workspace bytes for tq_hip_mlp_layer_async over n rows (gate, up and
@@ -280,6 +317,10 @@ int tq_hip_embed_lookup_q8(const void *embed, int rows, int cols, int token, flo
  * matrix.  n at most 65535. */
 int tq_hip_embed_lookup_q8_batch(const void *embed, int rows, int cols, const int32_t *d_tokens, int n, float *out,
                                  void *stream);
+/* The same for a tiled Q4 matrix (model/embedding.c:20-27: d * (nibble - 8)). */
+int tq_hip_embed_lookup_q4(const void *embed, int rows, int cols, int token, float *out, void *stream);
+int tq_hip_embed_lookup_q4_batch(const void *embed, int rows, int cols, const int32_t *d_tokens, int n, float *out,
+                                 void *stream);
 
 /* sample_greedy (model/sampler.c:3-13): the first index of the largest of n
  * logits (strict >, so NaN never wins and ties keep the lower index), written
@@ -289,7 +330,8 @@ int tq_hip_sample_greedy(const float *logits, int n, int32_t *out, void *stream)
 /* ---- the whole attention layer on the device --------------------------- */
 
 /* tq_attn_weights (model/model_ops.h:27-37) with device pointers: the four
- * projection matrices in the tiled Q8 layout (tq_hip_q8_pack) and the
+ * projection matrices in the tiled Q8 layout (tq_hip_q8_pack; tiled Q4 with
+ * format TQ_HIP_FORMAT_Q4) and the
  * head_dim RMSNorm weights of q and k (16-byte aligned). */
 typedef struct {
     const void *wq;          /* n_q_heads*head_dim x hidden   */
@@ -300,6 +342,7 @@ typedef struct {
     const float *k_norm;
     int hidden;
     float rms_eps;
+    int format;              /* TQ_HIP_FORMAT_Q8 (0) or TQ_HIP_FORMAT_Q4: the four matrices */
 } tq_hip_attn_weights;
 
 /* Device workspace bytes tq_hip_attention_layer_async needs for n_q tokens

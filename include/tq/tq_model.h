@@ -27,8 +27,10 @@ typedef struct {
 } tq_dev_layer_weights;
 
 /* tq_model (model/model_ops.h:50-73), device pointers; `layers` is a host
- * array of n_layers.  embed (vocab x hidden, tiled Q8) is also the lm_head
- * (model/embedding.c:35-40). */
+ * array of n_layers.  embed (vocab x hidden, tiled Q8, or tiled Q4 with
+ * embed_format TQ_HIP_FORMAT_Q4) is also the lm_head
+ * (model/embedding.c:35-40).  Each layer's attn.format and mlp.format say the
+ * format of its matrices, as each tq_matrix carries its own. */
 typedef struct {
     tq_attn_config attn;
     int n_layers;
@@ -37,6 +39,7 @@ typedef struct {
     const void *embed;
     const float *final_norm;
     const tq_dev_layer_weights *layers;
+    int embed_format;             /* TQ_HIP_FORMAT_Q8 (0) or TQ_HIP_FORMAT_Q4 */
 } tq_dev_model;
 
 /* tq_ctx (model/model_ops.h:75-95) for the device. */

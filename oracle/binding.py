@@ -20,6 +20,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 QK = 32
 BLOCK_Q8 = np.dtype([("d", "<f4"), ("q", "i1", (QK,))])
+BLOCK_Q4 = np.dtype([("d", "<f4"), ("q", "u1", (QK // 2,))])
 assert BLOCK_Q8.itemsize == 36
 
 _f32p = C.POINTER(C.c_float)
@@ -43,6 +44,10 @@ def f32(a) -> np.ndarray:
 
 def blocks(n: int) -> np.ndarray:
     return np.zeros(n, dtype=BLOCK_Q8)
+
+
+def blocks4(n: int) -> np.ndarray:
+    return np.zeros(n, dtype=BLOCK_Q4)
 
 
 def dequant(b: np.ndarray) -> np.ndarray:
@@ -94,6 +99,11 @@ class Oracle:
         L.oracle_matmul_q8.argtypes = [_vp, _vp, _vp, _i, _i]
         L.oracle_matmul_q8_batch.argtypes = [_vp, _vp, _vp, _i, _i, _i]
         L.oracle_project_q8.argtypes = [_vp, _i, _i, _vp, _i, _vp]
+        L.oracle_pack_matrix_q4.argtypes = [_vp, _i, _i, _vp]
+        L.oracle_unpack_matrix_q4.argtypes = [_vp, _i, _i, _vp]
+        L.oracle_matmul_q4_batch.argtypes = [_vp, _vp, _vp, _i, _i, _i]
+        L.oracle_embed_lookup_q4.argtypes = [_vp, _i, _i, _i, _vp]
+        L.oracle_embed_lookup_q4.restype = _i
 
     # --- element ops -------------------------------------------------------
     def quantize_row_q8(self, x) -> np.ndarray:
@@ -211,6 +221,35 @@ class Oracle:
         self.lib.oracle_pack_matrix_q8(ptr(W), rows, cols, ptr(out))
         return out
 
+    def pack_matrix_q4(self, W) -> np.ndarray:
+        """rows x cols floats -> rows x cols/32 block_q4 (packer/packer.c:40-52)."""
+        W = f32(W)
+        rows, cols = W.shape
+        out = blocks4(rows * (cols // QK)).reshape(rows, cols // QK)
+        self.lib.oracle_pack_matrix_q4(ptr(W), rows, cols, ptr(out))
+        return out
+
+    def unpack_matrix_q4(self, Wq, rows: int, cols: int) -> np.ndarray:
+        out = np.zeros((rows, cols), np.float32)
+        Wq = np.ascontiguousarray(Wq)
+        assert Wq.size == rows * (cols // QK)
+        self.lib.oracle_unpack_matrix_q4(ptr(Wq), rows, cols, ptr(out))
+        return out
+
+    def matmul_q4(self, Wq, xq, rows: int, cols: int, n_tok: int = 1) -> np.ndarray:
+        """y[n_tok, rows] from block_q4 weights and n_tok block_q8 rows."""
+        y = np.zeros((n_tok, rows), np.float32)
+        Wq = np.ascontiguousarray(Wq)
+        xq = np.ascontiguousarray(xq)
+        assert Wq.size == rows * (cols // QK) and xq.size == n_tok * (cols // QK)
+        self.lib.oracle_matmul_q4_batch(ptr(Wq), ptr(xq), ptr(y), rows, cols, n_tok)
+        return y
+
+    def embed_lookup_q4(self, E, rows: int, cols: int, token: int):
+        out = np.zeros(cols, np.float32)
+        rc = self.lib.oracle_embed_lookup_q4(ptr(np.ascontiguousarray(E)), rows, cols, token, ptr(out))
+        return rc, out
+
     def matmul_q8(self, Wq, xq, rows: int, cols: int, n_tok: int = 1) -> np.ndarray:
         """y[n_tok, rows] from block_q8 weights and n_tok block_q8 rows."""
         y = np.zeros((n_tok, rows), np.float32)
@@ -238,29 +277,33 @@ class Oracle:
 
 
 class OracleModel(C.Structure):
-    """struct oracle_model (oracle/tq_oracle.h): a Q8 model as flat per-layer pointer arrays."""
+    """struct oracle_model (oracle/tq_oracle.h): a Q8 or Q4 model as flat per-layer pointer arrays."""
     _fields_ = [("n_layers", _i), ("n_q_heads", _i), ("n_kv_heads", _i), ("head_dim", _i), ("hidden", _i),
                 ("inter", _i), ("vocab", _i), ("rope_theta", _f), ("rms_eps", _f), ("embed", _vp),
                 ("final_norm", _vp), ("input_norm", _vp), ("post_norm", _vp), ("wq", _vp), ("wk", _vp),
                 ("wv", _vp), ("wo", _vp), ("q_norm", _vp), ("k_norm", _vp), ("wgate", _vp), ("wup", _vp),
-                ("wdown", _vp)]
+                ("wdown", _vp), ("format", _i), ("embed_format", _i)]
 
 
 class Model:
-    """A random Q8 model held as numpy arrays, in the shapes tq_model uses."""
+    """A random model held as numpy arrays, in the shapes tq_model uses: layer
+    matrices in `fmt` ("q8" or "q4"), the embedding in `embed_fmt`."""
 
-    def __init__(self, oracle, n_layers, nq, nkv, hd, hidden, inter, vocab, theta=5e5, eps=1e-6, seed=0):
+    def __init__(self, oracle, n_layers, nq, nkv, hd, hidden, inter, vocab, theta=5e5, eps=1e-6, seed=0,
+                 fmt="q8", embed_fmt="q8"):
         rng = np.random.default_rng(seed)
         self.n_layers, self.nq, self.nkv, self.hd = n_layers, nq, nkv, hd
         self.hidden, self.inter, self.vocab, self.theta, self.eps = hidden, inter, vocab, theta, eps
+        self.format, self.embed_format = int(fmt == "q4"), int(embed_fmt == "q4")
 
-        def mat(r, c, scale):
-            return oracle.pack_matrix_q8((rng.standard_normal((r, c)) * scale).astype(np.float32)).reshape(-1)
+        def mat(r, c, scale, f=fmt):
+            pack = oracle.pack_matrix_q4 if f == "q4" else oracle.pack_matrix_q8
+            return pack((rng.standard_normal((r, c)) * scale).astype(np.float32)).reshape(-1)
 
         def norm(n):
             return rng.uniform(0.6, 1.4, n).astype(np.float32)
 
-        self.embed = mat(vocab, hidden, 1.0)
+        self.embed = mat(vocab, hidden, 1.0, embed_fmt)
         self.final_norm = norm(hidden)
         self.layers = []
         for _ in range(n_layers):
@@ -281,7 +324,8 @@ class Model:
                          self.theta, self.eps, ptr(self.embed), ptr(self.final_norm),
                          *[C.cast(keep[k], C.c_void_p) for k in ("input_norm", "post_norm", "wq", "wk", "wv",
                                                                   "wo", "q_norm", "k_norm", "wgate", "wup",
-                                                                  "wdown")])
+                                                                  "wdown")],
+                         getattr(self, "format", 0), getattr(self, "embed_format", 0))
         return st, keep
 
 
@@ -318,14 +362,16 @@ class Ref:
         L.sample_greedy.restype = _i
         L.tqref_mlp_run.argtypes = [_i, _i, _vp, _vp, _vp, _vp, _vp]
         L.tqref_mlp_run.restype = _i
-        L.tqref_forward_run.argtypes = [_i] * 7 + [_f, _f] + [_vp] * 13 + [_i, _i, _vp, _vp]
+        L.tqref_forward_run.argtypes = [_i] * 7 + [_f, _f] + [_vp] * 13 + [_i, _i] + [_i, _i, _vp, _vp]
         L.tqref_forward_run.restype = _i
-        L.tqref_prefill_run.argtypes = [_i] * 7 + [_f, _f] + [_vp] * 13 + [_i, _i, _vp, _vp, _vp, _vp]
+        L.tqref_prefill_run.argtypes = [_i] * 7 + [_f, _f] + [_vp] * 13 + [_i, _i] + [_i, _i, _vp, _vp, _vp, _vp]
         L.tqref_prefill_run.restype = _i
         L.pack_matrix.argtypes = [_vp, _i, _i, _vp, C.c_char]
         L.pack_matrix.restype = _i
-        simd = ("matmul_q8_avx2",) if not scalar else ()
-        for fn in ("matmul_q8_scalar",) + simd:
+        L.unpack_matrix.argtypes = [_vp, _i, _i, _vp, C.c_char]
+        L.unpack_matrix.restype = _i
+        simd = ("matmul_q8_avx2", "matmul_q4_avx2") if not scalar else ()
+        for fn in ("matmul_q8_scalar", "matmul_q4_scalar") + simd:
             getattr(L, fn).argtypes = [_vp, _vp, _vp, _i, _i]
             getattr(L, fn + "_batch").argtypes = [_vp, _vp, _vp, _i, _i, _i]
 
@@ -346,7 +392,9 @@ class Ref:
                                         model.vocab, model.theta, model.eps, ptr(model.embed),
                                         ptr(model.final_norm), *[keep[k] for k in (
                                             "input_norm", "post_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm",
-                                            "wgate", "wup", "wdown")], max_tokens, len(toks), ptr(toks), ptr(out))
+                                            "wgate", "wup", "wdown")], getattr(model, "format", 0),
+                                        getattr(model, "embed_format", 0), max_tokens, len(toks), ptr(toks),
+                                        ptr(out))
         assert rc == 0, rc
         return out
 
@@ -365,8 +413,9 @@ class Ref:
                                         model.vocab, model.theta, model.eps, ptr(model.embed),
                                         ptr(model.final_norm), *[keep[k] for k in (
                                             "input_norm", "post_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm",
-                                            "wgate", "wup", "wdown")], max_tokens, len(toks), ptr(toks), ptr(out),
-                                        karr, varr)
+                                            "wgate", "wup", "wdown")], getattr(model, "format", 0),
+                                        getattr(model, "embed_format", 0), max_tokens, len(toks), ptr(toks),
+                                        ptr(out), karr, varr)
         assert rc == 0, rc
         return out, kc, vc
 
@@ -388,12 +437,30 @@ class Ref:
         assert rc == 0
         return out
 
-    def matmul_q8(self, Wq, xq, rows: int, cols: int, n_tok: int = 1, simd: bool = False):
+    def pack_matrix_q4(self, W) -> np.ndarray:
+        W = f32(W)
+        rows, cols = W.shape
+        out = blocks4(rows * (cols // QK)).reshape(rows, cols // QK)
+        rc = self.lib.pack_matrix(ptr(W), rows, cols, ptr(out), b"4")
+        assert rc == 0
+        return out
+
+    def unpack_matrix_q4(self, Wq, rows: int, cols: int) -> np.ndarray:
+        out = np.zeros((rows, cols), np.float32)
+        rc = self.lib.unpack_matrix(ptr(np.ascontiguousarray(Wq)), rows, cols, ptr(out), b"4")
+        assert rc == 0
+        return out
+
+    def matmul_q4(self, Wq, xq, rows: int, cols: int, n_tok: int = 1, simd: bool = False):
+        """matmul_q4_scalar / matmul_q4_avx2 (their _batch forms for n_tok > 1)."""
+        return self.matmul_q8(Wq, xq, rows, cols, n_tok, simd, fmt="q4")
+
+    def matmul_q8(self, Wq, xq, rows: int, cols: int, n_tok: int = 1, simd: bool = False, fmt: str = "q8"):
         """matmul_q8_scalar / matmul_q8_avx2 (their _batch forms for n_tok > 1)."""
         y = np.zeros((n_tok, rows), np.float32)
         Wq = np.ascontiguousarray(Wq)
         xq = np.ascontiguousarray(xq)
-        name = "matmul_q8_avx2" if simd else "matmul_q8_scalar"
+        name = f"matmul_{fmt}_avx2" if simd else f"matmul_{fmt}_scalar"
         if n_tok == 1:
             getattr(self.lib, name)(ptr(Wq), ptr(xq), ptr(y), rows, cols)
         else:

@@ -211,7 +211,7 @@ int tqref_mlp_run(int hidden, int inter, const block_q8 *wgate, const block_q8 *
         const float *const *post_norm, const block_q8 *const *wq, const block_q8 *const *wk,             \
         const block_q8 *const *wv, const block_q8 *const *wo, const float *const *qn,                   \
         const float *const *kn, const block_q8 *const *wgate, const block_q8 *const *wup,                \
-        const block_q8 *const *wdown
+        const block_q8 *const *wdown, int fmt, int embed_fmt
 
 static int build_model(tq_model *m, tq_layer_weights **layers_out, TQREF_MODEL_ARGS) {
     tq_layer_weights *layers = calloc((size_t)n_layers, sizeof *layers);
@@ -225,11 +225,16 @@ static int build_model(tq_model *m, tq_layer_weights **layers_out, TQREF_MODEL_A
         bind(&layers[l].mlp.wgate, wgate[l], inter, hidden);
         bind(&layers[l].mlp.wup, wup[l], inter, hidden);
         bind(&layers[l].mlp.wdown, wdown[l], hidden, inter);
+        /* fmt 1: the arrays hold block_q4 rows (get_matmul(TQ_FORMAT_Q4)) */
+        tq_matrix *all[7] = {&layers[l].attn.wq, &layers[l].attn.wk, &layers[l].attn.wv, &layers[l].attn.wo,
+                             &layers[l].mlp.wgate, &layers[l].mlp.wup, &layers[l].mlp.wdown};
+        for (int i = 0; i < 7; i++) all[i]->format = fmt == 1 ? TQ_FORMAT_Q4 : TQ_FORMAT_Q8;
     }
     m->cfg.n_layers = n_layers;
     m->cfg.intermediate_size = inter;
     m->cfg.vocab_size = vocab;
     bind(&m->w.embed, embed, vocab, hidden);
+    m->w.embed.format = embed_fmt == 1 ? TQ_FORMAT_Q4 : TQ_FORMAT_Q8;
     m->w.final_norm = final_norm;
     m->w.layers = layers;
     *layers_out = layers;
@@ -238,7 +243,7 @@ static int build_model(tq_model *m, tq_layer_weights **layers_out, TQREF_MODEL_A
 
 #define TQREF_MODEL_PASS                                                                                \
     n_layers, nq, nkv, hd, hidden, inter, vocab, theta, eps, embed, final_norm, input_norm, post_norm, wq, \
-        wk, wv, wo, qn, kn, wgate, wup, wdown
+        wk, wv, wo, qn, kn, wgate, wup, wdown, fmt, embed_fmt
 
 /* The reference's own tq_ctx_init + tq_forward_token (model/context.c:6-52,
  * 104-126) over n_tok tokens on a Q8 model given as flat per-layer pointer

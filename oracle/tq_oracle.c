@@ -250,6 +250,81 @@ void oracle_pack_matrix_q8(const float *W, int rows, int cols, block_q8 *out) {
     }
 }
 
+/* packer/packer.c:40-52: block_scale (:11-19) with qmax 7 (d = amax / 7, 1
+ * for an all-zero block), codes lroundf(w * (1/d)) clamped to [-7, 7] (:4-9),
+ * stored + 8 with code j in the low nibble of byte j and code j + 16 in the
+ * high nibble. */
+void oracle_pack_matrix_q4(const float *W, int rows, int cols, block_q4 *out) {
+    const int nb = cols / QK;
+    for (int r = 0; r < rows; r++) {
+        for (int b = 0; b < nb; b++) {
+            const float *w = W + (size_t)r * cols + (size_t)b * QK;
+            block_q4 *o = out + (size_t)r * nb + b;
+            float amax = 0.0f;
+            for (int j = 0; j < QK; j++) {
+                const float v = fabsf(w[j]);
+                if (v > amax) amax = v;
+            }
+            float d = amax / 7.0f;
+            if (d == 0.0f) d = 1.0f;
+            const float id = 1.0f / d;
+            o->d = d;
+            for (int j = 0; j < QK / 2; j++) {
+                long lo = lroundf(w[j] * id), hi = lroundf(w[j + QK / 2] * id);
+                lo = lo > 7 ? 7 : (lo < -7 ? -7 : lo);
+                hi = hi > 7 ? 7 : (hi < -7 ? -7 : hi);
+                o->q[j] = (uint8_t)(((hi + 8) << 4) | (lo + 8));
+            }
+        }
+    }
+}
+
+/* packer/packer.c:54-61: ((nibble) - 8) * d. */
+void oracle_unpack_matrix_q4(const block_q4 *in, int rows, int cols, float *out) {
+    const int nb = cols / QK;
+    for (int r = 0; r < rows; r++) {
+        for (int b = 0; b < nb; b++) {
+            const block_q4 *k = in + (size_t)r * nb + b;
+            float *o = out + (size_t)r * cols + (size_t)b * QK;
+            for (int j = 0; j < QK / 2; j++) {
+                o[j] = (float)((k->q[j] & 0x0F) - 8) * k->d;
+                o[j + QK / 2] = (float)((k->q[j] >> 4) - 8) * k->d;
+            }
+        }
+    }
+}
+
+/* kernel/q4_scalar.c:3-15: per block the exact int32 sum of (nibble - 8) *
+ * x code over the 16 low and 16 high codes, then ((float)s * w.d) * x.d added
+ * to one serial fp32 sum in block order. */
+static float dot_q4(const block_q4 *w, const block_q8 *x, int nb) {
+    float sum = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        int32_t s = 0;
+        for (int j = 0; j < QK / 2; j++) {
+            const int lo = (w[b].q[j] & 0x0F) - 8;
+            const int hi = (w[b].q[j] >> 4) - 8;
+            s += lo * x[b].q[j] + hi * x[b].q[j + QK / 2];
+        }
+        sum += (float)s * w[b].d * x[b].d;
+    }
+    return sum;
+}
+
+void oracle_matmul_q4_batch(const block_q4 *W, const block_q8 *xq, float *y, int rows, int cols, int n_tok) {
+    const int nb = cols / QK;
+    for (int t = 0; t < n_tok; t++)
+        for (int r = 0; r < rows; r++)
+            y[(size_t)t * rows + r] = dot_q4(W + (size_t)r * nb, xq + (size_t)t * nb, nb);
+}
+
+/* model/embedding.c:20-27: the unpacked row `token`. */
+int oracle_embed_lookup_q4(const block_q4 *embed, int rows, int cols, int token, float *out) {
+    if (token < 0 || token >= rows || cols % QK != 0) return -1;
+    oracle_unpack_matrix_q4(embed + (size_t)token * (cols / QK), 1, cols, out);
+    return 0;
+}
+
 /* kernel/q8_scalar.c:3-13: exact int32 dot of each block's codes, then
  * ((float)s * w.d) * x.d added to one serial fp32 sum in block order. */
 static float dot_q8(const block_q8 *w, const block_q8 *x, int nb) {
@@ -301,6 +376,30 @@ void oracle_rmsnorm(const float *x, const float *weight, float *out, int n, floa
     for (int i = 0; i < n; i++) out[i] = x[i] * inv * weight[i];
 }
 
+/* One matmul / projection in a weight format: 0 Q8 (kernel/q8_scalar.c), 1 Q4
+ * (kernel/q4_scalar.c), as get_matmul(format) picks (kernel/dispatch.c). */
+static void matmul_fmt(int fmt, const void *W, const block_q8 *xq, float *y, int rows, int cols) {
+    if (fmt == 1)
+        oracle_matmul_q4_batch((const block_q4 *)W, xq, y, rows, cols, 1);
+    else
+        oracle_matmul_q8((const block_q8 *)W, xq, y, rows, cols);
+}
+
+static void project_fmt(int fmt, const void *W, int rows, int cols, const float *x, float *y) {
+    const int nb = cols / QK;
+    block_q8 xq[nb > 0 ? nb : 1];
+    oracle_quantize_row_q8(x, xq, cols);
+    matmul_fmt(fmt, W, xq, y, rows, cols);
+}
+
+static int attention_layer_fmt(int fmt, const void *wq, const void *wk, const void *wv, const void *wo,
+                               const float *q_norm, const float *k_norm, int n_q_heads, int n_kv_heads,
+                               int head_dim, int hidden, float rope_theta, float rms_eps, block_q8 *k_cache,
+                               block_q8 *v_cache, int max_tokens, int pos, const float *xn, float *scores,
+                               float *out);
+static int mlp_layer_fmt(int fmt, const void *wgate, const void *wup, const void *wdown, int hidden, int inter,
+                         const float *xn, float *out);
+
 /* model/attention_layer.c:169-194 (attention_layer) on the flat Q8 cache:
  * project_qkv (quantize_row_q8 of xn, then wq, wk, wv), per-head RMSNorm of q
  * and k (:48-53), RoPE + store_kv + attend_q8 (oracle_attention_qkv), then
@@ -312,12 +411,21 @@ int oracle_attention_layer(const block_q8 *wq, const block_q8 *wk, const block_q
                            float rope_theta, float rms_eps, block_q8 *k_cache,
                            block_q8 *v_cache, int max_tokens, int pos, const float *xn,
                            float *scores, float *out) {
+    return attention_layer_fmt(0, wq, wk, wv, wo, q_norm, k_norm, n_q_heads, n_kv_heads, head_dim, hidden,
+                               rope_theta, rms_eps, k_cache, v_cache, max_tokens, pos, xn, scores, out);
+}
+
+static int attention_layer_fmt(int fmt, const void *wq, const void *wk, const void *wv, const void *wo,
+                               const float *q_norm, const float *k_norm, int n_q_heads, int n_kv_heads,
+                               int head_dim, int hidden, float rope_theta, float rms_eps, block_q8 *k_cache,
+                               block_q8 *v_cache, int max_tokens, int pos, const float *xn, float *scores,
+                               float *out) {
     if (pos < 0 || pos >= max_tokens) return -1;
     const int qdim = n_q_heads * head_dim, kvdim = n_kv_heads * head_dim;
     float q[qdim], k[kvdim], v[kvdim], attn[qdim];
-    oracle_project_q8(wq, qdim, hidden, xn, 1, q);
-    oracle_project_q8(wk, kvdim, hidden, xn, 1, k);
-    oracle_project_q8(wv, kvdim, hidden, xn, 1, v);
+    project_fmt(fmt, wq, qdim, hidden, xn, q);
+    project_fmt(fmt, wk, kvdim, hidden, xn, k);
+    project_fmt(fmt, wv, kvdim, hidden, xn, v);
     for (int h = 0; h < n_q_heads; h++)
         oracle_rmsnorm(q + (size_t)h * head_dim, q_norm, q + (size_t)h * head_dim, head_dim, rms_eps);
     for (int h = 0; h < n_kv_heads; h++)
@@ -325,7 +433,7 @@ int oracle_attention_layer(const block_q8 *wq, const block_q8 *wk, const block_q
     int rc = oracle_attention_qkv(k_cache, v_cache, n_q_heads, n_kv_heads, head_dim, max_tokens,
                                   rope_theta, pos, q, k, v, scores, attn);
     if (rc != 0) return rc;
-    oracle_project_q8(wo, hidden, qdim, attn, 1, out);
+    project_fmt(fmt, wo, hidden, qdim, attn, out);
     return 0;
 }
 
@@ -344,6 +452,11 @@ void oracle_silu_mul(const float *gate, const float *up, float *out, int n) {
  * quantize, down matmul.  wgate/wup: inter x hidden; wdown: hidden x inter. */
 int oracle_mlp_layer(const block_q8 *wgate, const block_q8 *wup, const block_q8 *wdown, int hidden,
                      int inter, const float *xn, float *out) {
+    return mlp_layer_fmt(0, wgate, wup, wdown, hidden, inter, xn, out);
+}
+
+static int mlp_layer_fmt(int fmt, const void *wgate, const void *wup, const void *wdown, int hidden, int inter,
+                         const float *xn, float *out) {
     if (hidden % QK != 0 || inter % QK != 0) return -1;
     float *gate = (float *)malloc((size_t)inter * sizeof(float));
     float *up = (float *)malloc((size_t)inter * sizeof(float));
@@ -353,11 +466,11 @@ int oracle_mlp_layer(const block_q8 *wgate, const block_q8 *wup, const block_q8 
         return -100;
     }
     oracle_quantize_row_q8(xn, q, hidden);
-    oracle_matmul_q8(wgate, q, gate, inter, hidden);
-    oracle_matmul_q8(wup, q, up, inter, hidden);
+    matmul_fmt(fmt, wgate, q, gate, inter, hidden);
+    matmul_fmt(fmt, wup, q, up, inter, hidden);
     oracle_silu_mul(gate, up, gate, inter);
     oracle_quantize_row_q8(gate, q, inter);
-    oracle_matmul_q8(wdown, q, out, hidden, inter);
+    matmul_fmt(fmt, wdown, q, out, hidden, inter);
     free(gate); free(up); free(q);
     return 0;
 }
@@ -400,22 +513,24 @@ int oracle_forward_token(const struct oracle_model *m, block_q8 *const *k_caches
     float *y = (float *)malloc((size_t)hidden * sizeof(float));
     float *scores = (float *)malloc((size_t)m->n_q_heads * max_tokens * sizeof(float));
     int rc = (x && xn && y && scores) ? 0 : -100;
-    if (rc == 0) rc = oracle_embed_lookup_q8(m->embed, m->vocab, hidden, token, x);
+    if (rc == 0)
+        rc = m->embed_format == 1 ? oracle_embed_lookup_q4((const block_q4 *)m->embed, m->vocab, hidden, token, x)
+                                  : oracle_embed_lookup_q8((const block_q8 *)m->embed, m->vocab, hidden, token, x);
     for (int l = 0; rc == 0 && l < m->n_layers; l++) {
         oracle_rmsnorm(x, m->input_norm[l], xn, hidden, m->rms_eps);
-        rc = oracle_attention_layer(m->wq[l], m->wk[l], m->wv[l], m->wo[l], m->q_norm[l], m->k_norm[l],
-                                    m->n_q_heads, m->n_kv_heads, m->head_dim, hidden, m->rope_theta,
-                                    m->rms_eps, k_caches[l], v_caches[l], max_tokens, pos, xn, scores, y);
+        rc = attention_layer_fmt(m->format, m->wq[l], m->wk[l], m->wv[l], m->wo[l], m->q_norm[l], m->k_norm[l],
+                                 m->n_q_heads, m->n_kv_heads, m->head_dim, hidden, m->rope_theta,
+                                 m->rms_eps, k_caches[l], v_caches[l], max_tokens, pos, xn, scores, y);
         if (rc != 0) break;
         for (int i = 0; i < hidden; i++) x[i] += y[i];
         oracle_rmsnorm(x, m->post_norm[l], xn, hidden, m->rms_eps);
-        rc = oracle_mlp_layer(m->wgate[l], m->wup[l], m->wdown[l], hidden, m->inter, xn, y);
+        rc = mlp_layer_fmt(m->format, m->wgate[l], m->wup[l], m->wdown[l], hidden, m->inter, xn, y);
         if (rc != 0) break;
         for (int i = 0; i < hidden; i++) x[i] += y[i];
     }
     if (rc == 0) {
         oracle_rmsnorm(x, m->final_norm, xn, hidden, m->rms_eps);
-        oracle_project_q8(m->embed, m->vocab, hidden, xn, 1, logits);
+        project_fmt(m->embed_format, m->embed, m->vocab, hidden, xn, logits);
     }
     free(x); free(xn); free(y); free(scores);
     return rc;

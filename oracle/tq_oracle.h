@@ -94,18 +94,20 @@ int oracle_embed_lookup_q8(const block_q8 *embed, int rows, int cols, int token,
 /* model/sampler.c:3-13 */
 int oracle_sample_greedy(const float *logits, int n);
 
-/* A Q8 model as tq_model holds it (model/model_ops.h:50-73), per-layer
+/* A Q8 or Q4 model as tq_model holds it (model/model_ops.h:50-73), per-layer
  * pointers in arrays of n_layers; embed is vocab x hidden (tied lm_head). */
 struct oracle_model {
     int n_layers, n_q_heads, n_kv_heads, head_dim, hidden, inter, vocab;
     float rope_theta, rms_eps;
-    const block_q8 *embed;
+    const void *embed;               /* block_q8 or block_q4 rows (embed_format) */
     const float *final_norm;
     const float *const *input_norm;
     const float *const *post_norm;
-    const block_q8 *const *wq, *const *wk, *const *wv, *const *wo;
+    const void *const *wq, *const *wk, *const *wv, *const *wo;   /* block_q8 or block_q4 (format) */
     const float *const *q_norm, *const *k_norm;
-    const block_q8 *const *wgate, *const *wup, *const *wdown;
+    const void *const *wgate, *const *wup, *const *wdown;
+    int format;                      /* the layers' matrices: 0 Q8, 1 Q4 */
+    int embed_format;                /* the embedding / lm_head: 0 Q8, 1 Q4 */
 };
 
 /* model/context.c:104-126 (tq_forward_token) on flat Q8 caches. */
@@ -114,6 +116,19 @@ int oracle_forward_token(const struct oracle_model *m, block_q8 *const *k_caches
 
 /* packer/packer.c:4-31 (pack_row_q8 over every row): weights -> block_q8. */
 void oracle_pack_matrix_q8(const float *W, int rows, int cols, block_q8 *out);
+
+/* packer/packer.c:40-52 (pack_row_q4 over every row, block_scale with qmax 7,
+ * :11-19): weights -> block_q4. */
+void oracle_pack_matrix_q4(const float *W, int rows, int cols, block_q4 *out);
+
+/* packer/packer.c:54-61 (unpack_row_q4 over every row). */
+void oracle_unpack_matrix_q4(const block_q4 *in, int rows, int cols, float *out);
+
+/* kernel/q4_scalar.c:3-24 (and :27-32 for n_tok rows of input). */
+void oracle_matmul_q4_batch(const block_q4 *W, const block_q8 *xq, float *y, int rows, int cols, int n_tok);
+
+/* model/embedding.c:20-27 (Q4) */
+int oracle_embed_lookup_q4(const block_q4 *embed, int rows, int cols, int token, float *out);
 
 /* kernel/q8_scalar.c:3-22 */
 void oracle_matmul_q8(const block_q8 *W, const block_q8 *xq, float *y, int rows, int cols);

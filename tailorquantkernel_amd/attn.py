@@ -42,7 +42,7 @@ class DevLayerWeights(C.Structure):
 class DevModel(C.Structure):
     """tq_dev_model: tq_model (model/model_ops.h:50-73) with device weights."""
     _fields_ = [("attn", AttnConfig), ("n_layers", _i), ("intermediate_size", _i), ("vocab_size", _i),
-                ("embed", _vp), ("final_norm", _vp), ("layers", C.POINTER(DevLayerWeights))]
+                ("embed", _vp), ("final_norm", _vp), ("layers", C.POINTER(DevLayerWeights)), ("embed_format", _i)]
 
 
 class DevBatchWs(C.Structure):

@@ -121,6 +121,8 @@ __global__ __launch_bounds__(1024) void add_rmsnorm4_kernel(float *__restrict__ 
 // One row of a tiled Q8 matrix to fp32: out[b*32 + j] = d_b * code_j.  With
 // `tokens`, grid row y looks up tokens[y] into out + y*cols (a token outside
 // [0, rows) writes zeros).
+// Q4: a tiled Q4 row, out[b*32 + j] = d_b * (nibble - 8) (model/embedding.c:20-27).
+template <bool Q4>
 __global__ __launch_bounds__(256) void embed_q8_kernel(const unsigned char *__restrict__ E, int rows, int cols,
                                                        int token, const int32_t *__restrict__ tokens,
                                                        float *__restrict__ out) {
@@ -136,6 +138,13 @@ __global__ __launch_bounds__(256) void embed_q8_kernel(const unsigned char *__re
     }
     const int nb = cols / kQK;
     const int b = e / kQK, j = e - b * kQK;
+    if (Q4) {
+        const unsigned char byte = E[(size_t)token * (cols / 2) + 16 * b + (j & 15)];
+        const int code = (j < 16 ? (byte & 0x0F) : (byte >> 4)) - 8;
+        const float d = reinterpret_cast<const float *>(E + (size_t)rows * (cols / 2))[(size_t)token * nb + b];
+        out[e] = d * (float)code;
+        return;
+    }
     const int g = b / 64, rest = nb - 64 * g, n = rest < 64 ? rest : 64, i = b - 64 * g;
     const int off = g * 2048 + (j < 16 ? 16 * i + j : 16 * n + 16 * i + (j - 16));
     const signed char code = (signed char)E[(size_t)token * cols + off];
@@ -220,6 +229,22 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
 
 int herr(hipError_t e) { return e == hipSuccess ? TQ_HIP_OK : TQ_HIP_EHIP_BASE - (int)e; }
 
+int embed_lookup(bool q4, const void *embed, int rows, int cols, int token, const int32_t *d_tokens, int n,
+                 float *out, void *stream) {
+    if (!embed || !out || rows <= 0 || cols <= 0 || cols % kQK != 0 || ((uintptr_t)embed & 15)) return TQ_HIP_EINVAL;
+    if (!d_tokens && (token < 0 || token >= rows)) return TQ_HIP_EINVAL;   // model/embedding.c:5
+    if (d_tokens && (n < 0 || n > 65535)) return TQ_HIP_EINVAL;
+    if (d_tokens && n == 0) return TQ_HIP_OK;
+    const dim3 grid((unsigned)((cols + 255) / 256), d_tokens ? (unsigned)n : 1u);
+    if (q4)
+        hipLaunchKernelGGL(embed_q8_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream,
+                           (const unsigned char *)embed, rows, cols, token, d_tokens, out);
+    else
+        hipLaunchKernelGGL(embed_q8_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream,
+                           (const unsigned char *)embed, rows, cols, token, d_tokens, out);
+    return herr(hipGetLastError());
+}
+
 }  // namespace
 
 hipError_t tq_launch_silu_quant(const float *gate, const float *up, block_q8 *hq, long n, hipStream_t s) {
@@ -254,22 +279,23 @@ int tq_hip_add_rmsnorm(float *x, const float *y, const float *weight, float *xn,
 }
 
 int tq_hip_embed_lookup_q8(const void *embed, int rows, int cols, int token, float *out, void *stream) {
-    if (!embed || !out || rows <= 0 || cols <= 0 || cols % kQK != 0 || ((uintptr_t)embed & 15)) return TQ_HIP_EINVAL;
-    if (token < 0 || token >= rows) return TQ_HIP_EINVAL;   // model/embedding.c:5
-    hipLaunchKernelGGL(embed_q8_kernel, dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                       (const unsigned char *)embed, rows, cols, token, nullptr, out);
-    return herr(hipGetLastError());
+    return embed_lookup(false, embed, rows, cols, token, nullptr, 0, out, stream);
 }
 
 int tq_hip_embed_lookup_q8_batch(const void *embed, int rows, int cols, const int32_t *d_tokens, int n, float *out,
                                  void *stream) {
-    if (!embed || !out || !d_tokens || rows <= 0 || cols <= 0 || cols % kQK != 0 || ((uintptr_t)embed & 15) ||
-        n < 0 || n > 65535)
-        return TQ_HIP_EINVAL;
-    if (n == 0) return TQ_HIP_OK;
-    hipLaunchKernelGGL(embed_q8_kernel, dim3((unsigned)((cols + 255) / 256), (unsigned)n), dim3(256), 0,
-                       (hipStream_t)stream, (const unsigned char *)embed, rows, cols, 0, d_tokens, out);
-    return herr(hipGetLastError());
+    if (!d_tokens) return TQ_HIP_EINVAL;
+    return embed_lookup(false, embed, rows, cols, 0, d_tokens, n, out, stream);
+}
+
+int tq_hip_embed_lookup_q4(const void *embed, int rows, int cols, int token, float *out, void *stream) {
+    return embed_lookup(true, embed, rows, cols, token, nullptr, 0, out, stream);
+}
+
+int tq_hip_embed_lookup_q4_batch(const void *embed, int rows, int cols, const int32_t *d_tokens, int n, float *out,
+                                 void *stream) {
+    if (!d_tokens) return TQ_HIP_EINVAL;
+    return embed_lookup(true, embed, rows, cols, 0, d_tokens, n, out, stream);
 }
 
 int tq_hip_sample_greedy(const float *logits, int n, int32_t *out, void *stream) {

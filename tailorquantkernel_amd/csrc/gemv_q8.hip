@@ -16,6 +16,20 @@
 // tq_hip_q8_pack turns the reference's block_q8 rows into this layout on the
 // device; tq_hip_q8_unpack turns it back.
 //
+// "Tiled Q4" (packer/packer.h:9, the reference's 20-byte block_q4), the same
+// byte count as its rows x cols/32 block_q4 array:
+//   codes  [rows][cols/2]: each block's 16 nibble bytes as the reference
+//          stores them (byte j: code j + 8 in the low nibble, code j + 24 in
+//          the high nibble), blocks in order, so lane l of a wave reads block
+//          64g+l as one 16-byte load and a wave-wide load is 1 KiB.
+//   scales [rows][cols/32] fp32 at byte offset rows*cols/2.
+// A Q4 dword w is turned into two dwords of signed bytes 16*code with
+// x = w ^ 0x88888888 (the nibble n becomes n - 8 in 4-bit two's complement):
+// (x << 4) & 0xF0F0F0F0 holds the low codes, x & 0xF0F0F0F0 the high codes.
+// The int32 dot of those with the activation codes is 16 times the block's
+// exact dot sum_j (n_j - 8) * x_j of kernel/q4_scalar.c:6-11, and an
+// arithmetic shift by 4 gives it back exactly.
+//
 // Matmul: the work is one pass over the weight bytes (HBM-bound).  A
 // 256-thread work-group runs 4 waves; a wave owns RW consecutive rows.  The
 // work-group first copies the activation rows (up to T tokens of block_q8,
@@ -47,6 +61,8 @@ using namespace tq;
 constexpr int kGemvWaves = 4;
 constexpr int kGroupBlocks = 64;
 constexpr int kGroupBytes = kGroupBlocks * kQK;   // 2048
+constexpr int kGroupBytes4 = kGroupBlocks * 16;   // 1024: a Q4 group
+constexpr int kBlockBytes4 = 20;                  // sizeof(block_q4)
 constexpr int kMaxSegs = 3;
 // Activation rows in LDS per work-group: 8 rows of 8192 (73,728 bytes) fit,
 // two work-groups per CU's 160 KiB.
@@ -99,6 +115,32 @@ __global__ __launch_bounds__(256) void unpack_kernel(unsigned char *__restrict__
     blk[5] = hi.x; blk[6] = hi.y; blk[7] = hi.z; blk[8] = hi.w;
 }
 
+// block_q4 rows <-> tiled Q4.  One thread per block.
+__global__ __launch_bounds__(256) void pack4_kernel(unsigned char *__restrict__ dst,
+                                                    const unsigned char *__restrict__ src, long long n) {
+    const long long k = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (k >= n) return;
+    const uint32_t *blk = reinterpret_cast<const uint32_t *>(src + (size_t)k * kBlockBytes4);
+    u32x4 q;
+    q.x = blk[1]; q.y = blk[2]; q.z = blk[3]; q.w = blk[4];
+    *reinterpret_cast<u32x4 *>(dst + (size_t)k * 16) = q;
+    reinterpret_cast<uint32_t *>(dst + (size_t)n * 16)[k] = blk[0];
+}
+
+__global__ __launch_bounds__(256) void unpack4_kernel(unsigned char *__restrict__ dst,
+                                                      const unsigned char *__restrict__ src, long long n) {
+    const long long k = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (k >= n) return;
+    const u32x4 q = *reinterpret_cast<const u32x4 *>(src + (size_t)k * 16);
+    uint32_t *blk = reinterpret_cast<uint32_t *>(dst + (size_t)k * kBlockBytes4);
+    blk[0] = reinterpret_cast<const uint32_t *>(src + (size_t)n * 16)[k];
+    blk[1] = q.x; blk[2] = q.y; blk[3] = q.z; blk[4] = q.w;
+}
+
+// Signed bytes 16 * code from a dword of Q4 nibbles: low nibbles, high nibbles.
+__device__ __forceinline__ uint32_t q4_lo16(uint32_t w) { return ((w ^ 0x88888888u) << 4) & 0xF0F0F0F0u; }
+__device__ __forceinline__ uint32_t q4_hi16(uint32_t w) { return (w ^ 0x88888888u) & 0xF0F0F0F0u; }
+
 // ---------------------------------------------------------------------------
 // Matmul over up to three row-concatenated matrices sharing one input
 // (project_qkv runs wq, wk and wv in one launch).
@@ -118,6 +160,7 @@ struct GemvArgs {
     const float *x;           // fp32 [n_tok][cols], 16-byte aligned, quantized in LDS
     unsigned char *xq_out;    // where work-group 0 leaves quantize_row_q8(x), or null
     int n_tok;                // rows of input in this launch (<= T)
+    bool q4;                  // the matrices are tiled Q4 (else tiled Q8)
 };
 
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
@@ -201,7 +244,9 @@ __device__ __forceinline__ void quantize_lds(const GemvArgs &a, const unsigned c
 // result is left unread on any path and the compiler never has to wait for
 // one in-flight load before issuing the next.
 // XF: the input is fp32 rows, staged raw and quantized in LDS (T <= 2).
-template <int T, int RW, int GC, bool XF>
+// Q4: the matrices are tiled Q4: one 16-byte load per (row, block) instead of
+// two, turned into the two code halves before the dot products.
+template <int T, int RW, int GC, bool XF, bool Q4>
 __global__ __launch_bounds__(256) void gemv_q8_kernel(GemvArgs a) {
 #pragma clang fp contract(off)
     extern __shared__ __align__(16) unsigned char smem[];
@@ -229,8 +274,9 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(GemvArgs a) {
         float *y = s0 ? a.seg[0].y : (s1 ? a.seg[1].y : a.seg[2].y);
         const int rows = s0 ? a.seg[0].rows : (s1 ? a.seg[1].rows : a.seg[2].rows);
         const int lr = r - (s0 ? 0 : (s1 ? a.seg_end[0] : a.seg_end[1]));
-        wrow[i] = w + (size_t)lr * cols;
-        drow[i] = reinterpret_cast<const float *>(w + (size_t)rows * cols) + (size_t)lr * nb;
+        const size_t rowb = Q4 ? (size_t)cols / 2 : (size_t)cols;   // code bytes per row
+        wrow[i] = w + (size_t)lr * rowb;
+        drow[i] = reinterpret_cast<const float *>(w + (size_t)rows * rowb) + (size_t)lr * nb;
         yrow[i] = y + lr;
         ldy[i] = rows;
     }
@@ -252,14 +298,20 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(GemvArgs a) {
             const int bl = lane < n ? lane : n - 1;
 #pragma unroll
             for (int i = 0; i < RW; i++) {
-                const unsigned char *p = wrow[i] + g * kGroupBytes + 16 * bl;
-                wlo[u][i] = *reinterpret_cast<const u32x4 *>(p);
-                whi[u][i] = *reinterpret_cast<const u32x4 *>(p + 16 * n);
+                if (Q4) {
+                    wlo[u][i] = *reinterpret_cast<const u32x4 *>(wrow[i] + g * kGroupBytes4 + 16 * bl);
+                } else {
+                    const unsigned char *p = wrow[i] + g * kGroupBytes + 16 * bl;
+                    wlo[u][i] = *reinterpret_cast<const u32x4 *>(p);
+                    whi[u][i] = *reinterpret_cast<const u32x4 *>(p + 16 * n);
+                }
                 wd[u][i] = drow[i][g * kGroupBlocks + bl];
             }
         }
         if (g0 == 0) {
-            wait_vm<3 * GC * RW>();   // the activation copies, issued first, have landed
+            // the activation copies, issued first, have landed once no more
+            // than this wave's weight loads (2 or 3 per unit) are in flight
+            wait_vm<(Q4 ? 2 : 3) * GC * RW>();
             __syncthreads();
             if (XF) {
                 quantize_lds(a, smem, xs);
@@ -273,6 +325,14 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(GemvArgs a) {
             const int n = rest < kGroupBlocks ? rest : kGroupBlocks;
             const bool valid = lane < n && g0 + u < ng;
             const int bl = lane < n ? lane : n - 1;
+            if (Q4) {
+#pragma unroll
+                for (int i = 0; i < RW; i++) {
+                    const u32x4 w = wlo[u][i];
+                    wlo[u][i] = u32x4{q4_lo16(w.x), q4_lo16(w.y), q4_lo16(w.z), q4_lo16(w.w)};
+                    whi[u][i] = u32x4{q4_hi16(w.x), q4_hi16(w.y), q4_hi16(w.z), q4_hi16(w.w)};
+                }
+            }
             int s[T][RW];
             float xd[T];
 #pragma unroll
@@ -293,7 +353,7 @@ __global__ __launch_bounds__(256) void gemv_q8_kernel(GemvArgs a) {
                     d = __builtin_amdgcn_sdot4(whi[u][i].y, xb[6], d, false);
                     d = __builtin_amdgcn_sdot4(whi[u][i].z, xb[7], d, false);
                     d = __builtin_amdgcn_sdot4(whi[u][i].w, xb[8], d, false);
-                    s[t][i] = d;
+                    s[t][i] = Q4 ? d >> 4 : d;
                 }
             }
 #pragma unroll
@@ -375,9 +435,13 @@ __device__ __forceinline__ long lds_pair(const unsigned char *p) {
 }
 
 // BX4: the activation rows are 16-byte aligned and nb % 4 == 0.
-template <bool BX4>
+// Q4: tiled Q4 matrices.  A holds [4 blocks][128 rows][16 B] nibble bytes (one
+// copy per thread instead of two); each lane turns its 8 bytes into 16 x its
+// 8 codes (low nibbles for k < 16, high for k >= 16), and the int32 products
+// are shifted back by 4 before scaling.
+template <bool BX4, bool Q4>
 __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
-    constexpr int kCopies = BX4 ? kGemmCopiesX4 : kGemmCopiesX1;
+    constexpr int kCopies = (BX4 ? kGemmCopiesX4 : kGemmCopiesX1) - (Q4 ? 1 : 0);
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -403,19 +467,27 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
         const unsigned char *w = s0 ? a.seg[0].w : (s1 ? a.seg[1].w : a.seg[2].w);
         const int rows = s0 ? a.seg[0].rows : (s1 ? a.seg[1].rows : a.seg[2].rows);
         const int lr = r - (s0 ? 0 : (s1 ? a.seg_end[0] : a.seg_end[1]));
-        wrow = w + (size_t)lr * cols;
-        drow = reinterpret_cast<const float *>(w + (size_t)rows * cols) + (size_t)lr * nb;
+        const size_t rowb = Q4 ? (size_t)cols / 2 : (size_t)cols;
+        wrow = w + (size_t)lr * rowb;
+        drow = reinterpret_cast<const float *>(w + (size_t)rows * rowb) + (size_t)lr * nb;
     }
 
     // kGemmCopies direct-to-LDS copies per thread per stage, nothing else
     auto issue = [&](int st, unsigned char *buf) {
         const int b0 = st * kGemmKB;
-#pragma unroll
-        for (int j = 0; j < kGemmA / 16 / kGemmThreads; j++) {
-            const int c = tid + kGemmThreads * j;
-            const int blk = c >> 8, half = (c >> 7) & 1;
+        if (Q4) {
+            // chunk tid -> (block tid / 128, row tid % 128)
+            const int blk = tid >> 7;
             const int b = b0 + blk < nb ? b0 + blk : nb - 1;
-            dma16(wrow + tiled_offset(nb, b, 16 * half), buf + 16 * (c - lane));
+            dma16(wrow + 16 * b, buf + 16 * (tid - lane));
+        } else {
+#pragma unroll
+            for (int j = 0; j < kGemmA / 16 / kGemmThreads; j++) {
+                const int c = tid + kGemmThreads * j;
+                const int blk = c >> 8, half = (c >> 7) & 1;
+                const int b = b0 + blk < nb ? b0 + blk : nb - 1;
+                dma16(wrow + tiled_offset(nb, b, 16 * half), buf + 16 * (c - lane));
+            }
         }
         {
             const int blk = tid >> 7;
@@ -477,7 +549,15 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
 #pragma unroll
             for (int r2 = 0; r2 < 2; r2++) {
                 const int row = wr + 16 * r2;
-                av[r2] = lds_pair(A + (((blk * 2 + (lg >> 1)) * kGemmRows) + row + l16) * 16 + 8 * (lg & 1));
+                if (Q4) {
+                    const long raw = lds_pair(A + ((blk * kGemmRows) + row + l16) * 16 + 8 * (lg & 1));
+                    const uint32_t w0 = (uint32_t)raw, w1 = (uint32_t)((unsigned long)raw >> 32);
+                    const uint32_t c0 = lg < 2 ? q4_lo16(w0) : q4_hi16(w0);
+                    const uint32_t c1 = lg < 2 ? q4_lo16(w1) : q4_hi16(w1);
+                    av[r2] = (long)(((unsigned long)c1 << 32) | c0);
+                } else {
+                    av[r2] = lds_pair(A + (((blk * 2 + (lg >> 1)) * kGemmRows) + row + l16) * 16 + 8 * (lg & 1));
+                }
                 const float4 w4 = *reinterpret_cast<const float4 *>(WD + (blk * kGemmRows + row + 4 * lg) * 4);
                 wd[r2][0] = w4.x; wd[r2][1] = w4.y; wd[r2][2] = w4.z; wd[r2][3] = w4.w;
             }
@@ -501,7 +581,8 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
                 for (int t4 = 0; t4 < 4; t4++)
 #pragma unroll
                     for (int i = 0; i < 4; i++)
-                        acc[r2][t4][i] = fmaf((float)c[r2][t4][i], wd[r2][i] * xd[t4], acc[r2][t4][i]);
+                        acc[r2][t4][i] = fmaf((float)(Q4 ? c[r2][t4][i] >> 4 : c[r2][t4][i]), wd[r2][i] * xd[t4],
+                                              acc[r2][t4][i]);
         }
     }
 
@@ -558,7 +639,7 @@ int pick_tokens(int nb, bool xf) {
     return 0;
 }
 
-template <int T, int RW, int GC, bool XF>
+template <int T, int RW, int GC, bool XF, bool Q4>
 hipError_t launch_t(const GemvArgs &a, hipStream_t s) {
     const int waves = (a.rows_total + RW - 1) / RW;
     const int grid = (waves + kGemvWaves - 1) / kGemvWaves;
@@ -566,26 +647,31 @@ hipError_t launch_t(const GemvArgs &a, hipStream_t s) {
     if (lds > kDefaultLdsLimit) {
         static bool opted = false;   // once per instantiation (and process)
         if (!opted) {
-            const hipError_t e = hipFuncSetAttribute((const void *)gemv_q8_kernel<T, RW, GC, XF>,
+            const hipError_t e = hipFuncSetAttribute((const void *)gemv_q8_kernel<T, RW, GC, XF, Q4>,
                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      (int)kMaxStageBytes);
             if (e != hipSuccess) return e;
             opted = true;
         }
     }
-    hipLaunchKernelGGL((gemv_q8_kernel<T, RW, GC, XF>), dim3(grid), dim3(kThreads), lds, s, a);
+    hipLaunchKernelGGL((gemv_q8_kernel<T, RW, GC, XF, Q4>), dim3(grid), dim3(kThreads), lds, s, a);
     return hipGetLastError();
+}
+
+template <int RW, int GC, bool Q4>
+hipError_t launch_tok_f(const GemvArgs &a, int tmax, bool xf, hipStream_t s) {
+    if (xf) return tmax == 2 ? launch_t<2, RW, GC, true, Q4>(a, s) : launch_t<1, RW, GC, true, Q4>(a, s);
+    switch (tmax) {
+        case 8: return launch_t<8, RW, GC, false, Q4>(a, s);
+        case 4: return launch_t<4, RW, GC, false, Q4>(a, s);
+        case 2: return launch_t<2, RW, GC, false, Q4>(a, s);
+        default: return launch_t<1, RW, GC, false, Q4>(a, s);
+    }
 }
 
 template <int RW, int GC>
 hipError_t launch_tok(const GemvArgs &a, int tmax, bool xf, hipStream_t s) {
-    if (xf) return tmax == 2 ? launch_t<2, RW, GC, true>(a, s) : launch_t<1, RW, GC, true>(a, s);
-    switch (tmax) {
-        case 8: return launch_t<8, RW, GC, false>(a, s);
-        case 4: return launch_t<4, RW, GC, false>(a, s);
-        case 2: return launch_t<2, RW, GC, false>(a, s);
-        default: return launch_t<1, RW, GC, false>(a, s);
-    }
+    return a.q4 ? launch_tok_f<RW, GC, true>(a, tmax, xf, s) : launch_tok_f<RW, GC, false>(a, tmax, xf, s);
 }
 
 hipError_t launch_gemv(const GemvArgs &a, int tcap, bool xf, int rw, int gc, hipStream_t s) {
@@ -617,16 +703,26 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t s) {
     const size_t lds = (size_t)kGemmBufs * kGemmStage;
     static bool opted = false;
     if (!opted) {
-        for (const void *f : {(const void *)gemm_q8_kernel<true>, (const void *)gemm_q8_kernel<false>}) {
+        for (const void *f : {(const void *)gemm_q8_kernel<true, false>, (const void *)gemm_q8_kernel<false, false>,
+                              (const void *)gemm_q8_kernel<true, true>, (const void *)gemm_q8_kernel<false, true>}) {
             const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
             if (e != hipSuccess) return e;
         }
         opted = true;
     }
-    if ((((uintptr_t)a.xq & 15) == 0) && a.nb % kGemmKB == 0)
-        hipLaunchKernelGGL(gemm_q8_kernel<true>, dim3((unsigned)grid), dim3(kGemmThreads), lds, s, a);
-    else
-        hipLaunchKernelGGL(gemm_q8_kernel<false>, dim3((unsigned)grid), dim3(kGemmThreads), lds, s, a);
+    const bool bx4 = (((uintptr_t)a.xq & 15) == 0) && a.nb % kGemmKB == 0;
+    const dim3 g((unsigned)grid), b(kGemmThreads);
+    if (a.q4) {
+        if (bx4)
+            hipLaunchKernelGGL((gemm_q8_kernel<true, true>), g, b, lds, s, a);
+        else
+            hipLaunchKernelGGL((gemm_q8_kernel<false, true>), g, b, lds, s, a);
+    } else {
+        if (bx4)
+            hipLaunchKernelGGL((gemm_q8_kernel<true, false>), g, b, lds, s, a);
+        else
+            hipLaunchKernelGGL((gemm_q8_kernel<false, false>), g, b, lds, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -684,6 +780,21 @@ void init_args(GemvArgs &a, int cols) {
     a.ng = (a.nb + kGroupBlocks - 1) / kGroupBlocks;
 }
 
+int matmul_fmt(bool q4, const void *W, const block_q8 *xq, float *y, int rows, int cols, int n_tok,
+               void *stream) {
+    if (!shape_ok(rows, cols) || n_tok <= 0 || !W || !xq || !y || !aligned(W, 16) || !aligned(xq, 4) ||
+        !aligned(y, 4))
+        return TQ_HIP_EINVAL;
+    GemvArgs a;
+    init_args(a, cols);
+    a.q4 = q4;
+    a.seg[0] = GemvSeg{(const unsigned char *)W, y, rows};
+    a.seg_end[0] = a.seg_end[1] = a.seg_end[2] = rows;
+    a.rows_total = rows;
+    a.xq = (const unsigned char *)xq;
+    return run_gemv(a, n_tok, (hipStream_t)stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -713,25 +824,69 @@ int tq_hip_q8_unpack(block_q8 *dst, const void *src, int rows, int cols, void *s
 
 int tq_hip_matmul_q8_batch(const void *W, const block_q8 *xq, float *y, int rows, int cols, int n_tok,
                            void *stream) {
-    if (!shape_ok(rows, cols) || n_tok <= 0 || !W || !xq || !y || !aligned(W, 16) || !aligned(xq, 4) ||
-        !aligned(y, 4))
-        return TQ_HIP_EINVAL;
-    GemvArgs a;
-    init_args(a, cols);
-    a.seg[0] = GemvSeg{(const unsigned char *)W, y, rows};
-    a.seg_end[0] = a.seg_end[1] = a.seg_end[2] = rows;
-    a.rows_total = rows;
-    a.xq = (const unsigned char *)xq;
-    return run_gemv(a, n_tok, (hipStream_t)stream);
+    return matmul_fmt(false, W, xq, y, rows, cols, n_tok, stream);
 }
 
 int tq_hip_matmul_q8(const void *W, const block_q8 *xq, float *y, int rows, int cols, void *stream) {
-    return tq_hip_matmul_q8_batch(W, xq, y, rows, cols, 1, stream);
+    return matmul_fmt(false, W, xq, y, rows, cols, 1, stream);
+}
+
+size_t tq_hip_q4_matrix_bytes(int rows, int cols) {
+    if (!shape_ok(rows, cols)) return 0;
+    return (size_t)rows * (size_t)(cols / kQK) * kBlockBytes4;
+}
+
+int tq_hip_q4_pack(void *dst, const block_q4 *src, int rows, int cols, void *stream) {
+    if (!shape_ok(rows, cols) || !dst || !src || !aligned(dst, 16) || !aligned(src, 4)) return TQ_HIP_EINVAL;
+    const long long n = (long long)rows * (cols / kQK);
+    hipLaunchKernelGGL(pack4_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (unsigned char *)dst, (const unsigned char *)src, n);
+    return herr(hipGetLastError());
+}
+
+int tq_hip_q4_unpack(block_q4 *dst, const void *src, int rows, int cols, void *stream) {
+    if (!shape_ok(rows, cols) || !dst || !src || !aligned(src, 16) || !aligned(dst, 4)) return TQ_HIP_EINVAL;
+    const long long n = (long long)rows * (cols / kQK);
+    hipLaunchKernelGGL(unpack4_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (unsigned char *)dst, (const unsigned char *)src, n);
+    return herr(hipGetLastError());
+}
+
+int tq_hip_matmul_q4_batch(const void *W, const block_q8 *xq, float *y, int rows, int cols, int n_tok,
+                           void *stream) {
+    return matmul_fmt(true, W, xq, y, rows, cols, n_tok, stream);
+}
+
+int tq_hip_matmul_q4(const void *W, const block_q8 *xq, float *y, int rows, int cols, void *stream) {
+    return matmul_fmt(true, W, xq, y, rows, cols, 1, stream);
 }
 
 int tq_hip_project_qkv(const void *wq, const void *wk, const void *wv, int q_rows, int kv_rows,
                        int hidden, const float *xn, int n_tok, block_q8 *xq_ws, float *q, float *k,
                        float *v, void *stream) {
+    return tq_project_qkv_fmt(false, wq, wk, wv, q_rows, kv_rows, hidden, xn, n_tok, xq_ws, q, k, v, stream);
+}
+
+int tq_hip_project_qkv_q4(const void *wq, const void *wk, const void *wv, int q_rows, int kv_rows,
+                          int hidden, const float *xn, int n_tok, block_q8 *xq_ws, float *q, float *k,
+                          float *v, void *stream) {
+    return tq_project_qkv_fmt(true, wq, wk, wv, q_rows, kv_rows, hidden, xn, n_tok, xq_ws, q, k, v, stream);
+}
+
+int tq_hip_project_output(const void *wo, int rows, int cols, const float *attn, int n_tok,
+                          block_q8 *xq_ws, float *out, void *stream) {
+    return tq_project_output_fmt(false, wo, rows, cols, attn, n_tok, xq_ws, out, stream);
+}
+
+int tq_hip_project_output_q4(const void *wo, int rows, int cols, const float *attn, int n_tok,
+                             block_q8 *xq_ws, float *out, void *stream) {
+    return tq_project_output_fmt(true, wo, rows, cols, attn, n_tok, xq_ws, out, stream);
+}
+
+}  // extern "C"
+
+int tq_project_qkv_fmt(bool q4, const void *wq, const void *wk, const void *wv, int q_rows, int kv_rows, int hidden,
+                    const float *xn, int n_tok, block_q8 *xq_ws, float *q, float *k, float *v, void *stream) {
     if (!shape_ok(q_rows, hidden) || kv_rows <= 0 || n_tok <= 0 || !wq || !wk || !wv || !xn ||
         !xq_ws || !q || !k || !v || !aligned(wq, 16) || !aligned(wk, 16) || !aligned(wv, 16) ||
         !aligned(xn, 4) || !aligned(xq_ws, 4) || !aligned(q, 4) || !aligned(k, 4) || !aligned(v, 4))
@@ -739,6 +894,7 @@ int tq_hip_project_qkv(const void *wq, const void *wk, const void *wv, int q_row
     const hipStream_t s = (hipStream_t)stream;
     GemvArgs a;
     init_args(a, hidden);
+    a.q4 = q4;
     if (fuse_quantize(xn, n_tok, a.nb)) {
         a.x = xn;
         a.xq_out = (unsigned char *)xq_ws;
@@ -757,14 +913,15 @@ int tq_hip_project_qkv(const void *wq, const void *wk, const void *wv, int q_row
     return run_gemv(a, n_tok, s);
 }
 
-int tq_hip_project_output(const void *wo, int rows, int cols, const float *attn, int n_tok,
-                          block_q8 *xq_ws, float *out, void *stream) {
+int tq_project_output_fmt(bool q4, const void *wo, int rows, int cols, const float *attn, int n_tok,
+                       block_q8 *xq_ws, float *out, void *stream) {
     if (!shape_ok(rows, cols) || n_tok <= 0 || !wo || !attn || !xq_ws || !out || !aligned(wo, 16) ||
         !aligned(attn, 4) || !aligned(xq_ws, 4) || !aligned(out, 4))
         return TQ_HIP_EINVAL;
     const hipStream_t s = (hipStream_t)stream;
     GemvArgs a;
     init_args(a, cols);
+    a.q4 = q4;
     if (fuse_quantize(attn, n_tok, a.nb)) {
         a.x = attn;
         a.xq_out = (unsigned char *)xq_ws;
@@ -778,6 +935,8 @@ int tq_hip_project_output(const void *wo, int rows, int cols, const float *attn,
     a.rows_total = rows;
     return run_gemv(a, n_tok, s);
 }
+
+extern "C" {
 
 static size_t mlp_ws(int hidden, int inter, int n, size_t *off_gate, size_t *off_up, size_t *off_xq) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -793,7 +952,8 @@ static size_t mlp_ws(int hidden, int inter, int n, size_t *off_gate, size_t *off
 
 static bool mlp_ok(const tq_hip_mlp_weights *w, int n) {
     return w && n > 0 && w->wgate && w->wup && w->wdown && shape_ok(w->inter, w->hidden) &&
-           shape_ok(w->hidden, w->inter) && aligned(w->wgate, 16) && aligned(w->wup, 16) && aligned(w->wdown, 16);
+           shape_ok(w->hidden, w->inter) && aligned(w->wgate, 16) && aligned(w->wup, 16) &&
+           aligned(w->wdown, 16) && (w->format == TQ_HIP_FORMAT_Q8 || w->format == TQ_HIP_FORMAT_Q4);
 }
 
 size_t tq_hip_mlp_ws_bytes(const tq_hip_mlp_weights *w, int n) {
@@ -814,8 +974,10 @@ int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn
     block_q8 *xq = (block_q8 *)(ws + ox);
     const hipStream_t s = (hipStream_t)stream;
     // model/mlp.c:9-11: quantize xn, then the gate and up matmuls in one launch
+    const bool q4 = w->format == TQ_HIP_FORMAT_Q4;
     GemvArgs a;
     init_args(a, w->hidden);
+    a.q4 = q4;
     if (fuse_quantize(d_xn, n, a.nb)) {
         a.x = d_xn;
         a.xq_out = (unsigned char *)xq;
@@ -837,6 +999,7 @@ int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn
     // :14 the down matmul
     GemvArgs d;
     init_args(d, w->inter);
+    d.q4 = q4;
     d.seg[0] = GemvSeg{(const unsigned char *)w->wdown, d_out, w->hidden};
     d.seg_end[0] = d.seg_end[1] = d.seg_end[2] = w->hidden;
     d.rows_total = w->hidden;

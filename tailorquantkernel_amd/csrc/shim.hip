@@ -878,7 +878,8 @@ static size_t layer_ws(const tq_hip_kv_desc &D, int hidden, int n_q, size_t *off
 
 static bool layer_shape_ok(const tq_hip_kv *kv, const tq_hip_attn_weights *w, int n_q) {
     return kv && w && n_q > 0 && w->hidden > 0 && w->hidden % QK == 0 &&
-           (kv->desc.n_q_heads * kv->desc.head_dim) % QK == 0;
+           (kv->desc.n_q_heads * kv->desc.head_dim) % QK == 0 &&
+           (w->format == TQ_HIP_FORMAT_Q8 || w->format == TQ_HIP_FORMAT_Q4);
 }
 
 size_t tq_hip_attention_layer_ws_bytes(const tq_hip_kv *kv, const tq_hip_attn_weights *w, int n_q) {
@@ -903,12 +904,13 @@ int tq_hip_attention_layer_async(tq_hip_kv *kv, const tq_hip_attn_weights *w, in
     block_q8 *xq = (block_q8 *)(ws + ox);
     const int qd = D.n_q_heads * D.head_dim, kd = D.n_kv_heads * D.head_dim;
     void *s = (void *)pick(kv, stream);
-    int rc = tq_hip_project_qkv(w->wq, w->wk, w->wv, qd, kd, w->hidden, d_xn, n_q, xq, q, k, v, s);
+    const bool q4 = w->format == TQ_HIP_FORMAT_Q4;
+    int rc = tq_project_qkv_fmt(q4, w->wq, w->wk, w->wv, qd, kd, w->hidden, d_xn, n_q, xq, q, k, v, s);
     if (rc != TQ_HIP_OK) return rc;
     rc = tq_hip_decode_step_norm_async(kv, n_q, d_seq, d_pos, max_pos, q, k, v, w->q_norm, w->k_norm,
                                        w->rms_eps, d_cos, d_sin, attn, s);
     if (rc != TQ_HIP_OK) return rc;
-    return tq_hip_project_output(w->wo, w->hidden, qd, attn, n_q, xq, d_out, s);
+    return tq_project_output_fmt(q4, w->wo, w->hidden, qd, attn, n_q, xq, d_out, s);
 }
 
 int tq_hip_attention_layer_batch_async(tq_hip_kv *kv, const tq_hip_attn_weights *w, int seq, int pos0,
@@ -931,7 +933,8 @@ int tq_hip_attention_layer_batch_async(tq_hip_kv *kv, const tq_hip_attn_weights 
     const hipStream_t hs = pick(kv, stream);
     void *s = (void *)hs;
     // :213-218 quantize every row, then the batched q/k/v projections
-    int rc = tq_hip_project_qkv(w->wq, w->wk, w->wv, qd, kd, w->hidden, d_xn, n, xq, q, k, v, s);
+    const bool q4 = w->format == TQ_HIP_FORMAT_Q4;
+    int rc = tq_project_qkv_fmt(q4, w->wq, w->wk, w->wv, qd, kd, w->hidden, d_xn, n, xq, q, k, v, s);
     if (rc != TQ_HIP_OK) return rc;
     // :227-228 norm_heads on every token's q and k rows
     TQ_TRY(tq_launch_rmsnorm_rows(q, w->q_norm, q, n * D.n_q_heads, D.head_dim, w->rms_eps, hs));
@@ -940,7 +943,7 @@ int tq_hip_attention_layer_batch_async(tq_hip_kv *kv, const tq_hip_attn_weights 
     rc = tq_hip_prefill_async(kv, seq, pos0, n, q, k, v, d_cos, d_sin, attn, s);
     if (rc != TQ_HIP_OK) return rc;
     // :238-241 quantize the attention rows, then the batched output projection
-    return tq_hip_project_output(w->wo, w->hidden, qd, attn, n, xq, d_out, s);
+    return tq_project_output_fmt(q4, w->wo, w->hidden, qd, attn, n, xq, d_out, s);
 }
 
 }  // extern "C"

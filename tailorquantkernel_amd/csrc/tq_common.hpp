@@ -247,6 +247,13 @@ hipError_t tq_launch_accum(const float *w, size_t w_stride, int g, const block_q
 hipError_t tq_launch_softmax(float *x, int n, int rows, size_t stride, hipStream_t s);
 // h = silu(g) * u of n floats (rows of whole blocks), quantized to hq.
 hipError_t tq_launch_silu_quant(const float *gate, const float *up, block_q8 *hq, long n, hipStream_t s);
+
+// tq_hip_project_qkv / tq_hip_project_output over tiled Q8 (q4 false) or
+// tiled Q4 (q4 true) matrices; TQ_HIP_* codes.
+int tq_project_qkv_fmt(bool q4, const void *wq, const void *wk, const void *wv, int q_rows, int kv_rows, int hidden,
+                       const float *xn, int n_tok, block_q8 *xq_ws, float *q, float *k, float *v, void *stream);
+int tq_project_output_fmt(bool q4, const void *wo, int rows, int cols, const float *attn, int n_tok,
+                          block_q8 *xq_ws, float *out, void *stream);
 // In place allowed (out == x); n <= 8191.
 hipError_t tq_launch_rmsnorm_rows(const float *x, const float *w, float *out, int n_rows, int n, float eps,
                                   hipStream_t s);

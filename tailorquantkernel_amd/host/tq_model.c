@@ -14,6 +14,7 @@ static int check_model(const tq_dev_model *m) {
         m->intermediate_size % QK != 0)
         return -1;
     if (m->n_layers <= 0 || m->vocab_size <= 0) return -1;
+    if (m->embed_format != TQ_HIP_FORMAT_Q8 && m->embed_format != TQ_HIP_FORMAT_Q4) return -1;
     if (a->n_q_heads <= 0 || a->n_kv_heads <= 0 || a->head_dim <= 0 || a->head_dim % 2 != 0) return -1;
     for (int l = 0; l < m->n_layers; l++) {
         const tq_dev_layer_weights *L = &m->layers[l];
@@ -23,11 +24,22 @@ static int check_model(const tq_dev_model *m) {
         if (L->attn.hidden != a->hidden_size || L->mlp.hidden != a->hidden_size ||
             L->mlp.inter != m->intermediate_size)
             return -1;
+        if ((L->attn.format != TQ_HIP_FORMAT_Q8 && L->attn.format != TQ_HIP_FORMAT_Q4) ||
+            (L->mlp.format != TQ_HIP_FORMAT_Q8 && L->mlp.format != TQ_HIP_FORMAT_Q4))
+            return -1;
     }
     return 0;
 }
 
 static int dmalloc(void **p, size_t bytes) { return tq_hip_malloc(p, bytes) == TQ_HIP_OK ? 0 : -1; }
+
+/* lm_head (model/embedding.c:35-40) in the embedding's format. */
+static int lm_head(const tq_dev_model *m, const float *xn, void *ws, float *logits, void *s) {
+    const int hidden = m->attn.hidden_size;
+    return m->embed_format == TQ_HIP_FORMAT_Q4
+               ? tq_hip_project_output_q4(m->embed, m->vocab_size, hidden, xn, 1, (block_q8 *)ws, logits, s)
+               : tq_hip_project_output(m->embed, m->vocab_size, hidden, xn, 1, (block_q8 *)ws, logits, s);
+}
 
 int tq_dev_ctx_init(tq_dev_ctx *ctx, const tq_dev_model *m, int max_tokens) {
     memset(ctx, 0, sizeof *ctx);
@@ -115,7 +127,8 @@ int tq_dev_forward_token(tq_dev_ctx *ctx, int token) {
     void *s = ctx->stream;
     if (token < 0 || token >= m->vocab_size) return -1;
     /* :113 embed_lookup */
-    TRY(tq_hip_embed_lookup_q8(m->embed, m->vocab_size, hidden, token, ctx->x, s));
+    TRY(m->embed_format == TQ_HIP_FORMAT_Q4 ? tq_hip_embed_lookup_q4(m->embed, m->vocab_size, hidden, token, ctx->x, s)
+                                            : tq_hip_embed_lookup_q8(m->embed, m->vocab_size, hidden, token, ctx->x, s));
     const float *pending = NULL;   /* the previous block's output, added in the next norm */
     for (int l = 0; l < m->n_layers; l++) {
         const tq_dev_layer_weights *L = &m->layers[l];
@@ -133,7 +146,7 @@ int tq_dev_forward_token(tq_dev_ctx *ctx, int token) {
     }
     /* :100 x += mlp, :121 rmsnorm(final_norm), :122 lm_head */
     TRY(tq_hip_add_rmsnorm(ctx->x, pending, m->final_norm, ctx->xn, 1, hidden, a->rms_eps, s));
-    TRY(tq_hip_project_output(m->embed, m->vocab_size, hidden, ctx->xn, 1, (block_q8 *)ctx->ws, ctx->logits, s));
+    TRY(lm_head(m, ctx->xn, ctx->ws, ctx->logits, s));
     ctx->pos++;
     return 0;
 }
@@ -185,7 +198,9 @@ int tq_dev_forward_batch(tq_dev_ctx *ctx, tq_dev_batch_ws *ws, const int *tokens
     TRY(tq_hip_memcpy_h2d(ws->tokens, tokens, (size_t)n * sizeof(int32_t), s));
     TRY(tq_hip_stream_synchronize(s));
     /* :184-187 embed_lookup of every token */
-    TRY(tq_hip_embed_lookup_q8_batch(m->embed, m->vocab_size, hidden, ws->tokens, n, ws->x, s));
+    TRY(m->embed_format == TQ_HIP_FORMAT_Q4
+            ? tq_hip_embed_lookup_q4_batch(m->embed, m->vocab_size, hidden, ws->tokens, n, ws->x, s)
+            : tq_hip_embed_lookup_q8_batch(m->embed, m->vocab_size, hidden, ws->tokens, n, ws->x, s));
     const float *pending = NULL;   /* the previous block's rows, added in the next norm */
     for (int l = 0; l < m->n_layers; l++) {
         const tq_dev_layer_weights *L = &m->layers[l];
@@ -205,8 +220,7 @@ int tq_dev_forward_batch(tq_dev_ctx *ctx, tq_dev_batch_ws *ws, const int *tokens
         /* :203 x += mlp (the last row is the one read), :206-208 rmsnorm(final_norm) + lm_head */
         const size_t last = (size_t)(n - 1) * hidden;
         TRY(tq_hip_add_rmsnorm(ws->x + last, pending + last, m->final_norm, ctx->xn, 1, hidden, a->rms_eps, s));
-        TRY(tq_hip_project_output(m->embed, m->vocab_size, hidden, ctx->xn, 1, (block_q8 *)ctx->ws, ctx->logits,
-                                  s));
+        TRY(lm_head(m, ctx->xn, ctx->ws, ctx->logits, s));
     }
     ctx->pos += n;
     return 0;

@@ -90,6 +90,15 @@ _PROTOS = {
     "tq_hip_matmul_q8_batch": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "tq_hip_project_qkv": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
     "tq_hip_project_output": (_i, [_vp, _i, _i, _vp, _i, _vp, _vp, _vp]),
+    "tq_hip_q4_matrix_bytes": (_sz, [_i, _i]),
+    "tq_hip_q4_pack": (_i, [_vp, _vp, _i, _i, _vp]),
+    "tq_hip_q4_unpack": (_i, [_vp, _vp, _i, _i, _vp]),
+    "tq_hip_matmul_q4": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "tq_hip_matmul_q4_batch": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "tq_hip_project_qkv_q4": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
+    "tq_hip_project_output_q4": (_i, [_vp, _i, _i, _vp, _i, _vp, _vp, _vp]),
+    "tq_hip_embed_lookup_q4": (_i, [_vp, _i, _i, _i, _vp, _vp]),
+    "tq_hip_embed_lookup_q4_batch": (_i, [_vp, _i, _i, _vp, _i, _vp, _vp]),
 }
 
 EXPORTS = tuple(_PROTOS)
@@ -141,16 +150,22 @@ def device_arch() -> str:
     return buf.value.decode()
 
 
+FORMAT_Q8, FORMAT_Q4 = 0, 1   # TQ_HIP_FORMAT_Q8 / TQ_HIP_FORMAT_Q4
+
+
 class MlpWeights(C.Structure):
-    """tq_hip_mlp_weights: device gate/up/down matrices (tiled Q8)."""
+    """tq_hip_mlp_weights: device gate/up/down matrices (tiled Q8, or tiled Q4
+    with format FORMAT_Q4)."""
     _fields_ = [("wgate", C.c_void_p), ("wup", C.c_void_p), ("wdown", C.c_void_p), ("hidden", C.c_int),
-                ("inter", C.c_int)]
+                ("inter", C.c_int), ("format", C.c_int)]
 
 
 class AttnWeights(C.Structure):
-    """tq_hip_attn_weights: device projection matrices (tiled Q8) and norm weights."""
+    """tq_hip_attn_weights: device projection matrices (tiled Q8, or tiled Q4
+    with format FORMAT_Q4) and norm weights."""
     _fields_ = [("wq", C.c_void_p), ("wk", C.c_void_p), ("wv", C.c_void_p), ("wo", C.c_void_p),
-                ("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("hidden", C.c_int), ("rms_eps", C.c_float)]
+                ("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("hidden", C.c_int), ("rms_eps", C.c_float),
+                ("format", C.c_int)]
 
 
 class DeviceBuffer:

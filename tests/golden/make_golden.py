@@ -26,7 +26,9 @@ writes tests/golden/golden_matmul_q8.npz instead: the weight side of the
 path, on the shapes the reference's own kernel test runs
 (tools/test_kernel.c:178-180,187-190) — pack_matrix (packer/packer.c:22-31)
 of seeded weights, quantize_row_q8 of seeded activations and
-matmul_q8_scalar / matmul_q8_scalar_batch (kernel/q8_scalar.c:15-30).
+matmul_q8_scalar / matmul_q8_scalar_batch (kernel/q8_scalar.c:15-30); and
+the same weights packed as Q4 (packer/packer.c:40-52) with
+matmul_q4_scalar / matmul_q4_scalar_batch (kernel/q4_scalar.c:17-32).
 """
 from __future__ import annotations
 
@@ -39,7 +41,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 
-from oracle.binding import BLOCK_Q8, QK, Ref, blocks, f32, ptr  # noqa: E402
+from oracle.binding import BLOCK_Q8, QK, Ref, blocks, blocks4, f32, ptr  # noqa: E402
 from tests.golden.gen import checksum, fill_random  # noqa: E402
 
 OUT = os.path.join(HERE, "golden_q8.npz")
@@ -231,6 +233,16 @@ def weights() -> None:
         data[f"in_sum_{i}"] = np.array([checksum(W), checksum(x)], np.int64)
         data[f"packed_sum_{i}"] = np.array([checksum(Wq), checksum(xq)], np.int64)
         data[f"y_{i}"] = y
+        # the same weights as Q4 (pack_matrix '4', matmul_q4_scalar)
+        W4 = blocks4(rows * nb)
+        assert L.pack_matrix(ptr(W), rows, cols, ptr(W4), b"4") == 0
+        y4 = np.zeros(n_tok * rows, np.float32)
+        if n_tok == 1:
+            L.matmul_q4_scalar(ptr(W4), ptr(xq), ptr(y4), rows, cols)
+        else:
+            L.matmul_q4_scalar_batch(ptr(W4), ptr(xq), ptr(y4), rows, cols, n_tok)
+        data[f"packed4_sum_{i}"] = np.array([checksum(W4)], np.int64)
+        data[f"y4_{i}"] = y4
     np.savez_compressed(WEIGHTS_OUT, **data)
     print(f"wrote {WEIGHTS_OUT} ({os.path.getsize(WEIGHTS_OUT)} bytes, {len(data)} arrays)")
 

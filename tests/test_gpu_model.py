@@ -63,10 +63,12 @@ def rel_l2(a, b) -> float:
 
 
 def tiled(nat, Wq, rows, cols):
+    """block_q8 (or block_q4) rows -> a tiled matrix on the device."""
     lib = nat.load()
     src = dev(nat, Wq)
-    b = nat.DeviceBuffer(lib.tq_hip_q8_matrix_bytes(rows, cols))
-    nat.check(lib.tq_hip_q8_pack(b.ptr, src.ptr, rows, cols, None), "q8_pack")
+    q4 = Wq.dtype.itemsize == 20
+    b = nat.DeviceBuffer((lib.tq_hip_q4_matrix_bytes if q4 else lib.tq_hip_q8_matrix_bytes)(rows, cols))
+    nat.check((lib.tq_hip_q4_pack if q4 else lib.tq_hip_q8_pack)(b.ptr, src.ptr, rows, cols, None), "pack")
     sync(nat)
     return b
 
@@ -214,13 +216,13 @@ class DeviceModel:
             layers[i].post_norm = vec(L["post_norm"])
             layers[i].attn = nat.AttnWeights(mat(L["wq"], qd, m.hidden), mat(L["wk"], kd, m.hidden),
                                              mat(L["wv"], kd, m.hidden), mat(L["wo"], m.hidden, qd),
-                                             vec(L["q_norm"]), vec(L["k_norm"]), m.hidden, m.eps)
+                                             vec(L["q_norm"]), vec(L["k_norm"]), m.hidden, m.eps, m.format)
             layers[i].mlp = nat.MlpWeights(mat(L["wgate"], m.inter, m.hidden), mat(L["wup"], m.inter, m.hidden),
-                                           mat(L["wdown"], m.hidden, m.inter), m.hidden, m.inter)
+                                           mat(L["wdown"], m.hidden, m.inter), m.hidden, m.inter, m.format)
         self.layers = layers
         cfg = attn.AttnConfig(m.nq, m.nkv, hd, m.hidden, m.theta, m.eps)
         self.model = attn.DevModel(cfg, m.n_layers, m.inter, m.vocab, mat(m.embed, m.vocab, m.hidden),
-                                   vec(m.final_norm), layers)
+                                   vec(m.final_norm), layers, m.embed_format)
 
 
 @pytest.mark.parametrize("shape", [(2, 4, 2, 32, 128, 256, 300), (3, 8, 2, 64, 256, 512, 1000),
@@ -352,3 +354,45 @@ def test_forward_batch_and_prefill(nat, oracle, shape, n, chunks):
     assert L.tq_dev_forward_token(C.byref(ctx2), int(toks[0])) == 0
     L.tq_dev_ctx_free(C.byref(ctx2))
     L.tq_dev_ctx_free(C.byref(ctx))
+
+
+@pytest.mark.parametrize("shape,fmt,embed_fmt", [((2, 4, 2, 32, 128, 256, 300), "q4", "q4"),
+                                                 ((1, 32, 8, 128, 4096, 1024, 512), "q4", "q8"),
+                                                 ((2, 8, 2, 64, 256, 512, 1000), "q8", "q4")])
+def test_forward_q4(nat, oracle, shape, fmt, embed_fmt):
+    """A model with Q4 layer matrices and/or a Q4 embedding (each tq_matrix's
+    format, kernel/q4_scalar.c, model/embedding.c:20-27) through
+    tq_dev_forward_token and tq_dev_prefill: the token forward against the
+    oracle's (bit-exact with the reference's scalar build) with the bars of
+    test_forward_tokens; the prefill's last logits against the token loop's."""
+    from tailorquantkernel_amd import attn
+    L = attn.load()
+    m = Model(oracle, *shape, seed=shape[0] + 40, fmt=fmt, embed_fmt=embed_fmt)
+    dm = DeviceModel(nat, m)
+    tokens = [3, 77 % m.vocab, 12, 3, 96 % m.vocab, 0]
+    T = 8
+    ref, _, _ = oracle.forward(m, tokens, T)
+    ctx = attn.DevCtx()
+    assert L.tq_dev_ctx_init(C.byref(ctx), C.byref(dm.model), T) == 0
+    errs = []
+    for i, t in enumerate(tokens):
+        assert L.tq_dev_forward_token(C.byref(ctx), t) == 0
+        got = np.zeros(m.vocab, np.float32)
+        assert L.tq_dev_logits(C.byref(ctx), got.ctypes.data) == 0
+        errs.append(rel_l2(got, ref[i]))
+    print(f"{fmt}/{embed_fmt} logits relative L2 per token: {['%.1e' % e for e in errs]}")
+    assert errs[0] <= 1e-4 and max(errs) <= 3e-2
+    L.tq_dev_ctx_free(C.byref(ctx))
+    ctx2 = attn.DevCtx()
+    assert L.tq_dev_ctx_init(C.byref(ctx2), C.byref(dm.model), T) == 0
+    toks = np.array(tokens, np.int32)
+    assert L.tq_dev_prefill(C.byref(ctx2), toks.ctypes.data, len(tokens)) == 0
+    got = np.zeros(m.vocab, np.float32)
+    assert L.tq_dev_logits(C.byref(ctx2), got.ctypes.data) == 0
+    assert rel_l2(got, ref[-1]) <= 3e-2
+    L.tq_dev_ctx_free(C.byref(ctx2))
+    # a format outside Q8/Q4 is refused
+    bad = attn.DevModel(dm.model.attn, m.n_layers, m.inter, m.vocab, dm.model.embed, dm.model.final_norm,
+                        dm.layers, 7)
+    ctx3 = attn.DevCtx()
+    assert L.tq_dev_ctx_init(C.byref(ctx3), C.byref(bad), T) == -1

@@ -66,7 +66,8 @@ def test_model_struct_layout_matches_header(attn, tmp_path):
     fields = [("tq_hip_attn_weights", "rms_eps"), ("tq_hip_mlp_weights", "inter"),
               ("tq_dev_layer_weights", "post_norm"), ("tq_dev_layer_weights", "mlp"),
               ("tq_dev_model", "vocab_size"), ("tq_dev_model", "layers"), ("tq_dev_ctx", "ws_bytes"),
-              ("tq_dev_ctx", "sampled"), ("tq_dev_batch_ws", "tokens"), ("tq_dev_batch_ws", "ws_bytes")]
+              ("tq_dev_ctx", "sampled"), ("tq_dev_batch_ws", "tokens"), ("tq_dev_batch_ws", "ws_bytes"),
+              ("tq_hip_attn_weights", "format"), ("tq_hip_mlp_weights", "format"), ("tq_dev_model", "embed_format")]
     body = " ".join(f'printf("%zu %zu ", sizeof({t}), offsetof({t}, {f}));' for t, f in fields)
     src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "tq/tq_model.h"\n'
                    f"int main(void){{{body} return 0;}}\n")

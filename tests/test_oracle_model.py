@@ -12,6 +12,7 @@ quantized product chain, greedy ties to the first index.
 from __future__ import annotations
 
 import numpy as np
+import pytest
 
 from oracle.binding import Model, QK, ptr
 
@@ -83,3 +84,21 @@ def test_forward_token_vs_reference(oracle, ref_scalar):
         assert lo.tobytes() == lr.tobytes()
         assert [oracle.lib.oracle_sample_greedy(ptr(lo[i]), m.vocab) for i in range(len(tokens))] == \
                [int(np.argmax(lr[i])) for i in range(len(tokens))]
+
+
+@pytest.mark.parametrize("fmt,embed_fmt", [("q4", "q4"), ("q4", "q8"), ("q8", "q4")])
+def test_forward_token_q4_vs_reference(oracle, ref_scalar, fmt, embed_fmt):
+    """The forward with Q4 layer matrices and/or a Q4 embedding (get_matmul and
+    embed_lookup on TQ_FORMAT_Q4, kernel/q4_scalar.c, model/embedding.c:20-27):
+    bit-exact against the reference's scalar build, and its own prefill."""
+    m = Model(oracle, 2, 4, 2, 32, 128, 256, 300, seed=5, fmt=fmt, embed_fmt=embed_fmt)
+    tokens = [3, 77, 12, 3, 96, 0]
+    lo, kc, vc = oracle.forward(m, tokens, 8)
+    lr = ref_scalar.forward(m, tokens, 8)
+    assert lo.tobytes() == lr.tobytes()
+    lp, rk, rv = ref_scalar.prefill(m, tokens, 8)
+    assert lp.tobytes() == lr[-1].tobytes()
+    for l in range(m.n_layers):
+        n = len(tokens)
+        own = kc[l].reshape(m.nkv, 8, -1)[:, :n]
+        assert own.tobytes() == rk[l].reshape(m.nkv, 8, -1)[:, :n].tobytes()
