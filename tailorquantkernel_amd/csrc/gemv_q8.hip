@@ -622,10 +622,12 @@ int pick_rw(int rows_total) {
     return 1;
 }
 
-// Groups per row per pass: up to 8 (row, group) units in flight per wave,
-// never more groups than a row has.
-int pick_gc(int ng, int rw) {
-    int gc = 8 / rw;
+// Groups per row per pass: up to 8 (row, group) units in flight per wave (16
+// for Q4, whose units are half the bytes), never more groups than a row has
+// (TQ_HIP_GEMV_GC=1|2|4 overrides).
+int pick_gc(int ng, int rw, bool q4) {
+    const int forced = env_int("TQ_HIP_GEMV_GC", 0);
+    int gc = (forced == 1 || forced == 2 || forced == 4) ? forced : (q4 ? 16 : 8) / rw;
     if (gc > 4) gc = 4;
     while (gc > 1 && gc / 2 >= ng) gc /= 2;
     return gc;
@@ -683,6 +685,7 @@ hipError_t launch_gemv(const GemvArgs &a, int tcap, bool xf, int rw, int gc, hip
         case 0x22: return launch_tok<2, 2>(a, tcap, xf, s);
         case 0x24: return launch_tok<2, 4>(a, tcap, xf, s);
         case 0x41: return launch_tok<4, 1>(a, tcap, xf, s);
+        case 0x44: return launch_tok<4, 4>(a, tcap, xf, s);
         default: return launch_tok<4, 2>(a, tcap, xf, s);
     }
 }
@@ -739,7 +742,7 @@ int run_gemv(GemvArgs a, int n_tok, hipStream_t s) {
     const int tmax = pick_tokens(a.nb, xf);
     if (tmax == 0) return TQ_HIP_EINVAL;
     const int rw = pick_rw(a.rows_total);
-    const int gc = pick_gc(a.ng, rw);
+    const int gc = pick_gc(a.ng, rw, a.q4);
     const unsigned char *xq0 = a.xq;
     const float *x0 = a.x;
     unsigned char *out0 = a.xq_out;
