@@ -1,4 +1,4 @@
-"""ctypes binding for the CPU checker.
+"""ctypes binding for the CPU oracle.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and by
 bench.py's cpu_baseline leg.  The product package (tailorquantkernel_amd) never

@@ -1,6 +1,6 @@
 /* tq_oracle.c — CPU restatement of the reference's scalar Q8 attention path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker): loaded by tests/, by
+ * TEST INFRASTRUCTURE ONLY (the oracle): loaded by tests/, by
  * __graft_entry__.smoke() and by bench.py's cpu_baseline leg, never by the
  * product libraries.  Built with gcc -O2 -ffp-contract=off (see Makefile) so
  * that every a*b+c below is a rounded multiply followed by a rounded add, the

@@ -1,6 +1,6 @@
 /* tq_oracle.h — CPU restatement of the reference's scalar Q8 attention path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP path is
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle that the HIP path is
  * compared against.  Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg may load it; the product (libtqhip.so, libtqattn.so) never
  * links, loads or calls it.

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/tq_oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/tq_oracle.c) before the HIP path is compared against it.
 
 Three independent anchors:
 
