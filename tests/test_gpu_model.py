@@ -263,8 +263,12 @@ def test_forward_tokens(nat, oracle, shape):
           f"independent run: {['%.1e' % e for e in errs]}")
     assert errs[0] <= 1e-4
     assert max(errs_state) <= 3e-2 and max(errs) <= 3e-2
-    # the reference's checks: a token outside the vocabulary, then a full context
+    # the reference's checks (tools/test_model.c:1488-1507): a token outside the
+    # vocabulary leaves pos as it was, then a full context
+    pos = ctx.pos
     assert L.tq_dev_forward_token(C.byref(ctx), m.vocab) == -1
+    assert L.tq_dev_forward_token(C.byref(ctx), -1) == -1
+    assert ctx.pos == pos
     ctx2 = attn.DevCtx()
     assert L.tq_dev_ctx_init(C.byref(ctx2), C.byref(dm.model), 1) == 0
     assert L.tq_dev_forward_token(C.byref(ctx2), 1) == 0

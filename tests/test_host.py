@@ -185,3 +185,63 @@ def test_rope_table_matches_reference_build(attn, ref_scalar):
             rs = np.zeros(hd // 2, np.float32)
             ref_scalar.lib.rope_table(rc.ctypes.data, rs.ctypes.data, hd, pos, 5e5)
             assert c.tobytes() == rc.tobytes() and s.tobytes() == rs.tobytes()
+
+
+def test_dev_model_guards(attn):
+    """model/context.c:6-54 and :104-229's guards on the device model, checked
+    before any device call (tools/test_model.c:1455-1480,1488-1510): NULL model
+    or context, max_tokens 0, hidden not a multiple of 32, no layers, a missing
+    weight in the last layer, a layer whose sizes disagree with the model, an
+    unknown matrix format; a failed init leaves the context zeroed; free is
+    idempotent."""
+    from tailorquantkernel_amd import native
+    L = attn.load()
+    fake = 1 << 20        # never dereferenced: every call below fails validation first
+    n_layers = 2
+    layers = (attn.DevLayerWeights * n_layers)()
+    for l in range(n_layers):
+        layers[l].input_norm = layers[l].post_norm = fake
+        layers[l].attn = native.AttnWeights(fake, fake, fake, fake, fake, fake, 256, 1e-6)
+        layers[l].mlp = native.MlpWeights(fake, fake, fake, 256, 512)
+    cfg = attn.AttnConfig(4, 2, 64, 256, 1e4, 1e-6)
+
+    def model(**kw):
+        m = attn.DevModel(cfg, n_layers, 512, 300, fake, fake, layers)
+        for k, v in kw.items():
+            setattr(m, k, v)
+        return m
+
+    ctx = attn.DevCtx()
+    assert L.tq_dev_ctx_init(C.byref(ctx), None, 8) == -1
+    assert L.tq_dev_ctx_init(C.byref(ctx), C.byref(model()), 0) == -1
+    assert L.tq_dev_ctx_init(C.byref(ctx), C.byref(model(n_layers=0)), 8) == -1
+    assert L.tq_dev_ctx_init(C.byref(ctx), C.byref(model(vocab_size=0)), 8) == -1
+    assert L.tq_dev_ctx_init(C.byref(ctx), C.byref(model(embed_format=2)), 8) == -1
+    bad_cfg = attn.AttnConfig(4, 2, 64, 257, 1e4, 1e-6)
+    assert L.tq_dev_ctx_init(C.byref(ctx), C.byref(model(attn=bad_cfg)), 8) == -1
+    layers[1].attn.wq = None                       # the last layer's weights are checked too
+    assert L.tq_dev_ctx_init(C.byref(ctx), C.byref(model()), 8) == -1
+    layers[1].attn.wq = fake
+    layers[1].mlp.inter = 1024                     # disagrees with intermediate_size
+    assert L.tq_dev_ctx_init(C.byref(ctx), C.byref(model()), 8) == -1
+    layers[1].mlp.inter = 512
+    layers[0].mlp.format = 5
+    assert L.tq_dev_ctx_init(C.byref(ctx), C.byref(model()), 8) == -1
+    layers[0].mlp.format = 0
+    assert bytes(ctx) == bytes(attn.DevCtx())      # a failed init leaves the context zeroed
+    L.tq_dev_ctx_free(C.byref(ctx))
+    L.tq_dev_ctx_free(None)
+    # the token calls on a context with no model, and NULL pointers
+    assert L.tq_dev_forward_token(None, 0) == -1
+    assert L.tq_dev_forward_token(C.byref(ctx), 0) == -1
+    assert L.tq_dev_logits(C.byref(ctx), None) == -1
+    assert L.tq_dev_sample_greedy(C.byref(ctx)) == -1
+    ws = attn.DevBatchWs()
+    assert L.tq_dev_batch_ws_init(C.byref(ws), None, 4) == -1
+    assert L.tq_dev_batch_ws_init(C.byref(ws), C.byref(model()), 0) == -1
+    L.tq_dev_batch_ws_free(C.byref(ws))
+    toks = (C.c_int * 2)(1, 2)
+    assert L.tq_dev_forward_batch(None, C.byref(ws), toks, 2, 1) == -1
+    assert L.tq_dev_forward_batch(C.byref(ctx), C.byref(ws), toks, 2, 1) == -1
+    assert L.tq_dev_prefill(None, toks, 2) == -1
+    assert L.tq_dev_prefill(C.byref(ctx), toks, 2) == -1
