@@ -1183,7 +1183,7 @@ def bench_forward_8b(args, nat, hip, fmt="q8"):
 
     A.tq_dev_ctx_free(C.byref(ctx))
 
-    # prefill: 2048 tokens from an empty context, tq_dev_prefill (512-token calls)
+    # prefill: 2048 tokens from an empty context, tq_dev_prefill
     n_pf = 2048
     toks = rng.integers(0, vocab, n_pf).astype(np.int32)
     pf_ms = []
@@ -1221,9 +1221,9 @@ def bench_forward_8b(args, nat, hip, fmt="q8"):
                    "bytes_per_step": step_bytes},
         "ms_attention_32_layers": parts["attention"], "ms_mlp_32_layers": parts["mlp"],
         "prefill_2048": {"ms": pf, "tokens_per_s": n_pf * 1e3 / pf, "runs_ms": pf_ms,
-                         "what": "tq_dev_prefill of 2048 tokens on an empty 32-layer context (4 calls of "
-                                 "tq_dev_forward_batch, 512 tokens each, logits of the last token); median of "
-                                 "the runs after the first"},
+                         "what": "tq_dev_prefill of 2048 tokens on an empty 32-layer context (one "
+                                 "tq_dev_forward_batch call of 2048 tokens, logits of the last token); median "
+                                 "of the runs after the first"},
         "parity": parity,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,

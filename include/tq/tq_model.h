@@ -99,10 +99,12 @@ void tq_dev_batch_ws_free(tq_dev_batch_ws *ws);
 int tq_dev_forward_batch(tq_dev_ctx *ctx, tq_dev_batch_ws *ws, const int *tokens, int n, int want_logits);
 
 /* Tokens per tq_dev_forward_batch call of tq_dev_prefill.  The reference
- * uses 16 (model/model_ops.h:144), sized for its CPU; the device's batched
- * matmuls and causal attention want hundreds of tokens per call.  The chunk
- * changes only rounding: every token attends to all tokens before it. */
-#define TQ_DEV_PREFILL_BATCH 512
+ * uses 16 (model/model_ops.h:144), sized for its CPU; the device's GEMM
+ * tiles are 128 rows x 128 tokens, and at the 8B shape a 512-token call
+ * leaves the q/k/v and output projections half the CUs (128-192 tiles for
+ * 256 CUs).  The chunk changes only rounding: every token attends to all
+ * tokens before it. */
+#define TQ_DEV_PREFILL_BATCH 2048
 
 /* model/context.c:215-229: the whole prompt in chunks of
  * TQ_DEV_PREFILL_BATCH, logits of the last token in ctx->logits.  -1 for n

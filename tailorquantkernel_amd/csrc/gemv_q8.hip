@@ -472,6 +472,20 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
         drow = reinterpret_cast<const float *>(w + (size_t)rows * rowb) + (size_t)lr * nb;
     }
 
+    // The token rows' sources of this thread's B copies, fixed over the stages
+    // (a stage only adds 36 bytes per block to each).
+    const unsigned char *bsrc[kGemmBRounds];
+    if (BX4) {
+#pragma unroll
+        for (int j = 0; j < kGemmBRounds; j++) {
+            const int c = tid + kGemmThreads * j;
+            const int cc = c < kGemmBChunks ? c : kGemmBChunks - 1;
+            const int tk = cc / 9, piece = cc - 9 * tk;
+            const int t = tok0 + tk < a.n_tok ? tok0 + tk : a.n_tok - 1;
+            bsrc[j] = a.xq + (size_t)t * nb * kBlockBytes + 16 * piece;
+        }
+    }
+
     // kGemmCopies direct-to-LDS copies per thread per stage, nothing else
     auto issue = [&](int st, unsigned char *buf) {
         const int b0 = st * kGemmKB;
@@ -495,16 +509,10 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
             dma4(drow + b, buf + kGemmA + 4 * (tid - lane));
         }
         if (BX4) {
+            // copies past the tile fetch a real slice into the padding
 #pragma unroll
-            for (int j = 0; j < kGemmBRounds; j++) {
-                const int c = tid + kGemmThreads * j;
-                // copies past the tile fetch a real slice into the padding
-                const int cc = c < kGemmBChunks ? c : kGemmBChunks - 1;
-                const int tk = cc / 9, piece = cc - 9 * tk;
-                const int t = tok0 + tk < a.n_tok ? tok0 + tk : a.n_tok - 1;
-                dma16(a.xq + ((size_t)t * nb + b0) * kBlockBytes + 16 * piece,
-                      buf + kGemmA + kGemmWD + 16 * (c - lane));
-            }
+            for (int j = 0; j < kGemmBRounds; j++)
+                dma16(bsrc[j] + b0 * kBlockBytes, buf + kGemmA + kGemmWD + 16 * (tid + kGemmThreads * j - lane));
         } else {
 #pragma unroll
             for (int j = 0; j < kGemmBWords / kGemmThreads; j++) {
