@@ -27,6 +27,30 @@ __global__ __launch_bounds__(256) void silu_quant_kernel(const float *__restrict
     quantize_store32(h, hq + (e >> 5) * kBlockBytes);
 }
 
+// The same, 8 lanes x 4 values per block: float4 loads of gate and up, one
+// dword of codes per lane (16-byte aligned rows).  Whole 8-lane groups stay
+// together, as quantize8x4's DPP steps need.
+__global__ __launch_bounds__(256) void silu_quant8_kernel(const float *__restrict__ gate,
+                                                          const float *__restrict__ up,
+                                                          unsigned char *__restrict__ hq, long nblocks) {
+#pragma clang fp contract(off)
+    const long k = (long)blockIdx.x * 256 + threadIdx.x;
+    const long tb = k >> 3;
+    if (tb >= nblocks) return;
+    const int e = (int)(k & 7);
+    const float4 g4 = *reinterpret_cast<const float4 *>(gate + tb * kQK + 4 * e);
+    const float4 u4 = *reinterpret_cast<const float4 *>(up + tb * kQK + 4 * e);
+    const float g[4] = {g4.x, g4.y, g4.z, g4.w}, u[4] = {u4.x, u4.y, u4.z, u4.w};
+    float h[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float sig = 1.0f / (1.0f + expf(-g[i]));
+        h[i] = g[i] * sig * u[i];
+    }
+    unsigned char *blk = hq + tb * kBlockBytes;
+    quantize8x4(h, reinterpret_cast<float *>(blk), blk + 4 + 4 * e, e == 0);
+}
+
 // x += y (when y is given), then xn = rmsnorm(x) with `weight`: one
 // work-group per row.  The sum of squares is a parallel sum (per-thread
 // serial over a strided slice, then a wave tree and the four waves in
@@ -250,8 +274,12 @@ int embed_lookup(bool q4, const void *embed, int rows, int cols, int token, cons
 hipError_t tq_launch_silu_quant(const float *gate, const float *up, block_q8 *hq, long n, hipStream_t s) {
     const long nblocks = n / kQK;
     if (nblocks <= 0) return hipSuccess;
-    hipLaunchKernelGGL(silu_quant_kernel, dim3((unsigned)((nblocks * kQK + 255) / 256)), dim3(256), 0, s, gate, up,
-                       reinterpret_cast<unsigned char *>(hq), nblocks);
+    if ((((uintptr_t)gate | (uintptr_t)up) & 15) == 0 && ((uintptr_t)hq & 3) == 0)
+        hipLaunchKernelGGL(silu_quant8_kernel, dim3((unsigned)((nblocks * 8 + 255) / 256)), dim3(256), 0, s, gate,
+                           up, reinterpret_cast<unsigned char *>(hq), nblocks);
+    else
+        hipLaunchKernelGGL(silu_quant_kernel, dim3((unsigned)((nblocks * kQK + 255) / 256)), dim3(256), 0, s, gate,
+                           up, reinterpret_cast<unsigned char *>(hq), nblocks);
     return hipGetLastError();
 }
 

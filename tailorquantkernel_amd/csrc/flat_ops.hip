@@ -22,6 +22,21 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float *__restrict__
     quantize_store32(x[e], out + (size_t)blk * kBlockBytes);
 }
 
+// The same with 8 lanes x 4 values per block: one float4 load and one dword
+// of codes per lane (16-byte aligned x).  Whole 8-lane groups stay together
+// (256 is a multiple of 8), as quantize8x4's DPP steps need.
+__global__ __launch_bounds__(256) void quantize8_kernel(const float *__restrict__ x, unsigned char *__restrict__ out,
+                                                        long nblocks) {
+    const long k = (long)blockIdx.x * 256 + threadIdx.x;
+    const long tb = k >> 3;
+    if (tb >= nblocks) return;
+    const int e = (int)(k & 7);
+    const float4 v = *reinterpret_cast<const float4 *>(x + tb * kQK + 4 * e);
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    unsigned char *blk = out + tb * kBlockBytes;
+    quantize8x4(xv, reinterpret_cast<float *>(blk), blk + 4 + 4 * e, e == 0);
+}
+
 // One thread per (head, pair i < hd/2): reads both halves, writes both.
 __global__ __launch_bounds__(256) void rope_kernel(float *__restrict__ x, int n_heads, int hd,
                                                    const float *__restrict__ c,
@@ -140,8 +155,12 @@ inline unsigned grid_for(long items) { return (unsigned)((items + 255) / 256); }
 hipError_t tq_launch_quantize(const float *x, block_q8 *out, int n, hipStream_t s) {
     const int nblocks = n / kQK;
     if (nblocks <= 0) return hipSuccess;
-    hipLaunchKernelGGL(quantize_kernel, dim3(grid_for((long)nblocks * kQK)), dim3(256), 0, s, x,
-                       reinterpret_cast<unsigned char *>(out), nblocks);
+    if ((((uintptr_t)x & 15) | ((uintptr_t)out & 3)) == 0)
+        hipLaunchKernelGGL(quantize8_kernel, dim3(grid_for((long)nblocks * 8)), dim3(256), 0, s, x,
+                           reinterpret_cast<unsigned char *>(out), (long)nblocks);
+    else
+        hipLaunchKernelGGL(quantize_kernel, dim3(grid_for((long)nblocks * kQK)), dim3(256), 0, s, x,
+                           reinterpret_cast<unsigned char *>(out), nblocks);
     return hipGetLastError();
 }
 
