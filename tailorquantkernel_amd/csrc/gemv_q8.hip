@@ -389,8 +389,9 @@ size_t lds_bytes(int t, int nb, bool xf) {
 // Many tokens: int8 MFMA GEMM.  A work-group of 8 waves computes a 128-row x
 // 128-token tile; wave w owns rows 32(w%4)..+31 (two 16-row tiles) of tokens
 // 64(w/4)..+63 (four 16-token tiles).  The K dimension goes 4 blocks (128
-// codes) per stage through three LDS buffers filled by direct-to-LDS copies,
-// two stages ahead of the one being multiplied.  Per block,
+// codes) per stage through two LDS buffers filled by direct-to-LDS copies, one
+// stage ahead of the one being multiplied; at 73.7 KB two work-groups share a
+// CU, so one's scaling overlaps the other's products.  Per block,
 // v_mfma_i32_16x16x32_i8 gives the exact int32 block dot for a 16 x 16 tile,
 // and each lane folds its four into fp32 with fma(s, w_d * x_d, acc): one
 // fp32 scaling per (row, token, block), the reference's per-block product
@@ -402,29 +403,26 @@ size_t lds_bytes(int t, int nb, bool xf) {
 // (work-group w: XCD w % 8, row tile 8 (w/8 / n_tt) + w % 8) and the tile's
 // 128 weight rows are read from HBM once into that XCD's L2.
 //
-// LDS per stage (43,008 B):
+// LDS per stage (36,864 B):
 //   A   [4 blocks][2 halves][128 rows][16 B]   weight codes, one copy per 16 B
 //   WD  [4 blocks][128 rows] fp32             weight scales
 //   B   [128 tokens][4 blocks x 36 B]         the tokens' block_q8, as stored:
 //       with 16-byte aligned rows and a block count that is a multiple of 4,
 //       a token's 144 bytes are nine 16-byte copies (three rounds of 512, the
-//       last round's surplus copies land in 6 KB of padding so every wave
-//       issues the same count); otherwise 36 dword copies per token.
+//       last round's surplus lanes, whole waves, issue none); otherwise 36
+//       dword copies per token.
 constexpr int kGemmThreads = 512;
-constexpr int kGemmRows = 128, kGemmToks = 128, kGemmKB = 4, kGemmBufs = 3;
+constexpr int kGemmRows = 128, kGemmToks = 128, kGemmKB = 4, kGemmBufs = 2;
 constexpr int kGemmA = kGemmKB * 2 * kGemmRows * 16;            // 16,384
 constexpr int kGemmWD = kGemmKB * kGemmRows * 4;                // 2,048
 constexpr int kGemmBRow = kGemmKB * kBlockBytes;                // 144 bytes per token
 constexpr int kGemmB = kGemmToks * kGemmBRow;                   // 18,432
 constexpr int kGemmBChunks = kGemmB / 16;                       // 1,152 16-byte copies
 constexpr int kGemmBRounds = (kGemmBChunks + kGemmThreads - 1) / kGemmThreads;   // 3
-constexpr int kGemmBPad = kGemmBRounds * kGemmThreads * 16;     // 24,576
-constexpr int kGemmStage = kGemmA + kGemmWD + kGemmBPad;        // 43,008 (16-byte multiple)
+constexpr int kGemmStage = kGemmA + kGemmWD + kGemmB;           // 36,864 (16-byte multiple)
 constexpr int kGemmBWords = kGemmB / 4;                         // 4,608 dword copies
-// copies per thread per stage: A, WD, then B by 16 bytes or by dwords
-constexpr int kGemmCopiesX4 = kGemmA / 16 / kGemmThreads + kGemmWD / 4 / kGemmThreads + kGemmBRounds;
-constexpr int kGemmCopiesX1 = kGemmA / 16 / kGemmThreads + kGemmWD / 4 / kGemmThreads +
-                              kGemmBWords / kGemmThreads;
+static_assert(kGemmBChunks % 64 == 0 && (kGemmBRounds - 1) * kGemmThreads < kGemmBChunks,
+              "the last B round's copies past the tile are whole waves");
 static_assert(kGemmA / 16 % kGemmThreads == 0 && kGemmWD / 4 % kGemmThreads == 0 &&
               kGemmBWords % kGemmThreads == 0, "whole copy rounds per stage");
 
@@ -441,7 +439,6 @@ __device__ __forceinline__ long lds_pair(const unsigned char *p) {
 // are shifted back by 4 before scaling.
 template <bool BX4, bool Q4>
 __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
-    constexpr int kCopies = (BX4 ? kGemmCopiesX4 : kGemmCopiesX1) - (Q4 ? 1 : 0);
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -509,10 +506,11 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
             dma4(drow + b, buf + kGemmA + 4 * (tid - lane));
         }
         if (BX4) {
-            // copies past the tile fetch a real slice into the padding
+            // the last round's copies past the tile are left out (whole waves)
 #pragma unroll
             for (int j = 0; j < kGemmBRounds; j++)
-                dma16(bsrc[j] + b0 * kBlockBytes, buf + kGemmA + kGemmWD + 16 * (tid + kGemmThreads * j - lane));
+                if (tid + kGemmThreads * j < kGemmBChunks)
+                    dma16(bsrc[j] + b0 * kBlockBytes, buf + kGemmA + kGemmWD + 16 * (tid + kGemmThreads * j - lane));
         } else {
 #pragma unroll
             for (int j = 0; j < kGemmBWords / kGemmThreads; j++) {
@@ -535,17 +533,14 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[r2][t4][i] = 0.0f;
 
+    // Two buffers (73.7 KB, so two work-groups share a CU): stage st+1 is
+    // copied while stage st is multiplied.
     issue(0, smem);
-    if (stages > 1) issue(1, smem + kGemmStage);
     for (int st = 0; st < stages; st++) {
-        unsigned char *buf = smem + (st % kGemmBufs) * kGemmStage;
-        // stage st has landed once at most the next stage's copies are in flight
-        if (st + 1 < stages)
-            wait_vm<kCopies>();
-        else
-            wait_vm<0>();
+        unsigned char *buf = smem + (st & 1) * kGemmStage;
+        wait_vm<0>();      // this wave's copies of stage st have landed
         __syncthreads();   // stage st is in LDS everywhere; stage st-1's buffer is free
-        if (st + 2 < stages) issue(st + 2, smem + ((st + 2) % kGemmBufs) * kGemmStage);
+        if (st + 1 < stages) issue(st + 1, smem + ((st + 1) & 1) * kGemmStage);
         const unsigned char *A = buf, *WD = buf + kGemmA, *B = buf + kGemmA + kGemmWD;
         // two blocks at a time: the second block's LDS reads and products
         // overlap the first one's scaling
