@@ -59,7 +59,8 @@ int tq_hip_device_synchronize(void);
 
 /* ---- kernel-level ops on flat block_q8 arrays (device pointers) --------- */
 
-/* kernel/quant_x.c:12-33 quantize_row_q8: x[n] -> out[n/32], bit-exact. */
+/* kernel/quant_x.c:12-33 quantize_row_q8: x[n] -> out[n/32], bit-exact.  x and out
+ * must be 4-byte aligned (a float array, a block_q8 array), else -1. */
 int tq_hip_quantize_row_q8(const float *x, block_q8 *out, int n, void *stream);
 
 /* model/rope.c:14-22 rope_apply on n_heads consecutive heads of x, in place,

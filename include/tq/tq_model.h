@@ -42,8 +42,9 @@ typedef struct {
     int embed_format;             /* TQ_HIP_FORMAT_Q8 (0) or TQ_HIP_FORMAT_Q4 */
 } tq_dev_model;
 
-/* tq_ctx (model/model_ops.h:75-95) for the device. */
-typedef struct {
+/* tq_ctx (model/model_ops.h:75-95) for the device.  The struct tag lets a
+ * host tq_ctx point at one (struct tq_dev_ctx *) before this header. */
+typedef struct tq_dev_ctx {
     const tq_dev_model *model;
     tq_kv_cache *caches;          /* n_layers TQ_KV_Q8_DEVICE caches */
     int pos;

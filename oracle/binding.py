@@ -330,12 +330,37 @@ class Model:
 
 
 class Ref:
-    """The reference compiled from its own sources (oracle/_ref)."""
+    """The reference compiled from its own sources (oracle/_ref).
 
-    def __init__(self, scalar: bool = False):
-        name = "libtqref_scalar.so" if scalar else "libtqref.so"
-        self.lib = _load(os.path.join(HERE, "_ref", name))
+    dropin="fused" / "route" loads the scalar build whose attention_layer.c,
+    context.c and model_ops.h carry the MI355X library's drop-in edits
+    (oracle/dropin_patch.sh) and which links libtqattn.so: its entry points
+    take TQ_KV_Q8_DEVICE caches after set_kv_type(TQ_KV_Q8_DEVICE)."""
+
+    TQ_KV_Q8, TQ_KV_Q8_DEVICE = 1, 2
+
+    @staticmethod
+    def _name(scalar: bool, dropin: str | None) -> str:
+        if dropin == "fused":
+            return "libtqref_dropin.so"
+        if dropin == "route":
+            return "libtqref_dropin_route.so"
+        return "libtqref_scalar.so" if scalar else "libtqref.so"
+
+    def __init__(self, scalar: bool = False, dropin: str | None = None):
+        self.lib = _load(os.path.join(HERE, "_ref", self._name(scalar, dropin)))
+        self.dropin = dropin
+        scalar = scalar or dropin is not None
         L = self.lib
+        L.tqref_capture_attn.argtypes = [_vp]
+        if dropin is not None:
+            L.tqref_set_kv_type.argtypes = [_i]
+            L.tqref_set_cache_q_heads.argtypes = [_i]
+            L.tqref_layer_steps.argtypes = [_i, _i, _i, _i, _f, _f] + [_vp] * 6 + [_vp, _vp, _i, _i, _i, _vp, _vp,
+                                                                                   _vp]
+            L.tqref_layer_steps.restype = _i
+            L.tqref_forward_devmodel_run.argtypes = [_i] * 7 + [_f, _f] + [_vp] * 13 + [_i, _i] + [_i, _i, _vp, _vp]
+            L.tqref_forward_devmodel_run.restype = _i
         L.quantize_row_q8.argtypes = [_vp, _vp, _i]
         L.rope_table.argtypes = [_vp, _vp, _i, _i, _f]
         L.rope_apply.argtypes = [_vp, _i, _vp, _vp]
@@ -376,9 +401,27 @@ class Ref:
             getattr(L, fn + "_batch").argtypes = [_vp, _vp, _vp, _i, _i, _i]
 
     @staticmethod
-    def available(scalar: bool = False) -> bool:
-        name = "libtqref_scalar.so" if scalar else "libtqref.so"
-        return os.path.exists(os.path.join(HERE, "_ref", name))
+    def available(scalar: bool = False, dropin: str | None = None) -> bool:
+        return os.path.exists(os.path.join(HERE, "_ref", Ref._name(scalar, dropin)))
+
+    def set_kv_type(self, kv_type: int) -> None:
+        self.lib.tqref_set_kv_type(kv_type)
+
+    def forward_devmodel(self, model, tokens, max_tokens):
+        """tq_forward_token with ctx.dev set: each token on the device model
+        built from the same weights (the edited context.c's branch)."""
+        st, keep = model.struct()
+        toks = np.ascontiguousarray(tokens, np.int32)
+        out = np.zeros((len(toks), model.vocab), np.float32)
+        rc = self.lib.tqref_forward_devmodel_run(
+            model.n_layers, model.nq, model.nkv, model.hd, model.hidden, model.inter, model.vocab, model.theta,
+            model.eps, ptr(model.embed), ptr(model.final_norm),
+            *[keep[k] for k in ("input_norm", "post_norm", "wq", "wk", "wv", "wo", "q_norm", "k_norm", "wgate",
+                                "wup", "wdown")],
+            getattr(model, "format", 0), getattr(model, "embed_format", 0), max_tokens, len(toks), ptr(toks),
+            ptr(out))
+        assert rc == 0, rc
+        return out
 
     def isa(self) -> str:
         return self.lib.tqref_isa().decode()

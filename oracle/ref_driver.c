@@ -15,6 +15,16 @@
  *   tqref_attention_qkv                       the attention core alone (RoPE,
  *       store_kv, attend_q8) composed from the reference's public kernels with
  *       attend_q8's OpenMP policy; bench.py times it as the CPU baseline.
+ *
+ * Built with -DTQ_DROPIN against the reference's attention_layer.c,
+ * context.c and model_ops.h as edited by dropin_patch.sh (the MI355X
+ * library's drop-in edits) and linked with libtqattn.so, the same entry
+ * points run the reference's own callers on either cache type
+ * (tqref_set_kv_type): TQ_KV_Q8 host arrays or the TQ_KV_Q8_DEVICE HBM cache,
+ * whose contents are uploaded from and downloaded into the caller's arrays
+ * around each call.  tqref_layer_steps runs attention_layer over a run of
+ * positions on one cache, and tqref_forward_devmodel_run runs
+ * tq_forward_token through the edited context.c's device-model branch.
  */
 #include <math.h>
 #include <stdlib.h>
@@ -54,12 +64,66 @@ static void make_layer(tq_attn_weights *w, tq_attn_config *cfg, int nq, int nkv,
     w->k_norm = kn;
 }
 
+/* When set, tqref_layer_batch_run copies the attention rows it computed
+ * (the workspace's attn, [n][nq*hd], before the output projection) here. */
+static float *g_attn_rows = NULL;
+void tqref_capture_attn(float *dst) { g_attn_rows = dst; }
+
 static void make_cache(tq_kv_cache *c, block_q8 *k, block_q8 *v, int max_tokens) {
     memset(c, 0, sizeof *c);
     c->type = TQ_KV_Q8;
     c->k_q8 = k;
     c->v_q8 = v;
     c->max_tokens = max_tokens;
+}
+
+#ifdef TQ_DROPIN
+static tq_kv_type g_kv_type = TQ_KV_Q8;
+static int g_cache_q_heads = 0;
+
+/* Device caches are created for this many query heads instead of the
+ * layer's (0: the layer's), so a call whose config does not match its cache
+ * can be made on purpose. */
+void tqref_set_cache_q_heads(int nq) { g_cache_q_heads = nq; }
+
+/* The cache type the drivers build: TQ_KV_Q8 (the reference's host arrays,
+ * the default) or TQ_KV_Q8_DEVICE. */
+void tqref_set_kv_type(int type) { g_kv_type = (tq_kv_type)type; }
+#endif
+
+/* A cache over the caller's [nkv][max_tokens][nb] arrays: the arrays
+ * themselves (TQ_KV_Q8), or a device cache initialised from them. */
+static int open_cache(tq_kv_cache *c, const tq_attn_config *cfg, block_q8 *k, block_q8 *v, int max_tokens) {
+#ifdef TQ_DROPIN
+    if (g_kv_type == TQ_KV_Q8_DEVICE) {
+        tq_attn_config dc = *cfg;
+        if (g_cache_q_heads > 0) dc.n_q_heads = g_cache_q_heads;
+        if (tq_kv_cache_init(c, TQ_KV_Q8_DEVICE, &dc, max_tokens) != 0) return -100;
+        if (tq_kv_cache_upload(c, k, v) != 0) {
+            tq_kv_cache_free(c);
+            return -101;
+        }
+        return 0;
+    }
+#endif
+    (void)cfg;
+    make_cache(c, k, v, max_tokens);
+    return 0;
+}
+
+/* Leaves the cache's contents in the caller's arrays and releases it. */
+static int close_cache(tq_kv_cache *c, block_q8 *k, block_q8 *v) {
+#ifdef TQ_DROPIN
+    if (c->type == TQ_KV_Q8_DEVICE) {
+        const int rc = tq_kv_cache_download(c, k, v);
+        tq_kv_cache_free(c);
+        return rc != 0 ? -102 : 0;
+    }
+#endif
+    (void)c;
+    (void)k;
+    (void)v;
+    return 0;
 }
 
 int tqref_layer_run(int nq, int nkv, int hd, int hidden, float theta, float eps,
@@ -71,10 +135,34 @@ int tqref_layer_run(int nq, int nkv, int hd, int hidden, float theta, float eps,
     tq_attn_config cfg;
     tq_kv_cache cache;
     make_layer(&w, &cfg, nq, nkv, hd, hidden, theta, eps, wq, wk, wv, wo, qn, kn);
-    make_cache(&cache, k_cache, v_cache, max_tokens);
     int rc = tq_attn_validate(&w, &cfg);
     if (rc != 0) return rc;
-    return attention_layer(&w, &cfg, &cache, pos, xn, scores, out);
+    rc = open_cache(&cache, &cfg, k_cache, v_cache, max_tokens);
+    if (rc != 0) return rc;
+    rc = attention_layer(&w, &cfg, &cache, pos, xn, scores, out);
+    const int rc2 = close_cache(&cache, k_cache, v_cache);
+    return rc != 0 ? rc : rc2;
+}
+
+/* attention_layer for positions pos0 .. pos0+n-1 on one cache (xn and out:
+ * [n][hidden]).  Returns the first nonzero code. */
+int tqref_layer_steps(int nq, int nkv, int hd, int hidden, float theta, float eps, const block_q8 *wq,
+                      const block_q8 *wk, const block_q8 *wv, const block_q8 *wo, const float *qn,
+                      const float *kn, block_q8 *k_cache, block_q8 *v_cache, int max_tokens, int pos0, int n,
+                      const float *xn, float *scores, float *out) {
+    tq_attn_weights w;
+    tq_attn_config cfg;
+    tq_kv_cache cache;
+    make_layer(&w, &cfg, nq, nkv, hd, hidden, theta, eps, wq, wk, wv, wo, qn, kn);
+    int rc = tq_attn_validate(&w, &cfg);
+    if (rc != 0) return rc;
+    rc = open_cache(&cache, &cfg, k_cache, v_cache, max_tokens);
+    if (rc != 0) return rc;
+    rc = tq_attn_validate_cache(&cache);
+    for (int i = 0; rc == 0 && i < n; i++)
+        rc = attention_layer(&w, &cfg, &cache, pos0 + i, xn + (size_t)i * hidden, scores, out + (size_t)i * hidden);
+    const int rc2 = close_cache(&cache, k_cache, v_cache);
+    return rc != 0 ? rc : rc2;
 }
 
 int tqref_layer_batch_run(int nq, int nkv, int hd, int hidden, float theta, float eps,
@@ -86,8 +174,9 @@ int tqref_layer_batch_run(int nq, int nkv, int hd, int hidden, float theta, floa
     tq_attn_config cfg;
     tq_kv_cache cache;
     make_layer(&w, &cfg, nq, nkv, hd, hidden, theta, eps, wq, wk, wv, wo, qn, kn);
-    make_cache(&cache, k_cache, v_cache, max_tokens);
     int rc = tq_attn_validate(&w, &cfg);
+    if (rc != 0) return rc;
+    rc = open_cache(&cache, &cfg, k_cache, v_cache, max_tokens);
     if (rc != 0) return rc;
 
     /* attention_layer_batch touches only cap, q, k, v, attn and xq of the
@@ -107,13 +196,15 @@ int tqref_layer_batch_run(int nq, int nkv, int hd, int hidden, float theta, floa
         rc = -100;
     } else {
         rc = attention_layer_batch(&w, &cfg, &cache, pos0, n, xn, scores, out, &ws);
+        if (rc == 0 && g_attn_rows) memcpy(g_attn_rows, ws.attn, (size_t)n * qdim * sizeof(float));
     }
     free(ws.q);
     free(ws.attn);
     free(ws.k);
     free(ws.v);
     free(ws.xq);
-    return rc;
+    const int rc2 = close_cache(&cache, k_cache, v_cache);
+    return rc != 0 ? rc : rc2;
 }
 
 /* Projections and per-head RMSNorm as attention_layer performs them before
@@ -255,7 +346,11 @@ int tqref_forward_run(TQREF_MODEL_ARGS, int max_tokens, int n_tok, const int *to
     int rc = build_model(&m, &layers, TQREF_MODEL_PASS);
     if (rc != 0) return rc;
     tq_ctx ctx;
+#ifdef TQ_DROPIN
+    rc = tq_ctx_init(&ctx, &m, g_kv_type, max_tokens);
+#else
     rc = tq_ctx_init(&ctx, &m, TQ_KV_Q8, max_tokens);
+#endif
     for (int i = 0; rc == 0 && i < n_tok; i++) {
         rc = tq_forward_token(&ctx, tokens[i]);
         if (rc == 0) memcpy(logits + (size_t)i * vocab, ctx.logits, (size_t)vocab * sizeof(float));
@@ -276,12 +371,22 @@ int tqref_prefill_run(TQREF_MODEL_ARGS, int max_tokens, int n_tok, const int *to
     int rc = build_model(&m, &layers, TQREF_MODEL_PASS);
     if (rc != 0) return rc;
     tq_ctx ctx;
+#ifdef TQ_DROPIN
+    rc = tq_ctx_init(&ctx, &m, g_kv_type, max_tokens);
+#else
     rc = tq_ctx_init(&ctx, &m, TQ_KV_Q8, max_tokens);
+#endif
     if (rc == 0) rc = tq_prefill(&ctx, tokens, n_tok);
     if (rc == 0) {
         memcpy(logits, ctx.logits, (size_t)vocab * sizeof(float));
         const size_t cache = (size_t)nkv * max_tokens * (hd / QK) * sizeof(block_q8);
         for (int l = 0; k_out && v_out && l < n_layers; l++) {
+#ifdef TQ_DROPIN
+            if (ctx.caches[l].type == TQ_KV_Q8_DEVICE) {
+                if (tq_kv_cache_download(&ctx.caches[l], k_out[l], v_out[l]) != 0) rc = -102;
+                continue;
+            }
+#endif
             memcpy(k_out[l], ctx.caches[l].k_q8, cache);
             memcpy(v_out[l], ctx.caches[l].v_q8, cache);
         }
@@ -290,6 +395,109 @@ int tqref_prefill_run(TQREF_MODEL_ARGS, int max_tokens, int n_tok, const int *to
     free(layers);
     return rc;
 }
+
+#ifdef TQ_DROPIN
+/* One host matrix (block_q8 or block_q4 rows) on the device in the tiled
+ * layout of the MI355X library; NULL on failure. */
+static void *upload_matrix(const void *host, int rows, int cols, int q4) {
+    const size_t bytes = q4 ? tq_hip_q4_matrix_bytes(rows, cols) : tq_hip_q8_matrix_bytes(rows, cols);
+    void *staging = NULL, *dev = NULL;
+    int rc = tq_hip_malloc(&staging, bytes);
+    if (rc == 0) rc = tq_hip_malloc(&dev, bytes);
+    if (rc == 0) rc = tq_hip_memcpy_h2d(staging, host, bytes, NULL);
+    if (rc == 0)
+        rc = q4 ? tq_hip_q4_pack(dev, (const block_q4 *)staging, rows, cols, NULL)
+                : tq_hip_q8_pack(dev, (const block_q8 *)staging, rows, cols, NULL);
+    if (rc == 0) rc = tq_hip_device_synchronize();
+    tq_hip_free(staging);
+    if (rc != 0) {
+        tq_hip_free(dev);
+        return NULL;
+    }
+    return dev;
+}
+
+static float *upload_floats(const float *host, int n) {
+    void *dev = NULL;
+    if (tq_hip_malloc(&dev, (size_t)n * sizeof(float)) != 0) return NULL;
+    if (tq_hip_memcpy_h2d(dev, host, (size_t)n * sizeof(float), NULL) != 0) {
+        tq_hip_free(dev);
+        return NULL;
+    }
+    return (float *)dev;
+}
+
+/* The reference's tq_ctx_init + tq_forward_token with ctx.dev pointing at a
+ * device model built from the same host weights (tq_dev_ctx_init): the
+ * edited tq_forward_token runs each token there and copies the logits into
+ * ctx.logits, which land in logits [n_tok][vocab]. */
+int tqref_forward_devmodel_run(TQREF_MODEL_ARGS, int max_tokens, int n_tok, const int *tokens, float *logits) {
+    tq_model m;
+    tq_layer_weights *layers = NULL;
+    int rc = build_model(&m, &layers, TQREF_MODEL_PASS);
+    if (rc != 0) return rc;
+    const int q4 = fmt == 1;
+    tq_dev_layer_weights *dl = calloc((size_t)n_layers, sizeof *dl);
+    void **owned = calloc((size_t)n_layers * 11 + 2, sizeof(void *));
+    int n_owned = 0;
+#define KEEP(p) (owned[n_owned++] = (void *)(p), (p))
+    if (!dl || !owned) rc = -100;
+    for (int l = 0; rc == 0 && l < n_layers; l++) {
+        dl[l].input_norm = KEEP(upload_floats(input_norm[l], hidden));
+        dl[l].post_norm = KEEP(upload_floats(post_norm[l], hidden));
+        dl[l].attn.wq = KEEP(upload_matrix(wq[l], nq * hd, hidden, q4));
+        dl[l].attn.wk = KEEP(upload_matrix(wk[l], nkv * hd, hidden, q4));
+        dl[l].attn.wv = KEEP(upload_matrix(wv[l], nkv * hd, hidden, q4));
+        dl[l].attn.wo = KEEP(upload_matrix(wo[l], hidden, nq * hd, q4));
+        dl[l].attn.q_norm = KEEP(upload_floats(qn[l], hd));
+        dl[l].attn.k_norm = KEEP(upload_floats(kn[l], hd));
+        dl[l].attn.hidden = hidden;
+        dl[l].attn.rms_eps = eps;
+        dl[l].attn.format = q4 ? TQ_HIP_FORMAT_Q4 : TQ_HIP_FORMAT_Q8;
+        dl[l].mlp.wgate = KEEP(upload_matrix(wgate[l], inter, hidden, q4));
+        dl[l].mlp.wup = KEEP(upload_matrix(wup[l], inter, hidden, q4));
+        dl[l].mlp.wdown = KEEP(upload_matrix(wdown[l], hidden, inter, q4));
+        dl[l].mlp.hidden = hidden;
+        dl[l].mlp.inter = inter;
+        dl[l].mlp.format = dl[l].attn.format;
+        for (int i = n_owned - 11; i < n_owned; i++)
+            if (!owned[i]) rc = -103;
+    }
+    tq_dev_model dm;
+    memset(&dm, 0, sizeof dm);
+    if (rc == 0) {
+        dm.attn = m.cfg.attn;
+        dm.n_layers = n_layers;
+        dm.intermediate_size = inter;
+        dm.vocab_size = vocab;
+        dm.embed = KEEP(upload_matrix(embed, vocab, hidden, embed_fmt == 1));
+        dm.final_norm = KEEP(upload_floats(final_norm, hidden));
+        dm.layers = dl;
+        dm.embed_format = embed_fmt == 1 ? TQ_HIP_FORMAT_Q4 : TQ_HIP_FORMAT_Q8;
+        if (!dm.embed || !dm.final_norm) rc = -103;
+    }
+#undef KEEP
+    tq_dev_ctx dctx;
+    memset(&dctx, 0, sizeof dctx);
+    tq_ctx ctx;
+    memset(&ctx, 0, sizeof ctx);
+    if (rc == 0) rc = tq_dev_ctx_init(&dctx, &dm, max_tokens);
+    if (rc == 0) rc = tq_ctx_init(&ctx, &m, TQ_KV_Q8, max_tokens);
+    if (rc == 0) ctx.dev = &dctx;
+    for (int i = 0; rc == 0 && i < n_tok; i++) {
+        rc = tq_forward_token(&ctx, tokens[i]);
+        if (rc == 0) memcpy(logits + (size_t)i * vocab, ctx.logits, (size_t)vocab * sizeof(float));
+    }
+    ctx.dev = NULL;
+    tq_ctx_free(&ctx);
+    tq_dev_ctx_free(&dctx);
+    for (int i = 0; owned && i < n_owned; i++) tq_hip_free(owned[i]);
+    free(owned);
+    free(dl);
+    free(layers);
+    return rc;
+}
+#endif
 
 /* Which matmul/attention ISA the build dispatches to ("AVX2" or "scalar"). */
 const char *tqref_isa(void) { return kernel_isa_name(); }

@@ -12,24 +12,11 @@ using namespace tq;
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// h = silu(g) * u (silu(x) = x * (1 / (1 + expf(-x)))), then quantize_row_q8
-// of h: one 32-lane group per block, 8 blocks per work-group.  Rows are
-// contiguous, so blocks never straddle two of them.
-__global__ __launch_bounds__(256) void silu_quant_kernel(const float *__restrict__ gate,
-                                                         const float *__restrict__ up,
-                                                         unsigned char *__restrict__ hq, long nblocks) {
-#pragma clang fp contract(off)
-    const long e = (long)blockIdx.x * 256 + threadIdx.x;
-    if ((e >> 5) >= nblocks) return;   // whole 32-lane groups leave together
-    const float g = gate[e];
-    const float sig = 1.0f / (1.0f + expf(-g));
-    const float h = g * sig * up[e];
-    quantize_store32(h, hq + (e >> 5) * kBlockBytes);
-}
-
-// The same, 8 lanes x 4 values per block: float4 loads of gate and up, one
-// dword of codes per lane (16-byte aligned rows).  Whole 8-lane groups stay
-// together, as quantize8x4's DPP steps need.
+// h = silu(g) * u (silu(x) = x * (1 / (1 + expf(-x))), model/silu.c:6-18),
+// then quantize_row_q8 of h, 8 lanes x 4 values per block: float4 loads of
+// gate and up, one dword of codes per lane.  Rows are contiguous, so blocks
+// never straddle two of them; whole 8-lane groups stay together, as
+// quantize8x4's DPP steps need.
 __global__ __launch_bounds__(256) void silu_quant8_kernel(const float *__restrict__ gate,
                                                           const float *__restrict__ up,
                                                           unsigned char *__restrict__ hq, long nblocks) {
@@ -274,12 +261,11 @@ int embed_lookup(bool q4, const void *embed, int rows, int cols, int token, cons
 hipError_t tq_launch_silu_quant(const float *gate, const float *up, block_q8 *hq, long n, hipStream_t s) {
     const long nblocks = n / kQK;
     if (nblocks <= 0) return hipSuccess;
-    if ((((uintptr_t)gate | (uintptr_t)up) & 15) == 0 && ((uintptr_t)hq & 3) == 0)
-        hipLaunchKernelGGL(silu_quant8_kernel, dim3((unsigned)((nblocks * 8 + 255) / 256)), dim3(256), 0, s, gate,
-                           up, reinterpret_cast<unsigned char *>(hq), nblocks);
-    else
-        hipLaunchKernelGGL(silu_quant_kernel, dim3((unsigned)((nblocks * kQK + 255) / 256)), dim3(256), 0, s, gate,
-                           up, reinterpret_cast<unsigned char *>(hq), nblocks);
+    // gate, up and hq are workspace rows at 256-byte offsets of a 16-byte
+    // aligned workspace (tq_hip_mlp_layer_async checks it)
+    if ((((uintptr_t)gate | (uintptr_t)up) & 15) || ((uintptr_t)hq & 3)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(silu_quant8_kernel, dim3((unsigned)((nblocks * 8 + 255) / 256)), dim3(256), 0, s, gate, up,
+                       reinterpret_cast<unsigned char *>(hq), nblocks);
     return hipGetLastError();
 }
 

@@ -10,24 +10,26 @@
 // prefill_stage_kernel — once per (key tile of 32, kv head) over [0, kend):
 //   reads the tile's K and V rows from the paged cache and writes one
 //   contiguous tile image laid out as the MFMA operands want them:
-//     K' hi|lo [key half][block][lane][8 bf16]   (A of the score product)
+//     K codes [key half][block][lane][8 bf16]     (A of the score product)
+//     K scales [key half][block][lane group][4]   (kd of a lane's four keys)
 //     V' hi|lo [column tile][lane][8 bf16]        (A of the P.V product)
-//   with K' = code * kd and V' = code * vd rounded once to fp32 and split into
-//   bf16 hi + lo (hi + lo = x to 2^-18 relative).  Every query block then
-//   streams these images instead of re-deriving them.
+//   The int8 K codes are exact in bf16.  V' = code * vd is rounded once to
+//   fp32 and split into bf16 hi + lo (hi + lo = x to 2^-18 relative).  Every
+//   query block then streams these images instead of re-deriving them.
 //
 // prefill_kernel — work-group of 256 threads (4 waves), one kv head, 64*NJ
 //   (query, head) rows = QB = 64*NJ/G consecutive query tokens x the G heads
 //   of the group, in row tiles of 16 queries of one head; wave w owns NJ row
-//   tiles.  q is quantized exactly as quantize_row_q8 does, then q' = code *
-//   qd * scale * log2(e) is split into bf16 hi + lo, held in registers.
+//   tiles.  q is quantized exactly as quantize_row_q8 does; its codes go to
+//   registers as bf16 (exact), its scales times scale * log2(e) beside them.
 //   Key tiles are copied straight into two LDS buffers (global_load_lds), one
 //   tile ahead, one barrier per tile:
-//     S^T = K'.q'^T on v_mfma_f32_16x16x32_bf16 per 32-value block, three
-//       products (hi.hi + hi.lo + lo.hi): the dequantized dot of
-//       attn_scores_q8 (model/attn_q8.c:24-30) to ~2^-17 relative per term,
-//       in the exp2 domain, replacing a per-block int32 -> fp32 rescale on
-//       the VALU;
+//     S^T = sum over blocks b of (kd_b * qd_b) * D_b, D_b = Kcodes_b .
+//       qcodes_b^T on v_mfma_f32_16x16x32_bf16: products of integers below
+//       2^14, summed 32 at a time, stay below 2^24, so D_b is the exact int32
+//       block dot of attn_scores_q8 (model/attn_q8.c:24-30) in any
+//       accumulation order; each block's dot is scaled and added in block
+//       order (one multiply, one fma per score and block), exp2 domain;
 //     online softmax per query with a causal mask; the running max moves only
 //       when a tile exceeds it by more than 2^8;
 //     O^T += V'^T . P^T on the same bf16 product, P split into hi + lo.
@@ -76,13 +78,17 @@ struct TileImg {
     static constexpr int NB = HD / kQK;
     static constexpr int MT = HD / 16;
     static constexpr int ROW = NB * kBlockBytes;
-    static constexpr int KH_OFF = 0;                       // [2][NB][64] x 16 B
-    static constexpr int KL_OFF = KH_OFF + 2 * NB * 64 * 16;
-    static constexpr int VH_OFF = KL_OFF + 2 * NB * 64 * 16;   // [MT][64] x 16 B
+    static constexpr int KC_OFF = 0;                           // [2][NB][64] x 16 B: 8 bf16 codes
+    static constexpr int KD_OFF = KC_OFF + 2 * NB * 64 * 16;   // [2][NB][4][4] fp32 scales,
+    static constexpr int VH_OFF = KD_OFF + 1024;               //   padded to 1 KB; [MT][64] x 16 B
     static constexpr int VL_OFF = VH_OFF + MT * 64 * 16;
     static constexpr int BYTES = VL_OFF + MT * 64 * 16;
     static constexpr int CHUNKS = BYTES / 16;
-    static_assert(BYTES % 4096 == 0, "whole rounds of 16-byte copies by 256 threads");
+    static constexpr int ROUNDS = CHUNKS / kThreads;           // whole rounds of 16-byte copies
+    static constexpr int REM = CHUNKS % kThreads;              // copies of the last, partial round
+    static_assert(BYTES % 16 == 0 && KD_OFF % 16 == 0 && VH_OFF % 16 == 0, "16-byte chunks");
+    static_assert(2 * NB * 16 * 4 <= 1024, "K scales fit their 1 KB");
+    static_assert(REM % 64 == 0, "the partial round is whole waves");
 };
 
 // Key slot i (0..7) of lane group g in the MFMA k order used for P.V:
@@ -189,18 +195,21 @@ __global__ __launch_bounds__(kThreads) void prefill_stage_kernel(StageArgs a) {
     const unsigned char *rk = reinterpret_cast<const unsigned char *>(raw[0]);
     const unsigned char *rv = reinterpret_cast<const unsigned char *>(raw[1]);
     unsigned char *out = a.img + ((size_t)a.n_tiles * kvh + kt) * I::BYTES;
-    // K': entry (mt, b, lane) = key mt*16 + lane%16, block b, values 8*(lane/16)..+7
+    // K codes: entry (mt, b, lane) = key mt*16 + lane%16, block b, codes 8*(lane/16)..+7 as bf16
     for (int e = tid; e < 2 * I::NB * 64; e += kThreads) {
         const int mt = e / (I::NB * 64), b = (e / 64) % I::NB, ln = e % 64;
-        const unsigned char *row = rk + (mt * 16 + (ln & 15)) * ROW + b * kBlockBytes;
-        const float d = *reinterpret_cast<const float *>(row);
-        float x[8];
+        const unsigned char *row = rk + (mt * 16 + (ln & 15)) * ROW + b * kBlockBytes + 4 + 8 * (ln >> 4);
+        u32x4 w;
 #pragma unroll
-        for (int i = 0; i < 8; i++) x[i] = (float)(int8_t)row[4 + 8 * (ln >> 4) + i] * d;
-        u32x4 hi, lo;
-        split_bf16(x, hi, lo);
-        *reinterpret_cast<u32x4 *>(out + I::KH_OFF + e * 16) = hi;
-        *reinterpret_cast<u32x4 *>(out + I::KL_OFF + e * 16) = lo;
+        for (int i = 0; i < 4; i++) w[i] = bf16_pair((float)(int8_t)row[2 * i], (float)(int8_t)row[2 * i + 1]);
+        *reinterpret_cast<u32x4 *>(out + I::KC_OFF + e * 16) = w;
+    }
+    // K scales: entry (mt, b, g, r) = kd of key mt*16 + 4g + r, block b (the
+    // four keys a lane of group g holds of the score product)
+    for (int e = tid; e < 2 * I::NB * 16; e += kThreads) {
+        const int mt = e / (I::NB * 16), b = (e / 16) % I::NB, key = mt * 16 + (e & 15);
+        *reinterpret_cast<float *>(out + I::KD_OFF + e * 4) =
+            *reinterpret_cast<const float *>(rk + key * ROW + b * kBlockBytes);
     }
     // V' = code * vd: entry (m, lane) = column m*16 + lane%16, keys perm_key(lane/16, 0..7)
     for (int e = tid; e < I::MT * 64; e += kThreads) {
@@ -229,11 +238,9 @@ struct PShape {
     static constexpr int QT = QB / 16;             // query tiles per head
     static constexpr int MT = I::MT;               // output column tiles
     static constexpr int QCS = HD + 8;             // LDS stride of a q code row
-    static constexpr int ROUNDS = I::CHUNKS / kThreads;   // copies per thread per tile
     static constexpr int Q_BYTES = RW * QCS + RW * NB * 4;
     static_assert(RW % G == 0 && QB % 16 == 0, "whole query tiles");
     static_assert(Q_BYTES <= I::BYTES, "q staging fits one tile buffer");
-    static_assert(ROUNDS < 32, "vmcnt immediate");
 };
 
 struct PrefillArgs {
@@ -278,12 +285,15 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
     const unsigned char *img = a.img + (size_t)kvh * a.n_tiles * I::BYTES;
 
     // copy of tile kt into an LDS buffer: thread t's copy r is chunk t + 256 r
+    // (the partial last round: the first REM threads, whole waves)
     auto fetch = [&](unsigned char *buf, int kt) {
         const unsigned char *src = img + (size_t)kt * I::BYTES;
         const int wu = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
-        for (int r = 0; r < S::ROUNDS; r++)
+        for (int r = 0; r < I::ROUNDS; r++)
             dma16(src + 16 * (tid + kThreads * r), buf + 16 * (kThreads * r + 64 * wu));
+        if (I::REM > 0 && 64 * wu < I::REM)
+            dma16(src + 16 * (tid + kThreads * I::ROUNDS), buf + 16 * (kThreads * I::ROUNDS + 64 * wu));
     };
     // the first tile flies while q is quantized (q staging uses tile1)
     fetch(tile0, kt_begin);
@@ -336,9 +346,10 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
     }
     __syncthreads();
 
-    // ---- per-lane B operands: q' = code * qd * scale * log2(e) of query l16,
-    //      values 32b + 8lg .. +7, as bf16 hi | lo
-    v8bf qh[NJ][NB], ql[NJ][NB];
+    // ---- per-lane B operands: the q codes of query l16, values 32b + 8lg ..
+    //      +7, as bf16 (exact), and qd * scale * log2(e) per block
+    v8bf qcb[NJ][NB];
+    float qsc[NJ][NB];
     int qpos[NJ];
     const float qscale = a.scale * kLog2e;
 #pragma unroll
@@ -350,15 +361,12 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
         qpos[j] = a.pos0 + qi;
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            const float s = qd[r * NB + b] * qscale;
+            qsc[j][b] = qd[r * NB + b] * qscale;
             const unsigned char *c = qc + r * S::QCS + b * kQK + 8 * lg;
-            float x[8];
+            u32x4 w;
 #pragma unroll
-            for (int i = 0; i < 8; i++) x[i] = (float)(int8_t)c[i] * s;
-            u32x4 hi, lo;
-            split_bf16(x, hi, lo);
-            qh[j][b] = as_v8bf(hi);
-            ql[j][b] = as_v8bf(lo);
+            for (int i = 0; i < 4; i++) w[i] = bf16_pair((float)(int8_t)c[2 * i], (float)(int8_t)c[2 * i + 1]);
+            qcb[j][b] = as_v8bf(w);
         }
     }
 
@@ -385,7 +393,9 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
         __syncthreads();
         if (kt + 1 < kt_end) fetch(odd ? tile0 : tile1, kt + 1);
 
-        // S^T = K'.q'^T for keys [32kt, 32kt+32) x the wave's queries
+        // S^T for keys [32kt, 32kt+32) x the wave's queries: per block the
+        // exact int32 dot on the matrix cores, then (kd * qd') * dot added in
+        // block order
         v4f s[2][NJ];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
@@ -395,13 +405,14 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
         for (int b = 0; b < NB; b++) {
 #pragma unroll
             for (int mt = 0; mt < 2; mt++) {
-                const v8bf kh = as_v8bf(*reinterpret_cast<const u32x4 *>(T + I::KH_OFF + ((mt * NB + b) * 64 + lane) * 16));
-                const v8bf kl = as_v8bf(*reinterpret_cast<const u32x4 *>(T + I::KL_OFF + ((mt * NB + b) * 64 + lane) * 16));
+                const v8bf kc = as_v8bf(*reinterpret_cast<const u32x4 *>(T + I::KC_OFF + ((mt * NB + b) * 64 + lane) * 16));
+                const v4f kd = *reinterpret_cast<const v4f *>(T + I::KD_OFF + ((mt * NB + b) * 4 + lg) * 16);
 #pragma unroll
                 for (int j = 0; j < NJ; j++) {
-                    s[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[j][b], s[mt][j], 0, 0, 0);
-                    s[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[j][b], s[mt][j], 0, 0, 0);
-                    s[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[j][b], s[mt][j], 0, 0, 0);
+                    const v4f d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kc, qcb[j][b], v4f{0.0f, 0.0f, 0.0f, 0.0f},
+                                                                          0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) s[mt][j][r] = __builtin_fmaf(d[r], kd[r] * qsc[j][b], s[mt][j][r]);
                 }
             }
         }

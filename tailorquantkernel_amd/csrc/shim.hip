@@ -468,6 +468,7 @@ int tq_hip_device_synchronize(void) { return herr(hipDeviceSynchronize()); }
 
 int tq_hip_quantize_row_q8(const float *x, block_q8 *out, int n, void *stream) {
     if (n < 0 || (n > 0 && (!x || !out))) return TQ_HIP_EINVAL;
+    if (((uintptr_t)x | (uintptr_t)out) & 3) return TQ_HIP_EINVAL;   // the kernels store dwords
     return herr(tq_launch_quantize(x, out, n, (hipStream_t)stream));
 }
 

@@ -328,21 +328,28 @@ def C_ref(w):
 # ---------------------------------------------------------------------------
 # row RMSNorm and the batched layer (attention_layer_batch)
 
-@pytest.mark.parametrize("n,rows", [(128, 1000), (64, 63), (32, 65), (256, 130), (4096, 3), (128, 1)])
-def test_rmsnorm_rows_bitexact(nat, oracle, n, rows):
+@pytest.mark.parametrize("n,rows", [(128, 1000), (64, 63), (32, 65), (256, 130), (4096, 3), (128, 1), (30, 17),
+                                    (4094, 2)])
+@pytest.mark.parametrize("skew", [0, 4])
+def test_rmsnorm_rows_bitexact(nat, oracle, n, rows, skew):
+    """Rows of 16-byte aligned pointers and n % 4 == 0 take the float4 kernel;
+    a 4-byte skew (skew=4) or n % 4 != 0 takes the scalar one.  Both bit-exact."""
     lib = nat.load()
     rng = np.random.default_rng(n + rows)
     x = (rng.standard_normal(rows * n) * rng.choice([1e-3, 1.0, 40.0])).astype(np.float32)
     w = rng.uniform(-1.5, 1.5, n).astype(np.float32)
+    pad = np.zeros(skew // 4, np.float32)
     for eps in (1e-6, 1e-5):
         ref = oracle.rmsnorm(x, w, eps)
-        dx, dw = dev(nat, x), dev(nat, w)
-        out = nat.DeviceBuffer(x.nbytes)
-        nat.check(lib.tq_hip_rmsnorm_rows(dx.ptr, dw.ptr, out.ptr, rows, n, eps, None), "rmsnorm_rows")
-        nat.check(lib.tq_hip_rmsnorm_rows(dx.ptr, dw.ptr, dx.ptr, rows, n, eps, None), "rmsnorm_rows in place")
+        dx, dw = dev(nat, np.concatenate([pad, x])), dev(nat, np.concatenate([pad, w]))
+        out = nat.DeviceBuffer(x.nbytes + skew)
+        nat.check(lib.tq_hip_rmsnorm_rows(dx.ptr + skew, dw.ptr + skew, out.ptr + skew, rows, n, eps, None),
+                  "rmsnorm_rows")
+        nat.check(lib.tq_hip_rmsnorm_rows(dx.ptr + skew, dw.ptr + skew, dx.ptr + skew, rows, n, eps, None),
+                  "rmsnorm_rows in place")
         nat.check(lib.tq_hip_device_synchronize(), "sync")
-        assert out.download((x.size,), np.float32).tobytes() == ref.tobytes()
-        assert dx.download((x.size,), np.float32).tobytes() == ref.tobytes()
+        assert out.download((x.size + skew // 4,), np.float32)[skew // 4:].tobytes() == ref.tobytes()
+        assert dx.download((x.size + skew // 4,), np.float32)[skew // 4:].tobytes() == ref.tobytes()
 
 
 def ws_views(raw, nq, nkv, hd, hidden, n):

@@ -73,8 +73,12 @@ def tiled(nat, Wq, rows, cols):
     return b
 
 
-@pytest.mark.parametrize("hidden,inter,n", [(256, 640, 1), (256, 640, 2), (128, 320, 3), (512, 1024, 20)])
-def test_mlp_layer(nat, oracle, hidden, inter, n):
+@pytest.mark.parametrize("hidden,inter,n,skew", [(256, 640, 1, 0), (256, 640, 2, 0), (128, 320, 3, 0),
+                                                 (512, 1024, 20, 0), (256, 640, 1, 4), (128, 320, 3, 4),
+                                                 (512, 1024, 20, 4)])
+def test_mlp_layer(nat, oracle, hidden, inter, n, skew):
+    """skew=4: xn sits 4 bytes past a 16-byte boundary, so its rows are
+    quantized by the one-value-per-lane kernel before the matmuls."""
     lib = nat.load()
     rng = np.random.default_rng(hidden + n)
     wg = oracle.pack_matrix_q8(rng.standard_normal((inter, hidden)).astype(np.float32) * 0.1)
@@ -85,8 +89,8 @@ def test_mlp_layer(nat, oracle, hidden, inter, n):
     wsb = lib.tq_hip_mlp_ws_bytes(C.byref(w), n)
     ws = nat.DeviceBuffer(wsb)
     xn = normal(n * hidden, 7) * 2
-    dx, dout = dev(nat, xn), nat.DeviceBuffer(n * hidden * 4)
-    nat.check(lib.tq_hip_mlp_layer_async(C.byref(w), n, dx.ptr, dout.ptr, ws.ptr, wsb, None), "mlp")
+    dx, dout = dev(nat, np.concatenate([np.zeros(skew // 4, np.float32), xn])), nat.DeviceBuffer(n * hidden * 4)
+    nat.check(lib.tq_hip_mlp_layer_async(C.byref(w), n, dx.ptr + skew, dout.ptr, ws.ptr, wsb, None), "mlp")
     sync(nat)
     out = dout.download((n, hidden), np.float32)
     raw = ws.download((wsb,), np.uint8)

@@ -75,11 +75,32 @@ def test_quantize_bitexact_golden(nat):
     np.testing.assert_array_equal(qb["q"], g["quant_q"])
 
 
+def gpu_quantize_skewed(nat, x, skew_x, skew_out):
+    """quantize_row_q8 with x and out `skew_*` bytes past a 16-byte boundary
+    (multiples of 4): x off a 16-byte boundary takes the one-value-per-lane
+    kernel, the rest the 8-lane one."""
+    x = np.ascontiguousarray(x, np.float32)
+    nbk = x.size // QK
+    dx = dev(nat, np.concatenate([np.zeros(skew_x // 4, np.float32), x]))
+    dq = nat.DeviceBuffer(nbk * 36 + 16)
+    nat.check(nat.load().tq_hip_quantize_row_q8(dx.ptr + skew_x, dq.ptr + skew_out, x.size, None), "quantize")
+    sync(nat)
+    raw = dq.download((nbk * 36 + skew_out,), np.uint8)
+    return raw[skew_out:].view(BLOCK_Q8)
+
+
 def test_quantize_bitexact_oracle(nat, oracle):
     rng = np.random.default_rng(7)
     for scale in (1e-38, 1e-20, 1e-3, 1.0, 8.0, 1e20):
         x = (rng.standard_normal(32 * 997) * scale).astype(np.float32)
-        assert gpu_quantize(nat, x).tobytes() == oracle.quantize_row_q8(x).tobytes()
+        ref = oracle.quantize_row_q8(x).tobytes()
+        assert gpu_quantize(nat, x).tobytes() == ref
+        for skew_x, skew_out in ((4, 0), (8, 0), (12, 4), (0, 8)):
+            assert gpu_quantize_skewed(nat, x, skew_x, skew_out).tobytes() == ref, (scale, skew_x, skew_out)
+    # x and out must be 4-byte aligned (the kernels store dwords)
+    dx, dq = dev(nat, np.zeros(64, np.float32)), nat.DeviceBuffer(2 * 36 + 16)
+    assert nat.load().tq_hip_quantize_row_q8(dx.ptr, dq.ptr + 1, 32, None) == nat.EINVAL
+    assert nat.load().tq_hip_quantize_row_q8(dx.ptr + 2, dq.ptr, 32, None) == nat.EINVAL
     # trailing values past the last whole block are ignored, as n / QK drops them
     x = fill_random(100, 3)
     assert gpu_quantize(nat, x).tobytes() == oracle.quantize_row_q8(x).tobytes()
