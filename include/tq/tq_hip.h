@@ -38,6 +38,7 @@ extern "C" {
 #define TQ_HIP_ETYPE (-3)      /* unsupported head_dim / group size             */
 #define TQ_HIP_ENODEV (-4)     /* no usable gfx950 device                        */
 #define TQ_HIP_ENOTREADY (-5)  /* sequence has no page for a requested position  */
+#define TQ_HIP_ESCRATCH (-6)   /* beyond the allocation-free call's fixed scratch */
 #define TQ_HIP_EHIP_BASE (-1000)
 
 /* ---- device and plumbing ------------------------------------------------ */
@@ -172,6 +173,25 @@ int tq_hip_decode_step_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq,
                              const int32_t *d_pos, int max_pos, const float *d_q,
                              const float *d_k, const float *d_v, const float *d_cos,
                              const float *d_sin, float *d_out, void *stream);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): tq_hip_decode_step_async with its split-K scratch (the
+ * partial rows and arrival counters) taken from one fixed array of
+ * TQ_HIP_NOALLOC_SCRATCH_BYTES that the library holds on each GPU until the
+ * process ends, instead of buffers the cache grows with hipMalloc.  Same
+ * kernels, same results bit for bit; it allocates nothing.  A call whose
+ * scratch would not fit — split-K over more than 1024 (query, kv head)
+ * pairs, or more partial rows than the rest of the array holds (it holds 64
+ * queries of up to 16k tokens or one of up to 512k at the 8B shape, 16 of
+ * 32k at the 70B shape) — returns TQ_HIP_ESCRATCH before launching.  Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (several
+ * streams at once) race.  tq_hip_init sets the array up on its device
+ * (counters cleared); without it the first call on a device does, and must
+ * then not be inside a graph capture. */
+#define TQ_HIP_NOALLOC_SCRATCH_BYTES (8u << 20)
+int tq_hip_decode_step_noalloc(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_pos,
+                               int max_pos, const float *d_q, const float *d_k, const float *d_v,
+                               const float *d_cos, const float *d_sin, float *d_out, void *stream);
 /* The same step with the per-head RMSNorm of q and of the new K in front of
  * RoPE (norm_heads, model/attention_layer.c:48-53,183-184; model/rmsnorm.c:4-19):
  * d_q and d_k are the projections' raw outputs, d_q_norm / d_k_norm the

@@ -300,14 +300,24 @@ void seq_contig(const tq_hip_kv *kv, int seq, int *first, int *n) {
     while (*n < kv->desc.max_pages_per_seq && row[*n] == row[0] + *n) (*n)++;
 }
 
+// Split-K scratch a call brings instead of the cache's own (grown) buffers.
+struct CallScratch {
+    float *partials;
+    size_t partial_bytes;
+    int *counters;         // zero between launches
+    size_t counter_ints;
+};
+
 // contig_seq: the one sequence every query of this call reads, or -1.
 // q_norm non-null: q (and the new K) are raw projections, RMSNorm'd in the
 // kernel with q_norm / k_norm and eps (MFMA kernel only).
+// scratch non-null: the split-K partials and counters come from it (a call
+// that needs more returns TQ_HIP_ESCRATCH) and nothing is allocated.
 int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_len, int len_plus,
                   int seq_const, int seq_stride, int pos0, int max_len, const float *d_q, const float *d_cos,
                   const float *d_sin, const float *d_k, const float *d_v, float *d_out,
                   hipStream_t s, int contig_seq, const float *q_norm = nullptr,
-                  const float *k_norm = nullptr, float rms_eps = 0.0f) {
+                  const float *k_norm = nullptr, float rms_eps = 0.0f, const CallScratch *scratch = nullptr) {
     if (n_q <= 0) return TQ_HIP_OK;
     // queries and kv heads are grid dimensions y/z (at most 65535 each)
     if (n_q > 65535 || kv->desc.n_kv_heads > 65535) return TQ_HIP_EINVAL;
@@ -371,13 +381,64 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
         const int g = D.n_q_heads / D.n_kv_heads;
         const size_t row = v3 ? (size_t)tq_decode3_partial_floats(D.head_dim, g) : (size_t)g * (D.head_dim + 2);
         const size_t bytes = (size_t)n_q * D.n_kv_heads * a.n_splits * row * sizeof(float);
-        int rc = ensure_partials(kv, bytes);
-        if (rc == TQ_HIP_OK) rc = ensure_counters(kv, (size_t)n_q * D.n_kv_heads * TQ_DECODE_COUNTER_STRIDE, s);
-        if (rc != TQ_HIP_OK) return rc;
-        a.partials = kv->partials;
-        a.counters = kv->counters;
+        const size_t n_counters = (size_t)n_q * D.n_kv_heads * TQ_DECODE_COUNTER_STRIDE;
+        if (scratch) {
+            if (bytes > scratch->partial_bytes || n_counters > scratch->counter_ints) return TQ_HIP_ESCRATCH;
+            a.partials = scratch->partials;
+            a.counters = scratch->counters;
+        } else {
+            int rc = ensure_partials(kv, bytes);
+            if (rc == TQ_HIP_OK) rc = ensure_counters(kv, n_counters, s);
+            if (rc != TQ_HIP_OK) return rc;
+            a.partials = kv->partials;
+            a.counters = kv->counters;
+        }
     }
     return herr(v3 ? tq_launch_decode3(a, waves, s) : tq_launch_decode(a, s));
+}
+
+// ---- the allocation-free decode step's scratch ----------------------------
+// One fixed array per GPU, held until the process ends: [arrival counters |
+// split-K partial rows].  Host code never passes `scratch` itself (its name is
+// a host-side stand-in); it uses the device address hipGetSymbolAddress
+// returned for the current device.
+constexpr size_t kNoAllocCounterBytes = 256u << 10;   // 1024 (query, kv head) pairs x 256 B
+static_assert(TQ_HIP_NOALLOC_SCRATCH_BYTES % 256 == 0 && TQ_HIP_NOALLOC_SCRATCH_BYTES > kNoAllocCounterBytes,
+              "scratch layout");
+static __device__ __align__(256) unsigned char scratch[TQ_HIP_NOALLOC_SCRATCH_BYTES];
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t *p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0u;
+}
+
+constexpr int kMaxDevices = 64;
+struct NoAllocDevice {
+    std::once_flag once;
+    unsigned char *ptr = nullptr;   // scratch on this device
+    int rc = TQ_HIP_OK;
+};
+NoAllocDevice g_noalloc[kMaxDevices];
+
+// Once per device, with that device current: look up the array's device
+// address and clear its counters (a fill kernel, then a wait: not inside a
+// graph capture).  The decode kernel's combining work-group puts every
+// counter it used back to 0, so they stay zero between calls.
+int noalloc_setup(int device) {
+    if (device < 0 || device >= kMaxDevices) return TQ_HIP_ENODEV;
+    NoAllocDevice &d = g_noalloc[device];
+    std::call_once(d.once, [&d] {
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e == hipSuccess) {
+            hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, nullptr, static_cast<uint32_t *>(p),
+                               kNoAllocCounterBytes / 4);
+            e = hipGetLastError();
+        }
+        if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+        d.rc = herr(e);
+        if (e == hipSuccess) d.ptr = static_cast<unsigned char *>(p);
+    });
+    return d.rc;
 }
 
 bool seq_ok(const tq_hip_kv *kv, int seq) { return kv && seq >= 0 && seq < kv->desc.max_seqs; }
@@ -401,7 +462,7 @@ int tq_hip_init(int device) {
     hipDeviceProp_t p;
     TQ_TRY(hipGetDeviceProperties(&p, device));
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0) return TQ_HIP_ENODEV;
-    return TQ_HIP_OK;
+    return noalloc_setup(device);
 }
 
 const char *tq_hip_strerror(int code) {
@@ -412,6 +473,7 @@ const char *tq_hip_strerror(int code) {
         case TQ_HIP_ETYPE: return "unsupported head_dim or group size";
         case TQ_HIP_ENODEV: return "no gfx950 device";
         case TQ_HIP_ENOTREADY: return "position has no mapped page";
+        case TQ_HIP_ESCRATCH: return "call needs more split-K scratch than the allocation-free entry point holds";
         default: break;
     }
     if (code <= TQ_HIP_EHIP_BASE) return hipGetErrorString((hipError_t)(TQ_HIP_EHIP_BASE - code));
@@ -730,6 +792,24 @@ int tq_hip_decode_step_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const
     if (!d_seq && n_q > kv->desc.max_seqs) return TQ_HIP_EINVAL;
     return decode_common(kv, n_q, d_seq, d_pos, 1, 0, 1, 0, max_pos + 1, d_q, d_cos, d_sin, d_k, d_v, d_out,
                          pick(kv, stream), (!d_seq && n_q == 1) ? 0 : -1);
+}
+
+int tq_hip_decode_step_noalloc(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_pos, int max_pos,
+                               const float *d_q, const float *d_k, const float *d_v, const float *d_cos,
+                               const float *d_sin, float *d_out, void *stream) {
+    if (!kv || n_q < 0 || max_pos < 0) return TQ_HIP_EINVAL;
+    if (n_q > 0 && (!d_pos || !d_k || !d_v)) return TQ_HIP_EINVAL;
+    if (!d_seq && n_q > kv->desc.max_seqs) return TQ_HIP_EINVAL;
+    int dev = 0;
+    TQ_TRY(hipGetDevice(&dev));
+    const int rc = noalloc_setup(dev);
+    if (rc != TQ_HIP_OK) return rc;
+    unsigned char *base = g_noalloc[dev].ptr;
+    const CallScratch sc{reinterpret_cast<float *>(base + kNoAllocCounterBytes),
+                         TQ_HIP_NOALLOC_SCRATCH_BYTES - kNoAllocCounterBytes, reinterpret_cast<int *>(base),
+                         kNoAllocCounterBytes / sizeof(int)};
+    return decode_common(kv, n_q, d_seq, d_pos, 1, 0, 1, 0, max_pos + 1, d_q, d_cos, d_sin, d_k, d_v, d_out,
+                         pick(kv, stream), (!d_seq && n_q == 1) ? 0 : -1, nullptr, nullptr, 0.0f, &sc);
 }
 
 int tq_hip_decode_step_norm_async(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d_pos,

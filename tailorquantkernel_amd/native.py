@@ -17,7 +17,7 @@ QK = 32
 PAGE_TOKENS = 16
 BLOCK_Q8 = np.dtype([("d", "<f4"), ("q", "i1", (QK,))])
 
-OK, EINVAL, ENOMEM, ETYPE, ENODEV, ENOTREADY = 0, -1, -2, -3, -4, -5
+OK, EINVAL, ENOMEM, ETYPE, ENODEV, ENOTREADY, ESCRATCH = 0, -1, -2, -3, -4, -5, -6
 EHIP_BASE = -1000
 
 _vp, _i, _f, _sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t
@@ -71,6 +71,7 @@ _PROTOS = {
     "tq_hip_prefill_async": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tq_hip_membw_sink_bytes": (_sz, []),
     "tq_hip_membw_read": (_i, [_vp, _sz, _vp, C.c_uint, _vp]),
+    "tq_hip_decode_step_noalloc": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tq_hip_decode_step_norm_async": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp,
                                           _vp, _vp]),
     "tq_hip_attention_layer_ws_bytes": (_sz, [_vp, _vp, _i]),
