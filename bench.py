@@ -1,35 +1,43 @@
-"""Q8 GQA decode benchmark on one MI355X.
+"""Q8 GQA attention benchmark on one MI355X.
 
-Workload (default, --config decode-8b-4k): Llama-3-8B-shaped attention, 32 q heads / 8 kv
-heads / head_dim 128, batch 1, context 4096.  One step = the attention core of
-one layer for one new token: RoPE (theta 5e5) on q and k, quantize and append
-the token's K/V into that layer's paged HBM cache, and attend over all 4096
-tokens — one call of tq_hip_decode_step_async.  Steps rotate over 32 layer
-caches (32 x 9.44 MB = 302 MB > the 256 MB MALL) so every step streams its KV
-from HBM.  The timed steps are replayed from a HIP graph of 32 steps; inputs
-are resident in HBM before the timed region.
+Default run (--config all): the five workloads of the attention path, one
+JSON line.  Its own fields are the headline, the Llama-3-8B-shaped batch-1
+decode at context 4096 (32 q / 8 kv heads, head_dim 128): one step = the
+attention core of one layer for one new token, RoPE (theta 5e5) on q and k,
+quantize and append the token's K/V into that layer's paged HBM cache,
+attend over all 4096 tokens — one tq_hip_decode_step_async launch.  Steps
+rotate over 32 layer caches (32 x 9.44 MB = 302 MB > the 256 MB MALL) so
+every step streams its KV from HBM, replayed from a HIP graph of 32 steps.
+value = tokens/s of one layer step; KV bytes per step = n_tokens * n_kv_heads
+* 2 * (head_dim/32) * 36 = 9,437,184 (the reference's KV accounting,
+tools/bench_forward.c:153-159).
 
-value = tokens/s of one layer step (batch / step time).  KV bytes per step =
-n_tokens * n_kv_heads * 2 * (head_dim/32) * 36 = 9,437,184 (the reference's KV
-accounting, tools/bench_forward.c:153-159).
+"workloads" holds the other four, each with its roofline, CPU baseline and
+parity on a sample:
+  C1  8 q / 2 kv heads, head_dim 64, context 256, theta 1e4, batch 1 (us);
+  C3  64 sequences, context U[512, 8192] (seed 2024), 16-token pages
+      scattered over the pool, 8B heads, fused step;
+  C5  64 q / 8 kv heads (a 70B layer), batch 16 x 32768, 1 % of K/V values at
+      +-8 sigma, fused step;
+  C4  causal prefill of 2048 tokens at the 8B heads (append + attention).
+Every workload times at least 100 launches with HIP events on its launch
+stream, inputs resident in HBM; a `rocprofv3 --selected-regions` run of this
+script traces exactly those timed regions (roctx markers).
 
-Cache contents are N(0,1) rows quantized and written by the library's own
-append kernel; RoPE tables come from the library's host side (libtqattn).
-The CPU baseline leg (default on; --no-cpu skips it) times the reference's
-own kernels (oracle/_ref, AVX2 dispatch, OpenMP over kv heads) on host copies
-of the same workload and checks the GPU output of layer 0 against them.
+CPU baselines time the reference's own kernels (oracle/_ref, AVX2 dispatch,
+OpenMP as the reference runs it) on this host on a bounded sample of the same
+workload, and their outputs check the GPU's: for the batched decodes both the
+reference's policy (a loop over sequences, OpenMP over kv heads) and a
+best-effort variant (the sequences in parallel).  --no-cpu skips them.
 
-Other workloads: --config decode-batched (64 sequences, ragged 512..8192,
-paged), decode-70b-32k (64q/8kv, batch 16, context 32768, 1 % outliers),
-prefill-2k (causal prefill of 2048 tokens), project-8b / project-70b (the Q8
-weight GEMVs either side of attention for one token: project_qkv and
-project_output, 32 layers' weights rotated), layer-8b (the whole
-attention_layer for one token at ctx 4096: projections, q/k RMSNorm, RoPE,
-append, attend), layer-prefill-8b (attention_layer_batch for 2048 tokens).
-They print the same JSON fields for their own shape.
-
---copy-calibration BYTES runs one device-to-device copy of BYTES first: its
-FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc give the counters' scale.
+Other single workloads (--config): decode-8b-4k, decode-c1, decode-batched,
+decode-70b-32k, prefill-2k (each of the above alone), project-8b /
+project-70b (the Q8 weight GEMVs either side of attention for one token),
+layer-8b (the whole attention_layer for one token at ctx 4096), layer-prefill-8b
+(attention_layer_batch for 2048 tokens), forward-8b / forward-8b-q4 (the
+whole model).  --copy-calibration BYTES runs one device-to-device copy of
+BYTES first: its FETCH_SIZE / WRITE_SIZE under rocprofv3 --pmc give the
+counters' scale.
 """
 from __future__ import annotations
 
@@ -120,15 +128,52 @@ class Hip:
         self.ok(self.lib.hipGraphLaunch(ex, stream), "hipGraphLaunch")
 
 
+class Roctx:
+    """roctxProfilerResume / roctxProfilerPause: under `rocprofv3
+    --selected-regions` only what runs between them is traced, so a profile
+    of this script covers exactly its timed launches.  No-ops without the
+    library; without the profiler the calls do nothing."""
+
+    def __init__(self):
+        self.lib = None
+        for cand in ("librocprofiler-sdk-roctx.so.1", "/opt/rocm/lib/librocprofiler-sdk-roctx.so"):
+            try:
+                self.lib = C.CDLL(cand)
+                break
+            except OSError:
+                continue
+        if self.lib is not None:
+            for fn in ("roctxProfilerResume", "roctxProfilerPause"):
+                getattr(self.lib, fn).argtypes = [C.c_uint64]
+                getattr(self.lib, fn).restype = C.c_int
+
+    def resume(self):
+        if self.lib is not None:
+            self.lib.roctxProfilerResume(0)
+
+    def pause(self):
+        if self.lib is not None:
+            self.lib.roctxProfilerPause(0)
+
+
+ROCTX = Roctx()
+MIN_TIMED = 100   # timed launches per workload, whatever --steps asks
+
+
 def timed(hip, stream, n, fn):
-    """ms per call of fn() over n back-to-back calls, HIP events on `stream`."""
+    """ms per call of fn() over n back-to-back calls, HIP events on `stream`
+    (the timed region: the only one a `rocprofv3 --selected-regions` run of
+    this script traces)."""
     e0, e1 = hip.event(), hip.event()
     hip.sync()
+    ROCTX.resume()
     hip.record(e0, stream)
     for _ in range(n):
         fn()
     hip.record(e1, stream)
-    return hip.elapsed_ms(e0, e1) / n
+    ms = hip.elapsed_ms(e0, e1) / n
+    ROCTX.pause()
+    return ms
 
 
 # ---------------------------------------------------------------------------
@@ -211,20 +256,69 @@ def measured_traffic(name: str):
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the reference's kernels (oracle/_ref), AVX2 dispatch, OpenMP
-# over kv heads from 256 tokens on, as the reference runs them — and the
-# check of the GPU's layer-0 output against the same code.
+# CPU baselines: the reference's own kernels (oracle/_ref, AVX2 dispatch,
+# OpenMP as the reference runs them), timed on this host on a bounded sample
+# of the same workload; their outputs are also the parity check of the GPU's.
 
-def cpu_leg_decode_8b(nq, nkv, hd, T, theta, budget_s: float, check):
-    from oracle.binding import Oracle, Ref, ptr
+def host_info():
+    omp = int(os.environ.get("OMP_NUM_THREADS", str(os.cpu_count() or 1)))
+    try:
+        cpu_model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except Exception:
+        cpu_model = "unknown"
+    return omp, cpu_model
+
+
+def cpu_reference():
+    """The reference's AVX2 build (kind "reference"), or None where it was not built."""
+    from oracle.binding import Ref
+    if not Ref.available():
+        return None
+    ref = Ref()
+    L = ref.lib
+    vp, i, f = C.c_void_p, C.c_int, C.c_float
+    L.tqref_attention_batch.argtypes = [i, i, i, i, i, f, vp, vp, vp, vp, vp, vp, vp]
+    L.tqref_attention_batch.restype = i
+    L.tqref_prefill_core.argtypes = [i, i, i, i, f, vp, vp, i, i, vp, vp, vp, vp]
+    L.tqref_prefill_core.restype = i
+    return ref
+
+
+def time_cpu(fn, budget_s: float, min_reps: int = 3):
+    """Median seconds of fn() (which returns 0) over repetitions filling
+    budget_s, after one untimed call; (median, repetitions)."""
+    assert fn() == 0
+    times = []
+    t_start = time.perf_counter()
+    while (time.perf_counter() - t_start < budget_s and len(times) < 100000) or len(times) < min_reps:
+        t0 = time.perf_counter()
+        rc = fn()
+        times.append(time.perf_counter() - t0)
+        assert rc == 0, rc
+    return float(np.median(times)), len(times)
+
+
+def parity_of(got, ref, against):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    return {"ok": bool((err <= 1e-4 + 1e-3 * np.abs(ref)).all()), "max_abs_err": float(err.max()), "bar": TOL,
+            "against": against}
+
+
+def cpu_leg_attention(nq, nkv, hd, T, theta, budget_s: float, check):
+    """One sequence's attention core (RoPE + store_kv + attend_q8) at position
+    T-1 on the reference's kernels with attend_q8's OpenMP policy (over kv
+    heads from 256 tokens on); parity of the GPU's output on the GPU's own
+    cache content."""
+    from oracle.binding import Oracle, ptr
     oracle = Oracle()
-    kind = "reference" if Ref.available() else "port"
+    ref = cpu_reference()
+    kind = "reference" if ref else "port"
     scores = np.zeros(nq * T, np.float32)
     out = np.zeros(nq * hd, np.float32)
     pos = T - 1
-    if kind == "reference":
-        ref = Ref()
-
+    if ref:
         def fn(kc, vc, q, k, v):
             return ref.lib.tqref_attention_qkv(nq, nkv, hd, T, theta, ptr(kc), ptr(vc), pos, ptr(q), ptr(k),
                                                ptr(v), ptr(scores), ptr(out))
@@ -234,49 +328,111 @@ def cpu_leg_decode_8b(nq, nkv, hd, T, theta, budget_s: float, check):
             return oracle.lib.oracle_attention_qkv(ptr(kc), ptr(vc), nq, nkv, hd, T, theta, pos, ptr(q), ptr(k),
                                                    ptr(v), ptr(scores), ptr(out))
         isa = "scalar"
-
-    # check: the GPU's layer-0 output against the same computation on the
-    # GPU's cache content (downloaded), same q/k/v
     kc0, vc0, q, k, v, got = check
-    rc = fn(kc0.copy(), vc0.copy(), q.copy(), k.copy(), v.copy())
-    ref_out = out.astype(np.float64).copy()
-    err = np.abs(got.astype(np.float64) - ref_out)
-    parity = {"ok": bool(rc == 0 and (err <= 1e-4 + 1e-3 * np.abs(ref_out)).all()),
-              "max_abs_err": float(err.max()), "bar": TOL, "against": f"{kind} ({isa}) on layer 0"}
-
-    # timing: 8 host layer caches (75 MB, beyond the L3), rotated
+    assert fn(kc0.copy(), vc0.copy(), q.copy(), k.copy(), v.copy()) == 0
+    parity = parity_of(got, out, f"{kind} ({isa}), same cache and inputs")
+    # timing: 8 host caches rotated (beyond the host's last-level cache at 8B)
     layers = 8
     rng = np.random.default_rng(1)
-    caches = []
-    for _ in range(layers):
-        kc = oracle.quantize_row_q8(rng.standard_normal(nkv * T * hd, dtype=np.float32))
-        vc = oracle.quantize_row_q8(rng.standard_normal(nkv * T * hd, dtype=np.float32))
-        caches.append((kc, vc))
-    for l in range(2):
-        fn(caches[l][0], caches[l][1], q.copy(), k.copy(), v)
-    times = []
-    t_start = time.perf_counter()
-    i = 0
-    while (time.perf_counter() - t_start < budget_s and i < 100000) or i < 5:
-        kc, vc = caches[i % layers]
-        qi, ki = q.copy(), k.copy()
-        t0 = time.perf_counter()
-        rc = fn(kc, vc, qi, ki, v)
-        times.append(time.perf_counter() - t0)
-        assert rc == 0
-        i += 1
-    med = float(np.median(times))
-    omp = int(os.environ.get("OMP_NUM_THREADS", str(os.cpu_count() or 1)))
-    cores = min(nkv, omp, os.cpu_count() or 1) if kind == "reference" else 1
-    try:
-        cpu_model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
-    except Exception:
-        cpu_model = "unknown"
-    baseline = {"value": 1.0 / med, "unit": "tokens/s", "cores": cores, "kind": kind,
-                "sample": (f"{len(times)} single-token layer steps (RoPE+store_kv+attend_q8, ctx {T}, "
-                           f"{nq}q/{nkv}kv/hd{hd}) rotating {layers} host caches, median of {med * 1e3:.3f} ms; "
-                           f"{isa} kernels, OpenMP over kv heads (OMP_NUM_THREADS={omp}, "
-                           f"nproc={os.cpu_count()}, {cpu_model})")}
+    caches = [(oracle.quantize_row_q8(rng.standard_normal(nkv * T * hd, dtype=np.float32)),
+               oracle.quantize_row_q8(rng.standard_normal(nkv * T * hd, dtype=np.float32))) for _ in range(layers)]
+    it = [0]
+
+    def step():
+        kc, vc = caches[it[0] % layers]
+        it[0] += 1
+        return fn(kc, vc, q.copy(), k.copy(), v)
+    med, reps = time_cpu(step, budget_s)
+    omp, cpu_model = host_info()
+    cores = min(nkv, omp, os.cpu_count() or 1) if (kind == "reference" and T >= 256) else 1
+    baseline = {"value": 1.0 / med, "unit": "tokens/s", "cores": cores, "kind": kind, "ms_per_step": med * 1e3,
+                "sample": (f"{reps} single-token steps (RoPE + store_kv + attend_q8, ctx {T}, {nq}q/{nkv}kv/hd{hd}) "
+                           f"rotating {layers} host caches, median {med * 1e3:.3f} ms; {isa} kernels, OpenMP over "
+                           f"kv heads from 256 tokens on (OMP_NUM_THREADS={omp}, nproc={os.cpu_count()}, "
+                           f"{cpu_model})")}
+    return baseline, parity
+
+
+def host_host_info_line():
+    omp, cpu_model = host_info()
+    return f"OMP_NUM_THREADS={omp}, nproc={os.cpu_count()}, {cpu_model}"
+
+
+def cpu_leg_batched(host, budget_s: float):
+    """The batched decode on the reference's kernels: every sequence's
+    attention core on its own flat cache, (a) the reference's policy — a loop
+    over sequences, attend_q8's OpenMP over kv heads inside — and (b) best
+    effort — the sequences in parallel.  Parity: sampled sequences' GPU rows
+    against (a)."""
+    from oracle.binding import ptr
+    ref = cpu_reference()
+    if ref is None:
+        return None, None, {"ok": None, "against": "oracle/_ref not built"}
+    nq, nkv, hd, theta = host["nq"], host["nkv"], host["hd"], host["theta"]
+    lens, kpat, vpat = host["lens"], host["kpat"], host["vpat"]
+    pat = kpat.shape[1]
+    nseq = lens.size
+    kcs, vcs = [], []
+    for L in lens:
+        L = int(L)
+        reps = (L + pat - 1) // pat
+        kcs.append(np.ascontiguousarray(np.tile(kpat, (1, reps, 1))[:, :L]))
+        vcs.append(np.ascontiguousarray(np.tile(vpat, (1, reps, 1))[:, :L]))
+    karr = (C.c_void_p * nseq)(*[ptr(c) for c in kcs])
+    varr = (C.c_void_p * nseq)(*[ptr(c) for c in vcs])
+    lens32 = np.ascontiguousarray(lens, np.int32)
+    q, k, v = host["q"], host["k"], host["v"]
+    out = np.zeros((nseq, nq * hd), np.float32)
+
+    def run(policy):
+        return ref.lib.tqref_attention_batch(policy, nseq, nq, nkv, hd, theta, ptr(lens32), karr, varr, ptr(q),
+                                             ptr(k), ptr(v), ptr(out))
+    assert run(0) == 0
+    sample = sorted({int(np.argmax(lens)), int(np.argmin(lens)), 0, nseq - 1})
+    parity = parity_of(host["gpu_out"][sample], out[sample],
+                       f"reference ({ref.isa()}) on the same caches and inputs, sequences {sample}")
+    omp, _ = host_info()
+    kv_bytes = int(lens.sum()) * nkv * 2 * (hd // QK) * BLOCK_BYTES
+    legs = []
+    for policy, label, cores in ((0, "reference-policy: a loop over the sequences, attend_q8's OpenMP over kv "
+                                     "heads inside", min(nkv, omp)),
+                                 (1, "best-effort: the sequences in parallel (OpenMP over sequences, each "
+                                     "single-threaded)", min(nseq, omp))):
+        med, reps = time_cpu(lambda: run(policy), budget_s, min_reps=2)
+        legs.append({"value": nseq / med, "unit": "tokens/s", "cores": cores, "kind": "reference",
+                     "ms_per_step": med * 1e3, "kv_gbps": kv_bytes / med / 1e9, "variant": label,
+                     "sample": (f"{reps} whole batch steps ({nseq} sequences, RoPE + store_kv + attend_q8 each), "
+                                f"median {med * 1e3:.1f} ms; {ref.isa()} kernels ({host_host_info_line()})")})
+    return legs[0], legs[1], parity
+
+
+def cpu_leg_prefill(host, budget_s: float):
+    """attention_layer_batch's attention loop on the reference's kernels: per
+    token store_kv + attend over [0, pos] (attend_q8's OpenMP over kv heads
+    from 256 tokens on).  Parity: sampled token rows of the GPU's output."""
+    from oracle.binding import blocks, ptr
+    ref = cpu_reference()
+    if ref is None:
+        return None, {"ok": None, "against": "oracle/_ref not built"}
+    nq, nkv, hd, n, theta = host["nq"], host["nkv"], host["hd"], host["n"], host["theta"]
+    nb = hd // QK
+    kc, vc = blocks(nkv * n * nb), blocks(nkv * n * nb)
+    q, k, v = host["q"], host["k"], host["v"]
+    out = np.zeros((n, nq * hd), np.float32)
+
+    def run():
+        return ref.lib.tqref_prefill_core(nq, nkv, hd, n, theta, ptr(kc), ptr(vc), 0, n, ptr(q), ptr(k), ptr(v),
+                                          ptr(out))
+    med, reps = time_cpu(run, budget_s, min_reps=1)
+    sample = [0, 1, 31, 511, 1024, 1500, n - 1]
+    parity = parity_of(host["gpu_out"][sample], out[sample],
+                       f"reference ({ref.isa()}) per-token loop, same inputs, tokens {sample}")
+    omp, _ = host_info()
+    baseline = {"value": n / med, "unit": "tokens/s", "cores": min(nkv, omp), "kind": "reference",
+                "ms_per_step": med * 1e3,
+                "sample": (f"{reps} whole prefills of {n} tokens (the per-token store_kv + attend loop of "
+                           f"attention_layer_batch), median {med * 1e3:.0f} ms; {ref.isa()} kernels, OpenMP over kv "
+                           f"heads from 256 tokens on ({host_host_info_line()})")}
     return baseline, parity
 
 
@@ -302,16 +458,17 @@ def host_boundary_us(nq, nkv, hd, T, theta, q, k, v, calls=200):
 
 
 # ---------------------------------------------------------------------------
-# batch-1 decode at the 8B shape, context 4096
+# single-sequence decode: the 8B shape at context 4096 (the headline), and
+# the small reference test shape at context 256
 
-def bench_decode_8b(args, nat, hip):
-    nq, nkv, hd, T, theta = 32, 8, 128, 4096, 500000.0
+def bench_decode_single(args, nat, hip, *, nq, nkv, hd, T, theta, layers, seed, boundary):
+    """One fused step per layer cache (RoPE + append + attend at position
+    T-1), `layers` caches rotated in a HIP graph of `layers` launches, at
+    least MIN_TIMED launches timed.  Returns (timing dict, check tuple)."""
     nb = hd // QK
-    layers = args.layers
     kv_bytes = T * nkv * 2 * nb * BLOCK_BYTES
     lib = nat.load()
-    rng = np.random.default_rng(3)
-
+    rng = np.random.default_rng(seed)
     kvs = [nat.PagedKV.single(nq, nkv, hd, T) for _ in range(layers)]
     stream = kvs[0].stream
     D = nat.DeviceBuffer.from_numpy
@@ -321,7 +478,6 @@ def bench_decode_8b(args, nat, hip):
         fill_sequence(nat, kv, 0, T, dk_rows, dv_rows, T, kv.stream)
     dk_rows.free()
     dv_rows.free()
-
     pos = T - 1
     q = rng.standard_normal(nq * hd, dtype=np.float32)
     k = rng.standard_normal(nkv * hd, dtype=np.float32)
@@ -341,33 +497,39 @@ def bench_decode_8b(args, nat, hip):
     hip.sync()
     got = outs[0].download((nq * hd,), np.float32)
     kc0, vc0 = kvs[0].read(0, 0, T)
+    boundary_us = host_boundary_us(nq, nkv, hd, T, theta, q, k, v) if boundary else None
 
     graph, _ = hip.capture(stream, lambda: [step(l) for l in range(layers)])
     for _ in range(2):
         hip.launch_graph(graph, stream)
     hip.sync()
     replay_same = outs[0].download((nq * hd,), np.float32).tobytes() == got.tobytes()
-
-    reps = max(1, args.steps // layers)
-    steps = reps * layers
+    reps = max(-(-MIN_TIMED // layers), args.steps // layers)
     t0 = time.perf_counter()
     ms_per_step = timed(hip, stream, reps, lambda: hip.launch_graph(graph, stream)) / layers
-    hip.sync()
     wall = time.perf_counter() - t0
-    # one kernel launch per step, so the step time over the timed region is
-    # the kernel's average launch duration (including back-to-back gaps)
-    achieved = kv_bytes / (ms_per_step * 1e-3) / 1e9
-    traffic = measured_traffic("decode_8b_ctx4096_b1_pmc.txt")
-    boundary_us = host_boundary_us(nq, nkv, hd, T, theta, q, k, v)
+    for kv in kvs:
+        kv.close()
+    res = {"ms_per_step": ms_per_step, "steps": reps * layers, "wall_s": wall, "kv_bytes": kv_bytes,
+           "graph_replay_equals_eager": replay_same, "boundary_us": boundary_us}
+    return res, (kc0.reshape(-1), vc0.reshape(-1), q, k, v, got)
 
+
+def bench_decode_8b(args, nat, hip):
+    nq, nkv, hd, T, theta = 32, 8, 128, 4096, 500000.0
+    layers = args.layers
+    r, check = bench_decode_single(args, nat, hip, nq=nq, nkv=nkv, hd=hd, T=T, theta=theta, layers=layers, seed=3,
+                                   boundary=True)
+    kv_bytes, ms = r["kv_bytes"], r["ms_per_step"]
+    achieved = kv_bytes / (ms * 1e-3) / 1e9
     line = {
         "metric": METRIC,
-        "value": 1e3 / ms_per_step,
+        "value": 1e3 / ms,
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": steps,
+        "steps": r["steps"],
         "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -379,17 +541,37 @@ def bench_decode_8b(args, nat, hip):
                    "batch": 1, "context": T, "n_q_heads": nq, "n_kv_heads": nkv, "head_dim": hd,
                    "kv_bytes_per_step": kv_bytes, "layers_rotated": layers},
         "kv_gbps": achieved,
-        "tokens_per_s_32_layers": 1e3 / ms_per_step / 32,
-        "wall_s": wall,
-        "graph_replay_equals_eager": replay_same,
-        "host_boundary_us_per_call": boundary_us,
+        "tokens_per_s_32_layers": 1e3 / ms / 32,
+        "wall_s": r["wall_s"],
+        "graph_replay_equals_eager": r["graph_replay_equals_eager"],
+        "host_boundary_us_per_call": r["boundary_us"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic("decode_8b_ctx4096_b1_pmc.txt"),
                      "kernel": "decode3_kernel<128, 4, 4> (fused RoPE + append + split-K attend + combine)",
-                     "kernel_ms": ms_per_step, "algorithmic_bytes": kv_bytes},
+                     "kernel_ms": ms, "algorithmic_bytes": kv_bytes},
     }
-    check = (kc0.reshape(-1), vc0.reshape(-1), q, k, v, got)
     return line, check
+
+
+def bench_decode_c1(args, nat, hip):
+    """The reference's small test shape: 8 q / 2 kv heads, head_dim 64,
+    context 256, theta 1e4, batch 1 — a latency-bound step (73,728 KV bytes)."""
+    nq, nkv, hd, T, theta = 8, 2, 64, 256, 10000.0
+    r, check = bench_decode_single(args, nat, hip, nq=nq, nkv=nkv, hd=hd, T=T, theta=theta, layers=32, seed=4,
+                                   boundary=False)
+    kv_bytes, ms = r["kv_bytes"], r["ms_per_step"]
+    achieved = kv_bytes / (ms * 1e-3) / 1e9
+    res = {"metric": "Q8 GQA decode step latency, 8q/2kv/hd64, context 256, batch 1, 1 GPU", "value": ms * 1e3,
+           "unit": "us", "higher_is_better": False, "ms_per_step": ms, "steps": r["steps"],
+           "tokens_per_s": 1e3 / ms,
+           "config": {"workload": ("Q8 GQA decode, 8q/2kv/hd64, batch 1, context 256, fused RoPE(theta 1e4) + KV "
+                                   "append + attend, 32 caches in a HIP graph of 32 steps"),
+                      "batch": 1, "context": T, "kv_bytes_per_step": kv_bytes},
+           "graph_replay_equals_eager": r["graph_replay_equals_eager"],
+           "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": achieved / HBM_PEAK_GBS, "traffic": None, "latency_bound": True,
+                        "kernel": "decode3_kernel<64, 4, 4>", "kernel_ms": ms, "algorithmic_bytes": kv_bytes}}
+    return res, check
 
 
 # ---------------------------------------------------------------------------
@@ -413,8 +595,9 @@ def bench_batched(args, nat, hip, *, nq, nkv, hd, lens, theta, outliers, workloa
     stream = kv.stream
     D = nat.DeviceBuffer.from_numpy
     pat = 8192
-    dk_rows = D(normal_rows(rng, pat, nkv * hd, outliers))
-    dv_rows = D(normal_rows(rng, pat, nkv * hd, outliers))
+    krows = normal_rows(rng, pat, nkv * hd, outliers)
+    vrows = normal_rows(rng, pat, nkv * hd, outliers)
+    dk_rows, dv_rows = D(krows), D(vrows)
     for i in range(nseq):
         fill_sequence(nat, kv, i, int(lens[i]), dk_rows, dv_rows, pat, stream)
     dk_rows.free()
@@ -444,31 +627,48 @@ def bench_batched(args, nat, hip, *, nq, nkv, hd, lens, theta, outliers, workloa
     hip.sync()
     repeat_same = out.download((nseq, nq * hd), np.float32).tobytes() == first.tobytes()
 
-    steps = max(4, args.steps // 64)
+    steps = max(MIN_TIMED, args.steps)
     t0 = time.perf_counter()
     ms = timed(hip, stream, steps, step)
-    hip.sync()
     wall = time.perf_counter() - t0
+    kv.close()
     gbs = kv_bytes / (ms * 1e-3) / 1e9
-    return {
-        "metric": metric, "value": nseq * 1e3 / ms, "unit": "tokens/s", "n_gpus": 1, "steps": steps,
-        "warmup": warm, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+    res = {
+        "metric": metric, "value": nseq * 1e3 / ms, "unit": "tokens/s", "higher_is_better": True,
+        "ms_per_step": ms, "steps": steps, "warmup": warm,
         "config": {"workload": workload, "batch": nseq, "n_q_heads": nq, "n_kv_heads": nkv, "head_dim": hd,
                    "context_sum": int(lens.sum()), "context_max": int(lens.max()), "kv_bytes_per_step": kv_bytes,
                    "pool_mb": total * page_bytes / 1e6},
         "kv_gbps": gbs, "wall_s": wall, "repeat_equals_first": repeat_same,
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": gbs / HBM_PEAK_GBS, "traffic": measured_traffic(profile),
-                     "kernel": f"decode3_kernel<{hd}, {nq // nkv}, 4>", "kernel_ms": ms, "algorithmic_bytes": kv_bytes},
+                     "kernel": f"decode3_kernel<{hd}, {nq // nkv}, 4>", "kernel_ms": ms,
+                     "algorithmic_bytes": kv_bytes},
     }
+    from oracle.binding import Oracle
+    oracle = Oracle()
+    host = {"nq": nq, "nkv": nkv, "hd": hd, "theta": theta, "lens": lens, "q": q, "k": k, "v": v, "gpu_out": first,
+            "kpat": quantize_heads(oracle, krows, nkv, hd), "vpat": quantize_heads(oracle, vrows, nkv, hd)}
+    return res, host
+
+
+def quantize_heads(oracle, rows, nkv, hd):
+    """rows [T][nkv*hd] fp32 -> the reference's flat cache layout [nkv][T][nb] (quantize_row_q8)."""
+    T = rows.shape[0]
+    per_head = np.ascontiguousarray(rows.reshape(T, nkv, hd).transpose(1, 0, 2))
+    return oracle.quantize_row_q8(per_head.reshape(-1)).reshape(nkv, T, hd // QK)
+
+
+C3_WORKLOAD = ("Q8 GQA batched decode, 64 sequences, context U[512,8192] (seed 2024), 16-token pages scattered "
+               "over the pool, 32q/8kv/hd128, fused RoPE + append + attend")
+C5_WORKLOAD = ("Q8 GQA long-context decode, 64q/8kv/hd128 (70B layer), batch 16, context 32768, 1% K/V outliers at "
+               "+-8 sigma, split-K, fused RoPE + append + attend")
 
 
 def bench_decode_batched(args, nat, hip):
     lens = np.random.default_rng(2024).integers(512, 8193, size=64).astype(np.int32)
     return bench_batched(args, nat, hip, nq=32, nkv=8, hd=128, lens=lens, theta=500000.0, outliers=0.0,
-                         workload="Q8 GQA batched decode, 64 sequences, context U[512,8192] (seeded), 16-token "
-                                  "pages scattered over the pool, 32q/8kv/hd128, fused RoPE + append + attend",
+                         workload=C3_WORKLOAD,
                          metric="Q8 GQA batched decode tokens/sec + achieved HBM GB/s (KV bytes), 1 GPU",
                          profile="decode_8b_batch64_ragged_pmc.txt")
 
@@ -476,8 +676,7 @@ def bench_decode_batched(args, nat, hip):
 def bench_decode_70b(args, nat, hip):
     lens = np.full(16, 32768, np.int32)
     return bench_batched(args, nat, hip, nq=64, nkv=8, hd=128, lens=lens, theta=500000.0, outliers=0.01,
-                         workload="Q8 GQA long-context decode, 64q/8kv/hd128 (70B layer), batch 16, context 32768, "
-                                  "1% K/V outliers at +-8 sigma, split-K, fused RoPE + append + attend",
+                         workload=C5_WORKLOAD,
                          metric="Q8 GQA long-context decode tokens/sec + achieved HBM GB/s (KV bytes), 1 GPU",
                          profile="decode_70b_ctx32768_b16_pmc.txt")
 
@@ -506,27 +705,29 @@ def bench_prefill_2k(args, nat, hip):
     step()
     hip.sync()
     first = out.download((n, nq * hd), np.float32)
-    steps = max(3, args.steps // 400)
+    steps = max(MIN_TIMED, args.steps // 4)
     ms = timed(hip, stream, steps, step)
-    hip.sync()
     repeat_same = out.download((n, nq * hd), np.float32).tobytes() == first.tobytes()
+    kv.close()
     useful_ops = 2.0 * nq * (n * (n + 1) / 2) * hd * 2      # Q.K^T and P.V over the causal triangle
     tflops = useful_ops / (ms * 1e-3) / 1e12
-    return {
+    res = {
         "metric": "Q8 GQA causal prefill tokens/sec + MFMA utilisation, 2048 tokens at 8B shape, 1 GPU",
-        "value": n * 1e3 / ms, "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": 1, "ms_per_step": ms,
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "value": n * 1e3 / ms, "unit": "tokens/s", "higher_is_better": True, "steps": steps, "warmup": 1,
+        "ms_per_step": ms, "dtype": "bf16",
         "config": {"workload": "Q8 GQA causal prefill, 2048 tokens, 32q/8kv/hd128, RoPE theta 5e5, KV append + "
                                "causal attention", "tokens": n, "useful_ops": useful_ops},
         "repeat_equals_first": repeat_same,
-        # bf16 MFMA (dense 2.5 PFLOP/s) runs each product as hi.hi + hi.lo + lo.hi:
-        # executed flops are three times the useful ones
+        # Q.K^T: one bf16 product per block over the int8 codes (exact dots);
+        # P.V: three (V' hi.P hi + hi.lo + lo.hi): executed = 2 x useful
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s",
-                     "frac": tflops / 2500.0, "executed_tflops": 3 * tflops,
+                     "frac": tflops / 2500.0, "executed_tflops": 2 * tflops,
                      "traffic": measured_traffic("prefill_8b_2048_pmc.txt"),
                      "kernel": "append_kernel + prefill_stage_kernel<128> + prefill_kernel<128, 4, 2> (one step)",
                      "kernel_ms": ms},
     }
+    host = {"nq": nq, "nkv": nkv, "hd": hd, "n": n, "theta": theta, "q": q, "k": k, "v": v, "gpu_out": first}
+    return res, host
 
 
 # ---------------------------------------------------------------------------
@@ -1283,16 +1484,48 @@ def cpu_leg_forward(host, embed, final_norm, shape, budget_s: float, fmt: int = 
                        f"{time.perf_counter() - t_start:.0f} s of sampling")}
 
 
+def run_all(args, nat, hip):
+    """The headline (8B decode at context 4096) as the line's own fields, the
+    other four workloads as sub-objects, each with its roofline, the
+    reference's kernels timed on this host beside it, and parity on a sample."""
+    line, check = bench_decode_8b(args, nat, hip)
+    if not args.no_cpu:
+        line["cpu_baseline"], line["parity"] = cpu_leg_attention(32, 8, 128, 4096, 500000.0, args.cpu_budget, check)
+    work = {}
+
+    c1, check1 = bench_decode_c1(args, nat, hip)
+    if not args.no_cpu:
+        c1["cpu_baseline"], c1["parity"] = cpu_leg_attention(8, 2, 64, 256, 10000.0, args.cpu_budget / 2, check1)
+    work["C1_decode_8q2kv_hd64_ctx256"] = c1
+
+    for key, fn in (("C3_decode_batch64_ragged", bench_decode_batched),
+                    ("C5_decode_70b_b16_ctx32768", bench_decode_70b)):
+        res, host = fn(args, nat, hip)
+        if not args.no_cpu:
+            res["cpu_baseline"], res["cpu_baseline_best_effort"], res["parity"] = cpu_leg_batched(host,
+                                                                                                 args.cpu_budget / 2)
+        del host
+        work[key] = res
+
+    c4, host4 = bench_prefill_2k(args, nat, hip)
+    if not args.no_cpu:
+        c4["cpu_baseline"], c4["parity"] = cpu_leg_prefill(host4, args.cpu_budget)
+    work["C4_prefill_2048"] = c4
+    line["workloads"] = work
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=3200)
+    ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--config", default="decode-8b-4k",
-                    choices=["decode-8b-4k", "decode-batched", "prefill-2k", "decode-70b-32k", "project-8b",
-                             "project-70b", "layer-8b", "layer-prefill-8b", "forward-8b", "forward-8b-q4"])
+    ap.add_argument("--config", default="all",
+                    choices=["all", "decode-8b-4k", "decode-c1", "decode-batched", "prefill-2k", "decode-70b-32k",
+                             "project-8b", "project-70b", "layer-8b", "layer-prefill-8b", "forward-8b",
+                             "forward-8b-q4"])
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline sampling")
+    ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds of CPU baseline sampling per leg")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
     args = ap.parse_args()
@@ -1306,24 +1539,39 @@ def main():
     hip = Hip()
     if args.copy_calibration > 0:
         copy_calibration(nat, hip, args.copy_calibration)
-    if args.config == "decode-8b-4k":
+    if args.config == "all":
+        line = run_all(args, nat, hip)
+    elif args.config == "decode-8b-4k":
         line, check = bench_decode_8b(args, nat, hip)
         if not args.no_cpu:
-            baseline, parity = cpu_leg_decode_8b(32, 8, 128, 4096, 500000.0, args.cpu_budget, check)
-            line["cpu_baseline"] = baseline
-            line["parity"] = parity
+            line["cpu_baseline"], line["parity"] = cpu_leg_attention(32, 8, 128, 4096, 500000.0, args.cpu_budget,
+                                                                     check)
+    elif args.config == "decode-c1":
+        line, check = bench_decode_c1(args, nat, hip)
+        if not args.no_cpu:
+            line["cpu_baseline"], line["parity"] = cpu_leg_attention(8, 2, 64, 256, 10000.0, args.cpu_budget, check)
+    elif args.config in ("decode-batched", "decode-70b-32k"):
+        line, host = (bench_decode_batched if args.config == "decode-batched" else bench_decode_70b)(args, nat, hip)
+        if not args.no_cpu:
+            line["cpu_baseline"], line["cpu_baseline_best_effort"], line["parity"] = cpu_leg_batched(
+                host, args.cpu_budget)
+    elif args.config == "prefill-2k":
+        line, host = bench_prefill_2k(args, nat, hip)
+        if not args.no_cpu:
+            line["cpu_baseline"], line["parity"] = cpu_leg_prefill(host, args.cpu_budget)
     else:
-        line = {"decode-batched": bench_decode_batched, "prefill-2k": bench_prefill_2k,
-                "decode-70b-32k": bench_decode_70b, "project-8b": bench_project_8b,
-                "project-70b": bench_project_70b, "layer-8b": bench_layer_8b,
-                "layer-prefill-8b": bench_layer_prefill_8b,
-                "forward-8b": bench_forward_8b,
+        line = {"project-8b": bench_project_8b, "project-70b": bench_project_70b, "layer-8b": bench_layer_8b,
+                "layer-prefill-8b": bench_layer_prefill_8b, "forward-8b": bench_forward_8b,
                 "forward-8b-q4": lambda a, n, h: bench_forward_8b(a, n, h, fmt="q4")}[args.config](args, nat, hip)
-    if args.config.startswith(("decode", "project", "forward")) or args.config == "layer-8b":
+    if args.config in ("all", "decode-8b-4k", "decode-batched", "decode-70b-32k") or \
+            args.config.startswith(("project", "forward")) or args.config == "layer-8b":
         # the achievable read rate of this box, beside the 8 TB/s spec peak
         peak = measure_hbm_read(nat, hip)
-        line["roofline"]["measured_peak"] = peak
-        line["roofline"]["frac_of_measured"] = line["roofline"]["achieved"] / peak
+        rooflines = [line["roofline"]] + [w["roofline"] for w in line.get("workloads", {}).values()
+                                          if w["roofline"]["unit"] == "GB/s"]
+        for r in rooflines:
+            r["measured_peak"] = peak
+            r["frac_of_measured"] = r["achieved"] / peak
     print(json.dumps(line), flush=True)
 
 

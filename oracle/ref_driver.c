@@ -27,6 +27,7 @@
  * tq_forward_token through the edited context.c's device-model branch.
  */
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -277,6 +278,65 @@ int tqref_attention_qkv(int nq, int nkv, int hd, int max_tokens, float theta,
                       out + (size_t)kvh * group * hd, (size_t)hd);
     }
     return 0;
+}
+
+/* A batch of independent sequences, each one attention core (RoPE, store_kv
+ * of its new token at lens[s]-1, attend over [0, lens[s])) on its own flat
+ * cache kc[s] / vc[s] of lens[s] positions.  The reference has no batch API:
+ * policy 0 loops over the sequences, each call with attend_q8's own OpenMP
+ * over kv heads (the reference's policy); policy 1 runs the sequences in
+ * parallel (OpenMP over sequences, each single-threaded).  q [nseq][nq*hd],
+ * k, v [nseq][nkv*hd] (k, q pre-RoPE; copied, not modified); out
+ * [nseq][nq*hd].  Returns the first nonzero code. */
+int tqref_attention_batch(int policy, int nseq, int nq, int nkv, int hd, float theta, const int *lens,
+                          block_q8 *const *kc, block_q8 *const *vc, const float *q, const float *k,
+                          const float *v, float *out) {
+    int rc = 0;
+    const int levels = omp_get_max_active_levels();
+    if (policy == 1) omp_set_max_active_levels(1);   /* each sequence's attend_q8 on one thread */
+#pragma omp parallel for schedule(dynamic, 1) if (policy == 1) reduction(min : rc)
+    for (int s = 0; s < nseq; s++) {
+        const int L = lens[s];
+        float *qs = malloc((size_t)nq * hd * sizeof(float));
+        float *ks = malloc((size_t)nkv * hd * sizeof(float));
+        float *sc = malloc((size_t)nq * L * sizeof(float));
+        int r = -100;
+        if (qs && ks && sc) {
+            memcpy(qs, q + (size_t)s * nq * hd, (size_t)nq * hd * sizeof(float));
+            memcpy(ks, k + (size_t)s * nkv * hd, (size_t)nkv * hd * sizeof(float));
+            r = tqref_attention_qkv(nq, nkv, hd, L, theta, kc[s], vc[s], L - 1, qs, ks, v + (size_t)s * nkv * hd, sc,
+                                    out + (size_t)s * nq * hd);
+        }
+        free(qs);
+        free(ks);
+        free(sc);
+        if (r < rc) rc = r;
+    }
+    omp_set_max_active_levels(levels);
+    return rc;
+}
+
+/* The attention loop of attention_layer_batch (model/attention_layer.c:
+ * 221-236) for tokens pos0 .. pos0+n-1 of one flat cache: for each token,
+ * the attention core (RoPE, store_kv, attend over [0, pos]) with attend_q8's
+ * OpenMP over kv heads.  q [n][nq*hd], k, v [n][nkv*hd] (post-norm, pre-RoPE;
+ * copied, not modified); out [n][nq*hd]. */
+int tqref_prefill_core(int nq, int nkv, int hd, int max_tokens, float theta, block_q8 *kc, block_q8 *vc, int pos0,
+                       int n, const float *q, const float *k, const float *v, float *out) {
+    float *qs = malloc((size_t)nq * hd * sizeof(float));
+    float *ks = malloc((size_t)nkv * hd * sizeof(float));
+    float *sc = malloc((size_t)nq * max_tokens * sizeof(float));
+    int rc = (qs && ks && sc) ? 0 : -100;
+    for (int i = 0; rc == 0 && i < n; i++) {
+        memcpy(qs, q + (size_t)i * nq * hd, (size_t)nq * hd * sizeof(float));
+        memcpy(ks, k + (size_t)i * nkv * hd, (size_t)nkv * hd * sizeof(float));
+        rc = tqref_attention_qkv(nq, nkv, hd, max_tokens, theta, kc, vc, pos0 + i, qs, ks, v + (size_t)i * nkv * hd,
+                                 sc, out + (size_t)i * nq * hd);
+    }
+    free(qs);
+    free(ks);
+    free(sc);
+    return rc;
 }
 
 /* The reference's own mlp_layer (model/mlp.c:3-17) on Q8 matrices. */
