@@ -21,8 +21,9 @@ parity on a sample:
       +-8 sigma, fused step;
   C4  causal prefill of 2048 tokens at the 8B heads (append + attention).
 Every workload times at least 100 launches with HIP events on its launch
-stream, inputs resident in HBM; a `rocprofv3 --selected-regions` run of this
-script traces exactly those timed regions (roctx markers).
+stream, inputs resident in HBM.  Profiles of a single workload are taken with
+--no-cpu --steps 3200 --warmup 1 (and --no-boundary for the headline), so
+that the timed launches are all but ~1 % of the kernel's dispatches.
 
 CPU baselines time the reference's own kernels (oracle/_ref, AVX2 dispatch,
 OpenMP as the reference runs it) on this host on a bounded sample of the same
@@ -128,52 +129,18 @@ class Hip:
         self.ok(self.lib.hipGraphLaunch(ex, stream), "hipGraphLaunch")
 
 
-class Roctx:
-    """roctxProfilerResume / roctxProfilerPause: under `rocprofv3
-    --selected-regions` only what runs between them is traced, so a profile
-    of this script covers exactly its timed launches.  No-ops without the
-    library; without the profiler the calls do nothing."""
-
-    def __init__(self):
-        self.lib = None
-        for cand in ("librocprofiler-sdk-roctx.so.1", "/opt/rocm/lib/librocprofiler-sdk-roctx.so"):
-            try:
-                self.lib = C.CDLL(cand)
-                break
-            except OSError:
-                continue
-        if self.lib is not None:
-            for fn in ("roctxProfilerResume", "roctxProfilerPause"):
-                getattr(self.lib, fn).argtypes = [C.c_uint64]
-                getattr(self.lib, fn).restype = C.c_int
-
-    def resume(self):
-        if self.lib is not None:
-            self.lib.roctxProfilerResume(0)
-
-    def pause(self):
-        if self.lib is not None:
-            self.lib.roctxProfilerPause(0)
-
-
-ROCTX = Roctx()
 MIN_TIMED = 100   # timed launches per workload, whatever --steps asks
 
 
 def timed(hip, stream, n, fn):
-    """ms per call of fn() over n back-to-back calls, HIP events on `stream`
-    (the timed region: the only one a `rocprofv3 --selected-regions` run of
-    this script traces)."""
+    """ms per call of fn() over n back-to-back calls, HIP events on `stream`."""
     e0, e1 = hip.event(), hip.event()
     hip.sync()
-    ROCTX.resume()
     hip.record(e0, stream)
     for _ in range(n):
         fn()
     hip.record(e1, stream)
-    ms = hip.elapsed_ms(e0, e1) / n
-    ROCTX.pause()
-    return ms
+    return hip.elapsed_ms(e0, e1) / n
 
 
 # ---------------------------------------------------------------------------
@@ -497,7 +464,7 @@ def bench_decode_single(args, nat, hip, *, nq, nkv, hd, T, theta, layers, seed, 
     hip.sync()
     got = outs[0].download((nq * hd,), np.float32)
     kc0, vc0 = kvs[0].read(0, 0, T)
-    boundary_us = host_boundary_us(nq, nkv, hd, T, theta, q, k, v) if boundary else None
+    boundary_us = host_boundary_us(nq, nkv, hd, T, theta, q, k, v) if (boundary and not args.no_boundary) else None
 
     graph, _ = hip.capture(stream, lambda: [step(l) for l in range(layers)])
     for _ in range(2):
@@ -508,11 +475,47 @@ def bench_decode_single(args, nat, hip, *, nq, nkv, hd, T, theta, layers, seed, 
     t0 = time.perf_counter()
     ms_per_step = timed(hip, stream, reps, lambda: hip.launch_graph(graph, stream)) / layers
     wall = time.perf_counter() - t0
+    floor = step_floor(nat, hip, stream, [kv.pool()[0] for kv in kvs], kv_bytes, nkv, reps) if boundary else None
     for kv in kvs:
         kv.close()
     res = {"ms_per_step": ms_per_step, "steps": reps * layers, "wall_s": wall, "kv_bytes": kv_bytes,
-           "graph_replay_equals_eager": replay_same, "boundary_us": boundary_us}
+           "graph_replay_equals_eager": replay_same, "boundary_us": boundary_us, "floor": floor}
     return res, (kc0.reshape(-1), vc0.reshape(-1), q, k, v, got)
+
+
+def step_floor(nat, hip, stream, bufs, nbytes, n_heads, reps, n_splits=32):
+    """The floor of this step's shape on this GPU, measured the same way (a
+    HIP graph of one launch per layer buffer, the same buffers): the launch
+    alone, the read of the layer's KV bytes by n_heads x n_splits work-groups,
+    and that read plus the split-K combine chain with no attention math
+    (tq_hip_floor_step)."""
+    lib = nat.load()
+    scratch = nat.DeviceBuffer(lib.tq_hip_floor_scratch_bytes(n_heads, n_splits))
+    zeros = np.zeros(n_heads * 64, np.int32)   # held until the copy has read it
+    nat.check(lib.tq_hip_memcpy_h2d(scratch.ptr, zeros.ctypes.data, zeros.nbytes, None), "zero counters")
+    out = nat.DeviceBuffer(lib.tq_hip_floor_out_bytes(n_heads, n_splits))
+    res = {}
+    for mode, key in ((0, "launch_us"), (1, "read_us"), (2, "read_combine_us")):
+        def one(b):
+            nat.check(lib.tq_hip_floor_step(b, nbytes, n_heads, n_splits, mode, scratch.ptr, out.ptr, stream), "floor")
+        for b in bufs:
+            one(b)
+        hip.sync()
+        graph, _ = hip.capture(stream, lambda: [one(b) for b in bufs])
+        hip.launch_graph(graph, stream)
+        hip.sync()
+        res[key] = timed(hip, stream, reps, lambda: hip.launch_graph(graph, stream)) / len(bufs) * 1e3
+    sums = out.download((n_heads, 520), np.float32)
+    want = float(n_splits * (n_splits - 1) // 2)
+    res["combine_checked"] = bool(np.all(sums == want))
+    res["read_gbps"] = nbytes / (res["read_us"] * 1e-6) / 1e9
+    res["note"] = (f"{n_heads} x {n_splits} work-groups of 256 threads, one graph launch per layer buffer as the "
+                   "step is run: launch = an empty kernel, read = each work-group streams its chunk, "
+                   "read_combine = + one 520-float partial per work-group, an arrival counter per head, the "
+                   "last work-group pulls and sums the head's rows (tq_hip_floor_step)")
+    scratch.free()
+    out.free()
+    return res
 
 
 def bench_decode_8b(args, nat, hip):
@@ -545,6 +548,7 @@ def bench_decode_8b(args, nat, hip):
         "wall_s": r["wall_s"],
         "graph_replay_equals_eager": r["graph_replay_equals_eager"],
         "host_boundary_us_per_call": r["boundary_us"],
+        "step_floor": r["floor"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic("decode_8b_ctx4096_b1_pmc.txt"),
                      "kernel": "decode3_kernel<128, 4, 4> (fused RoPE + append + split-K attend + combine)",
@@ -1527,6 +1531,7 @@ def main():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds of CPU baseline sampling per leg")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-boundary", action="store_true", help="skip the synchronous-boundary timing (profiles)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
     args = ap.parse_args()
     if args.gpus != 1:

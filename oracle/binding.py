@@ -120,7 +120,8 @@ class Oracle:
 
     def rope_apply(self, x, cos_t, sin_t) -> np.ndarray:
         x = f32(x).copy()
-        self.lib.oracle_rope_apply(ptr(x), x.size, ptr(f32(cos_t)), ptr(f32(sin_t)))
+        c, sn = f32(cos_t), f32(sin_t)   # held across the call (ptr of a temporary dangles)
+        self.lib.oracle_rope_apply(ptr(x), x.size, ptr(c), ptr(sn))
         return x
 
     def softmax(self, x) -> np.ndarray:
@@ -179,9 +180,10 @@ class Oracle:
         wq, wk, wv, wo, qn, kn = (np.ascontiguousarray(a) for a in w)
         scores = np.zeros(nq * max_tokens, np.float32)
         out = np.zeros(hidden, np.float32)
-        rc = self.lib.oracle_attention_layer(ptr(wq), ptr(wk), ptr(wv), ptr(wo), ptr(f32(qn)), ptr(f32(kn)),
+        qn, kn, xn = f32(qn), f32(kn), f32(xn)
+        rc = self.lib.oracle_attention_layer(ptr(wq), ptr(wk), ptr(wv), ptr(wo), ptr(qn), ptr(kn),
                                              nq, nkv, hd, hidden, theta, eps, ptr(kc), ptr(vc), max_tokens,
-                                             pos, ptr(f32(xn)), ptr(scores), ptr(out))
+                                             pos, ptr(xn), ptr(scores), ptr(out))
         return rc, out
 
     # --- the rest of the block ----------------------------------------------
@@ -193,8 +195,9 @@ class Oracle:
 
     def mlp_layer(self, wgate, wup, wdown, hidden, inter, xn) -> np.ndarray:
         out = np.zeros(hidden, np.float32)
-        rc = self.lib.oracle_mlp_layer(ptr(np.ascontiguousarray(wgate)), ptr(np.ascontiguousarray(wup)),
-                                       ptr(np.ascontiguousarray(wdown)), hidden, inter, ptr(f32(xn)), ptr(out))
+        wgate, wup, wdown, xn = (np.ascontiguousarray(wgate), np.ascontiguousarray(wup), np.ascontiguousarray(wdown),
+                                 f32(xn))
+        rc = self.lib.oracle_mlp_layer(ptr(wgate), ptr(wup), ptr(wdown), hidden, inter, ptr(xn), ptr(out))
         assert rc == 0
         return out
 
@@ -247,7 +250,8 @@ class Oracle:
 
     def embed_lookup_q4(self, E, rows: int, cols: int, token: int):
         out = np.zeros(cols, np.float32)
-        rc = self.lib.oracle_embed_lookup_q4(ptr(np.ascontiguousarray(E)), rows, cols, token, ptr(out))
+        E = np.ascontiguousarray(E)
+        rc = self.lib.oracle_embed_lookup_q4(ptr(E), rows, cols, token, ptr(out))
         return rc, out
 
     def matmul_q8(self, Wq, xq, rows: int, cols: int, n_tok: int = 1) -> np.ndarray:
@@ -271,7 +275,8 @@ class Oracle:
     def attend_q8(self, kc, vc, nq, nkv, hd, max_tokens, q, pos):
         scores = np.zeros(nq * max_tokens, np.float32)
         out = np.zeros(nq * hd, np.float32)
-        rc = self.lib.oracle_attend_q8(ptr(kc), ptr(vc), nq, nkv, hd, max_tokens, ptr(f32(q)), pos,
+        q = f32(q)
+        rc = self.lib.oracle_attend_q8(ptr(kc), ptr(vc), nq, nkv, hd, max_tokens, ptr(q), pos,
                                        ptr(scores), ptr(out))
         return rc, out
 
@@ -490,7 +495,8 @@ class Ref:
 
     def unpack_matrix_q4(self, Wq, rows: int, cols: int) -> np.ndarray:
         out = np.zeros((rows, cols), np.float32)
-        rc = self.lib.unpack_matrix(ptr(np.ascontiguousarray(Wq)), rows, cols, ptr(out), b"4")
+        Wq = np.ascontiguousarray(Wq)
+        rc = self.lib.unpack_matrix(ptr(Wq), rows, cols, ptr(out), b"4")
         assert rc == 0
         return out
 

@@ -523,9 +523,8 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
     auto process = [&](const unsigned char *tb, int k0) {
         const unsigned char *Kt = tb;
         const unsigned char *Vt = tb + kTK * ROW;
-        bool valid[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) valid[i] = k0 + slot_key(lg, i) < t_end;
+        // only a split's last tile can hold keys past its end (wave-uniform)
+        const bool edge = k0 + kTK > t_end;
 
         // scores: exact int32 block dots, column (h, b) keeps block b
         v4i acc[2][NT];
@@ -555,9 +554,10 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
         for (int nt = 0; nt < NT; nt++) {
             float s[8];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float sc = head_block_sum<NB>((float)acc[i >> 2][nt][i & 3] * (qdl[nt] * kd[i]));
-                s[i] = valid[i] ? sc : -INFINITY;
+            for (int i = 0; i < 8; i++) s[i] = head_block_sum<NB>((float)acc[i >> 2][nt][i & 3] * (qdl[nt] * kd[i]));
+            if (edge) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) s[i] = k0 + slot_key(lg, i) < t_end ? s[i] : -INFINITY;
             }
             float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
             mx = xrow_max(mx);
@@ -570,7 +570,13 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
             for (int i = 0; i < 8; i++) {
                 const float p = __builtin_amdgcn_exp2f(s[i] - m_new);
                 ps += p;
-                w[i] = valid[i] ? p * vd[i] : 0.0f;
+                w[i] = p * vd[i];
+            }
+            if (edge) {
+                // keys past the end: p is 0, and their slot's scale may be
+                // anything the copy saw (an unmapped page reads page 0)
+#pragma unroll
+                for (int i = 0; i < 8; i++) w[i] = k0 + slot_key(lg, i) < t_end ? w[i] : 0.0f;
             }
             l_run[nt] = l_run[nt] * corr + xrow_sum(ps);
             if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0) {

@@ -61,7 +61,8 @@ def test_sample_greedy(oracle, ref_scalar):
         a = L.oracle_sample_greedy(ptr(logits), logits.size)
         b = ref_scalar.lib.sample_greedy(ptr(logits), logits.size)
         assert a == b
-    assert L.oracle_sample_greedy(ptr(np.array([0.5, 2.0, 2.0], np.float32)), 3) == 1
+    tie = np.array([0.5, 2.0, 2.0], np.float32)
+    assert L.oracle_sample_greedy(ptr(tie), 3) == 1
     assert L.oracle_sample_greedy(None, 0) == -1
 
 
