@@ -30,8 +30,10 @@
 //       block dot of attn_scores_q8 (model/attn_q8.c:24-30) in any
 //       accumulation order; each block's dot is scaled and added in block
 //       order (one multiply, one fma per score and block), exp2 domain;
-//     online softmax per query with a causal mask; the running max moves only
-//       when a tile exceeds it by more than 2^8;
+//     online softmax per query with a causal mask; scores are accumulated
+//       against the running max, which moves only when a tile exceeds it by
+//       more than 2^8: a tile that needs no mask and stays under that for
+//       every row of the wave takes a fast path with no cross-lane reduction;
 //     O^T += V'^T . P^T on the same bf16 product, P split into hi + lo.
 //   The S^T orientation leaves each lane with 8 keys of one query: exactly a
 //   B operand of the P.V product (keys permuted identically in A and B), so P
@@ -43,10 +45,12 @@
 // sequence (the later block's tiles, then the earlier block's) is cut into nsp
 // equal chunks, one work item each, so all items carry the same work.  An item
 // runs one or two segments (a block and a tile range).  A block covered by
-// several segments gets a partial (o, m, l per row) from each, written with
-// agent-coherent 16-byte stores; an arrival counter picks the last segment to
-// finish, which merges them in segment order, so the result does not depend
-// on which work-group finished last.
+// several segments is merged by the segment that finishes last, picked by an
+// arrival counter: every other segment writes its partial (o, m, l per row)
+// with agent-coherent 16-byte stores and counts itself on a second counter,
+// which the last one waits on; it merges the partials and its own registers
+// in segment order, so the result does not depend on which work-group
+// finished last.
 //
 // Grid: one dimension, work-group w serves kv head w % n_kv, so with 8 kv
 // heads each XCD (work-groups go round-robin over the 8 XCDs) works on one
@@ -376,10 +380,16 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
     for (int m = 0; m < S::MT; m++)
 #pragma unroll
         for (int j = 0; j < NJ; j++) o[m][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    float mrow[NJ], lsum[NJ];
+    // per row (the same in the row's four lanes): mrow the running max, moff
+    // the offset o and lsum are taken against (mrow, or 0 before any key),
+    // thr the largest score - moff a tile may hold without moving the max
+    // (kLazy; -inf before any key, so the first visible key takes the slow path)
+    float mrow[NJ], moff[NJ], thr[NJ], lsum[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         mrow[j] = -INFINITY;
+        moff[j] = 0.0f;
+        thr[j] = -INFINITY;
         lsum[j] = 0.0f;
     }
 
@@ -393,14 +403,10 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
         __syncthreads();
         if (kt + 1 < kt_end) fetch(odd ? tile0 : tile1, kt + 1);
 
-        // S^T for keys [32kt, 32kt+32) x the wave's queries: per block the
-        // exact int32 dot on the matrix cores, then (kd * qd') * dot added in
-        // block order
+        // S^T - moff for keys [32kt, 32kt+32) x the wave's queries: per block
+        // the exact int32 dot on the matrix cores, then (kd * qd') * dot added
+        // in block order onto -moff
         v4f s[2][NJ];
-#pragma unroll
-        for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-            for (int j = 0; j < NJ; j++) s[mt][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int b = 0; b < NB; b++) {
 #pragma unroll
@@ -412,48 +418,79 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
                     const v4f d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kc, qcb[j][b], v4f{0.0f, 0.0f, 0.0f, 0.0f},
                                                                           0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 4; r++) s[mt][j][r] = __builtin_fmaf(d[r], kd[r] * qsc[j][b], s[mt][j][r]);
+                    for (int r = 0; r < 4; r++)
+                        s[mt][j][r] = __builtin_fmaf(d[r], kd[r] * qsc[j][b], b == 0 ? -moff[j] : s[mt][j][r]);
                 }
             }
         }
 
-        // causal mask, online softmax, P split into bf16 hi | lo (B operands)
+        // fast path: no row's tile max passes its threshold, and the tile needs
+        // no causal mask (it ends at or before the block's first query); the
+        // lane maxima are taken here, in the block that computes the scores
+        auto max8 = [](const v4f &x, const v4f &y) {
+            return fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])));
+        };
         const int k0 = kt * kKT;
-        u32x4 phi[NJ], plo[NJ];
+        const bool diag = k0 + kKT - 1 > a.pos0 + i0;
+        bool move = false;
 #pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            if (k0 + kKT - 1 > a.pos0 + i0) {   // tiles past the block's first query need the mask
+        for (int j = 0; j < NJ; j++) move |= max8(s[0][j], s[1][j]) > thr[j];
+        if (diag || __builtin_amdgcn_ballot_w64(move) != 0) {
+            // slow path, for the whole wave: the causal mask, the row max over
+            // the four lanes, the lazy move (only by more than kLazy), o and
+            // lsum rescaled and the tile re-offset
+            if (diag) {
+#pragma unroll
+                for (int j = 0; j < NJ; j++)
+#pragma unroll
+                    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const int kp = k0 + mt * 16 + 4 * lg + r;
+                            s[mt][j][r] = kp > qpos[j] ? -INFINITY : s[mt][j][r];
+                        }
+            }
+            bool rescale = false;
+            float corr[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const float mx = xrow_max(max8(s[0][j], s[1][j])) + moff[j];
+                const float mnew = mx > mrow[j] + kLazy ? mx : mrow[j];
+                const float onew = mnew == -INFINITY ? 0.0f : mnew;
+                // nothing is accumulated while mrow is -inf: corr 0, not exp2 of a difference
+                corr[j] = mrow[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(moff[j] - onew);
+                const float delta = moff[j] - onew;
 #pragma unroll
                 for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int kp = k0 + mt * 16 + 4 * lg + r;
-                        s[mt][j][r] = kp > qpos[j] ? -INFINITY : s[mt][j][r];
-                    }
+                    for (int r = 0; r < 4; r++) s[mt][j][r] += delta;
+                rescale |= corr[j] != 1.0f;
+                lsum[j] *= corr[j];
+                mrow[j] = mnew;
+                moff[j] = onew;
+                thr[j] = mnew == -INFINITY ? -INFINITY : kLazy;
             }
-            float mx = fmaxf(fmaxf(fmaxf(s[0][j][0], s[0][j][1]), fmaxf(s[0][j][2], s[0][j][3])),
-                             fmaxf(fmaxf(s[1][j][0], s[1][j][1]), fmaxf(s[1][j][2], s[1][j][3])));
-            mx = xrow_max(mx);
-            const float mnew = mx > mrow[j] + kLazy ? mx : mrow[j];
-            // a split's first tiles can be fully masked for its early rows:
-            // offset by 0 while the max is still -inf (p = 0, no NaN)
-            const float moff = mnew == -INFINITY ? 0.0f : mnew;
-            const float corr = __builtin_amdgcn_exp2f(mrow[j] - moff);
-            mrow[j] = mnew;
+            if (__builtin_amdgcn_ballot_w64(rescale) != 0) {
+#pragma unroll
+                for (int m = 0; m < S::MT; m++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++) o[m][j] *= corr[j];
+            }
+        }
+        // P = exp2(S - moff) <= 2^kLazy, split into bf16 hi | lo (B operands)
+        u32x4 phi[NJ], plo[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
             float p[8];
             float ps = 0.0f;
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    p[mt * 4 + r] = __builtin_amdgcn_exp2f(s[mt][j][r] - moff);
+                    p[mt * 4 + r] = __builtin_amdgcn_exp2f(s[mt][j][r]);
                     ps += p[mt * 4 + r];
                 }
-            lsum[j] = lsum[j] * corr + ps;
-            if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0) {
-#pragma unroll
-                for (int m = 0; m < S::MT; m++) o[m][j] *= corr;
-            }
+            lsum[j] += ps;
             split_bf16(p, phi[j], plo[j]);
         }
 
@@ -495,32 +532,49 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
         return;
     }
 
-    // ---- split: partial rows [RW][HD + 4] (o unnormalised, m, l) of this split
+    // ---- split: the arrival counter first; only the splits that are not the
+    //      last to arrive write their partial rows [RW][HD + 4] (o
+    //      unnormalised, m, l) and then count themselves on a second counter
     constexpr int PS = HD + 4;
     const size_t pblock = ((size_t)kvh * a.qblocks + blk) * a.nsp;
     const __amdgpu_buffer_rsrc_t prs =
         __builtin_amdgcn_make_buffer_rsrc(a.partials + pblock * S::RW * PS, 0, nsp * S::RW * PS * 4, 0x00020000);
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int r = (wave * NJ + j) * 16 + l16;
-        const int base = (sp * S::RW + r) * PS;
-#pragma unroll
-        for (int m = 0; m < S::MT; m++)
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[m][j]), prs,
-                                                   (base + m * 16 + 4 * lg) * 4, 0, kCoherentP);
-        if (lg == 0) {
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(mrow[j]), prs, (base + HD) * 4, 0, kCoherentP);
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lrow[j]), prs, (base + HD + 1) * 4, 0, kCoherentP);
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0);   // the partial is at the point of coherence
-    __syncthreads();
     int *counter = a.counters + ((size_t)kvh * a.qblocks + blk) * kCounterStrideP;
+    int *ready = counter + kCounterStrideP / 2;   // a line of its own
     int *flag = reinterpret_cast<int *>(tile0);
+    __syncthreads();   // every wave is done with the tile buffers
     if (tid == 0) *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsp - 1;
     __syncthreads();
-    if (!*flag) return;
-    if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!*flag) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int r = (wave * NJ + j) * 16 + l16;
+            const int base = (sp * S::RW + r) * PS;
+#pragma unroll
+            for (int m = 0; m < S::MT; m++)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[m][j]), prs,
+                                                       (base + m * 16 + 4 * lg) * 4, 0, kCoherentP);
+            if (lg == 0) {
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(mrow[j]), prs, (base + HD) * 4, 0, kCoherentP);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lrow[j]), prs, (base + HD + 1) * 4, 0,
+                                                      kCoherentP);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);   // this thread's partial is at the point of coherence
+        __syncthreads();
+        if (tid == 0) __hip_atomic_fetch_add(ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    // the last to arrive waits for the other nsp - 1 partials: their splits
+    // have arrived, so they are running, and they finish without waiting on
+    // anything; then both counters go back to 0 for the next launch
+    if (tid == 0) {
+        while (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != nsp - 1)
+            __builtin_amdgcn_s_sleep(1);
+        __hip_atomic_store(ready, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
 
     // ---- the last split merges all of them in split order (its own from registers)
 #pragma unroll
