@@ -51,15 +51,20 @@ hipStream_t pick(tq_hip_kv *kv, void *stream) {
     return stream ? static_cast<hipStream_t>(stream) : kv->stream;
 }
 
-// Work-groups the decode aims for: several per CU of the 256-CU MI355X so
-// that each CU streams from a few splits at once.  Overridable for sweeps.
-int decode_wg_target() {
+// Work-groups the decode aims for on the 256-CU MI355X.  One sequence: four
+// per CU, so that a 4k-token context is cut into 128-token splits over every
+// CU.  A batch: two per CU, in one round of resident work-groups; each
+// work-group's fixed cost (staging q, the wave merge, the split combine)
+// outweighs the balance that shorter splits buy (64 ragged 512-8192 token
+// sequences at the 8B shape: 117 us per step with one split per sequence and
+// head, against 135-180 us at 1024-2048 work-groups).  Overridable for sweeps.
+int decode_wg_target(int n_q) {
     static int v = [] {
         const char *s = getenv("TQ_HIP_DECODE_WG_TARGET");
         const int x = s ? atoi(s) : 0;
-        return x > 0 ? x : 1024;
+        return x > 0 ? x : 0;
     }();
-    return v;
+    return v ? v : (n_q > 1 ? 512 : 1024);
 }
 
 // Fewest new tokens for which a prefill call uses the dense kernel.
@@ -92,7 +97,7 @@ void plan_splits(const tq_hip_kv *kv, int n_q, int max_len, int *split_tokens, i
     const long pairs = (long)n_q * kv->desc.n_kv_heads;
     const int cap = std::min(decode_max_splits(),
                              tq_decode_max_splits(kv->desc.head_dim, kv->desc.n_q_heads / kv->desc.n_kv_heads));
-    long want = (decode_wg_target() + pairs - 1) / pairs;
+    long want = (decode_wg_target(n_q) + pairs - 1) / pairs;
     want = std::max(1L, std::min<long>(want, cap));
     want = std::min<long>(want, chunks);
     // a work-group stages at most tq_decode_max_split_tokens() page ids
@@ -115,12 +120,13 @@ bool use_decode3(const tq_hip_kv *kv) {
 }
 
 // Longest split (tokens) the MFMA decode gives one work-group when the split
-// count allows: shorter splits keep ragged batches balanced over the CUs.
+// count allows (TQ_HIP_DECODE_SPLIT_CAP, for sweeps); by default only the
+// page-id staging limits it.
 int decode3_split_cap() {
     static int v = [] {
         const char *s = getenv("TQ_HIP_DECODE_SPLIT_CAP");
         const int x = s ? atoi(s) : 0;
-        return x > 0 ? x : 4096;
+        return x > 0 ? x : tq_decode3_max_split_tokens();
     }();
     return v;
 }
@@ -143,7 +149,7 @@ void plan_splits3(const tq_hip_kv *kv, int n_q, int max_len, int waves, int *spl
     const long units = std::max(1, (max_len + unit - 1) / unit);
     const long pairs = (long)n_q * kv->desc.n_kv_heads;
     const long cap = tq_decode3_max_splits();
-    long want = (decode_wg_target() + pairs - 1) / pairs;
+    long want = (decode_wg_target(n_q) + pairs - 1) / pairs;
     want = std::max(1L, std::min(std::min(want, cap), units));
     long per = (units + want - 1) / want;
     per = std::min<long>(per, std::max(1, decode3_split_cap() / unit));
@@ -370,15 +376,18 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
     }
     // four waves per work-group: for a single 4k-token sequence at the 8B
     // shape this spreads one 32-key tile per wave over all 256 CUs, which beats
-    // eight waves on half of them (8.7 against 9.1 us per step)
-    int waves = 4;
+    // eight waves on half of them (8.7 against 9.1 us per step).  A batch at
+    // G <= 4 takes eight: two resident work-groups per CU then stream 16 tiles
+    // at once (the 64-sequence batch: 117 against 129 us); at G = 8 four waves
+    // stay ahead (234 against 240 us at 16 x 32k tokens).
+    const int g = D.n_q_heads / D.n_kv_heads;
+    int waves = n_q > 1 && g <= 4 ? 8 : 4;
     if (decode3_waves_env()) waves = decode3_waves_env();
     if (v3)
         plan_splits3(kv, n_q, max_len, waves, &a.split_tokens, &a.n_splits);
     else
         plan_splits(kv, n_q, max_len, &a.split_tokens, &a.n_splits);
     if (a.n_splits > 1) {
-        const int g = D.n_q_heads / D.n_kv_heads;
         const size_t row = v3 ? (size_t)tq_decode3_partial_floats(D.head_dim, g) : (size_t)g * (D.head_dim + 2);
         const size_t bytes = (size_t)n_q * D.n_kv_heads * a.n_splits * row * sizeof(float);
         const size_t n_counters = (size_t)n_q * D.n_kv_heads * TQ_DECODE_COUNTER_STRIDE;

@@ -95,10 +95,11 @@ def test_noalloc_matches_step(nat, oracle):
 
 
 def test_noalloc_refuses_oversized_call(nat, oracle):
-    """129 queries x 8 kv heads with split-K (8192 keys: 2 splits) need more
-    arrival counters than the array holds: TQ_HIP_ESCRATCH, nothing launched."""
+    """129 queries x 8 kv heads with split-K (16384 keys: two splits of 8192,
+    the most one work-group stages) need more arrival counters than the array
+    holds: TQ_HIP_ESCRATCH, nothing launched."""
     lib = nat.load()
-    nq, nkv, hd, T, nseq = 32, 8, 128, 8192, 129
+    nq, nkv, hd, T, nseq = 32, 8, 128, 16384, 129
     kv = nat.PagedKV(nq, nkv, hd, n_pages=T // PAGE, max_seqs=1, max_pages_per_seq=T // PAGE)
     kv.set_pages(0, np.arange(T // PAGE, dtype=np.int32))
     pos = np.full(nseq, T - 1, np.int32)
