@@ -22,10 +22,15 @@
 //           them with two DPP butterflies: the score of attn_scores_q8_scalar
 //           (model/attn_q8.c:17-34) up to fp32 rounding order, in the exp2
 //           domain.
-//   softmax online, per lane, exp2 domain; max and sum over the four 16-lane
-//           rows holding the tile's keys with permlane32/16 swaps.  The
-//           running max moves only when a tile exceeds it by more than 2^8,
-//           so rescaling the accumulators is rare (p <= 256 in between).
+//   softmax online, per lane, exp2 domain, the scores taken against the
+//           running max, which moves only when a tile exceeds it by more
+//           than 2^8 (p <= 256 in between).  A tile with no key past the
+//           split's end and no lane over that threshold takes a fast path:
+//           no cross-lane work at all.  Otherwise the max over the four
+//           16-lane rows holding the tile's keys comes from permlane32/16
+//           swaps and the accumulators are rescaled when it moves.  Each lane
+//           keeps its own share of the row sum; the rows are added once, at
+//           the end.
 //   P.V     O[col][(h,b)] += V[key][col] * W[key][(h,b)] on
 //           v_mfma_f32_16x16x32_bf16, K = 32 keys.  W = p * vd (the weight of
 //           attn_accum_q8's ws = wt * vb[b].d, model/attn_q8.c:48) lies in
@@ -511,11 +516,19 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
     for (int c = 0; c < CT; c++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) o[c][nt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    float m_run[NT], l_run[NT];
+    // per column (the same in the head's lanes and over the four 16-lane
+    // rows): m_run the running max, moff the offset o and l_part are taken
+    // against (m_run, or 0 before any key), thr the largest score - moff a
+    // tile may hold without moving the max (kLazy; -inf before any key);
+    // l_part is this lane's share of the row sum, added over the rows once
+    // at the end
+    float m_run[NT], moff[NT], thr[NT], l_part[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         m_run[nt] = -INFINITY;
-        l_run[nt] = 0.0f;
+        moff[nt] = 0.0f;
+        thr[nt] = -INFINITY;
+        l_part[nt] = 0.0f;
     }
     const int pr_new = wave_new ? pos_new : -1;
 
@@ -549,26 +562,66 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
             vd[i] = lds_f(Vt + slot_key(lg, i) * ROW + bl * kBlockBytes);
         }
 
+        // scores - moff: each of the head's NB lanes adds -moff/NB (exact) to
+        // its scaled block dot before the butterfly sums them
+        float sc[NT][8];
+        bool move = false;
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const float mq = moff[nt] * (1.0f / NB);
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                sc[nt][i] = head_block_sum<NB>(__builtin_fmaf((float)acc[i >> 2][nt][i & 3], qdl[nt] * kd[i], -mq));
+            const float lmax = fmaxf(fmaxf(fmaxf(sc[nt][0], sc[nt][1]), fmaxf(sc[nt][2], sc[nt][3])),
+                                     fmaxf(fmaxf(sc[nt][4], sc[nt][5]), fmaxf(sc[nt][6], sc[nt][7])));
+            move |= lmax > thr[nt];
+        }
+        // slow path, for the whole wave when the tile holds keys past the
+        // split's end or any column's tile max passes its threshold: the mask,
+        // the max over the four rows, the lazy move (only by more than kLazy),
+        // o and l_part rescaled and the tile re-offset
+        if (edge || __builtin_amdgcn_ballot_w64(move) != 0) {
+            bool rescale = false;
+            float corr[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                if (edge) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) sc[nt][i] = k0 + slot_key(lg, i) < t_end ? sc[nt][i] : -INFINITY;
+                }
+                float mx = fmaxf(fmaxf(fmaxf(sc[nt][0], sc[nt][1]), fmaxf(sc[nt][2], sc[nt][3])),
+                                 fmaxf(fmaxf(sc[nt][4], sc[nt][5]), fmaxf(sc[nt][6], sc[nt][7])));
+                mx = xrow_max(mx) + moff[nt];
+                const float m_new = mx > m_run[nt] + kLazy ? mx : m_run[nt];
+                const float onew = m_new == -INFINITY ? 0.0f : m_new;
+                // nothing is accumulated while m_run is -inf: corr 0, not exp2 of a difference
+                corr[nt] = m_run[nt] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(moff[nt] - onew);
+                const float delta = moff[nt] - onew;
+#pragma unroll
+                for (int i = 0; i < 8; i++) sc[nt][i] += delta;
+                rescale |= corr[nt] != 1.0f;
+                l_part[nt] *= corr[nt];
+                m_run[nt] = m_new;
+                moff[nt] = onew;
+                thr[nt] = m_new == -INFINITY ? -INFINITY : kLazy;
+            }
+            if (__builtin_amdgcn_ballot_w64(rescale) != 0) {
+#pragma unroll
+                for (int c = 0; c < CT; c++)
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++) o[c][nt] *= corr[nt];
+            }
+        }
+
+        // W = exp2(S - moff) * vd <= 2^kLazy * vd, split into bf16 hi | lo
         v8bf whi[NT], wlo[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
-            float s[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) s[i] = head_block_sum<NB>((float)acc[i >> 2][nt][i & 3] * (qdl[nt] * kd[i]));
-            if (edge) {
-#pragma unroll
-                for (int i = 0; i < 8; i++) s[i] = k0 + slot_key(lg, i) < t_end ? s[i] : -INFINITY;
-            }
-            float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-            mx = xrow_max(mx);
-            const float m_new = mx > m_run[nt] + kLazy ? mx : m_run[nt];
-            const float corr = __builtin_amdgcn_exp2f(m_run[nt] - m_new);
-            m_run[nt] = m_new;
             float w[8];
             float ps = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const float p = __builtin_amdgcn_exp2f(s[i] - m_new);
+                const float p = __builtin_amdgcn_exp2f(sc[nt][i]);
                 ps += p;
                 w[i] = p * vd[i];
             }
@@ -578,11 +631,7 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
 #pragma unroll
                 for (int i = 0; i < 8; i++) w[i] = k0 + slot_key(lg, i) < t_end ? w[i] : 0.0f;
             }
-            l_run[nt] = l_run[nt] * corr + xrow_sum(ps);
-            if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0) {
-#pragma unroll
-                for (int c = 0; c < CT; c++) o[c][nt] *= corr;
-            }
+            l_part[nt] += ps;
             split_bf16(w, whi[nt], wlo[nt]);
         }
 
@@ -659,13 +708,16 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
     float *mw = reinterpret_cast<float *>(&slot0[0][0]);     // [W][G]
     float *lw = mw + kWaves * G;                               // [W][G]
     float *ow = lw + kWaves * G;                               // [W][G][HD]
+    float l_row[NT];   // every lane takes part in the cross-row sums
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) l_row[nt] = xrow_sum(l_part[nt]);
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int h = (16 * nt + l16) / NB;
         if (h < G) {
             if (lg == 0 && bl == 0) {
                 mw[wave * G + h] = m_run[nt];
-                lw[wave * G + h] = l_run[nt];
+                lw[wave * G + h] = l_row[nt];
             }
 #pragma unroll
             for (int c = 0; c < CT; c++) {
