@@ -47,6 +47,7 @@ import ctypes as C
 import json
 import os
 import re
+import subprocess
 import sys
 import time
 
@@ -424,6 +425,19 @@ def host_boundary_us(nq, nkv, hd, T, theta, q, k, v, calls=200):
     return us
 
 
+def host_boundary_c(pos: int = 4095, calls: int = 2000):
+    """The same synchronous call timed from C (tailorquantkernel_amd/boundary_bench,
+    built beside the libraries), with its pieces: the host RoPE table, the
+    append alone and the attend alone.  None if the program is not built."""
+    exe = os.path.join(ROOT, "tailorquantkernel_amd", "boundary_bench")
+    if not os.path.exists(exe):
+        return None
+    r = subprocess.run([exe, str(pos), str(calls)], capture_output=True, text=True, timeout=120)
+    if r.returncode != 0:
+        raise RuntimeError(f"boundary_bench failed ({r.returncode}): {r.stderr.strip()}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 # ---------------------------------------------------------------------------
 # single-sequence decode: the 8B shape at context 4096 (the headline), and
 # the small reference test shape at context 256
@@ -481,6 +495,23 @@ def bench_decode_single(args, nat, hip, *, nq, nkv, hd, T, theta, layers, seed, 
     res = {"ms_per_step": ms_per_step, "steps": reps * layers, "wall_s": wall, "kv_bytes": kv_bytes,
            "graph_replay_equals_eager": replay_same, "boundary_us": boundary_us, "floor": floor}
     return res, (kc0.reshape(-1), vc0.reshape(-1), q, k, v, got)
+
+
+CURVE_CONTEXTS = (256, 1024, 4096, 16384, 32768)
+
+
+def decode_curve(args, nat, hip):
+    """Batch-1 step time of the 8B-shape fused decode over the contexts the
+    reference's forward benchmark sweeps (tools/bench_forward.c:50), each as
+    the headline is measured (32 layer caches rotated in a HIP graph): where the
+    fixed cost of a step gives way to the KV stream."""
+    points = []
+    for T in CURVE_CONTEXTS:
+        r, _ = bench_decode_single(args, nat, hip, nq=32, nkv=8, hd=128, T=T, theta=500000.0, layers=32,
+                                   seed=100 + T, boundary=False)
+        points.append({"context": T, "us_per_step": r["ms_per_step"] * 1e3, "kv_bytes": r["kv_bytes"],
+                       "kv_gbps": r["kv_bytes"] / (r["ms_per_step"] * 1e-3) / 1e9})
+    return points
 
 
 def step_floor(nat, hip, stream, bufs, nbytes, n_heads, reps, n_splits=32):
@@ -548,6 +579,7 @@ def bench_decode_8b(args, nat, hip):
         "wall_s": r["wall_s"],
         "graph_replay_equals_eager": r["graph_replay_equals_eager"],
         "host_boundary_us_per_call": r["boundary_us"],
+        "host_boundary_c": None if args.no_boundary else host_boundary_c(),
         "step_floor": r["floor"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic("decode_8b_ctx4096_b1_pmc.txt"),
@@ -1495,6 +1527,7 @@ def run_all(args, nat, hip):
     line, check = bench_decode_8b(args, nat, hip)
     if not args.no_cpu:
         line["cpu_baseline"], line["parity"] = cpu_leg_attention(32, 8, 128, 4096, 500000.0, args.cpu_budget, check)
+    line["decode_context_curve"] = decode_curve(args, nat, hip)
     work = {}
 
     c1, check1 = bench_decode_c1(args, nat, hip)
@@ -1525,7 +1558,8 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--config", default="all",
-                    choices=["all", "decode-8b-4k", "decode-c1", "decode-batched", "prefill-2k", "decode-70b-32k",
+                    choices=["all", "decode-8b-4k", "decode-c1", "decode-curve", "decode-batched", "prefill-2k",
+                             "decode-70b-32k",
                              "project-8b", "project-70b", "layer-8b", "layer-prefill-8b", "forward-8b",
                              "forward-8b-q4"])
     ap.add_argument("--layers", type=int, default=32)
@@ -1551,6 +1585,9 @@ def main():
         if not args.no_cpu:
             line["cpu_baseline"], line["parity"] = cpu_leg_attention(32, 8, 128, 4096, 500000.0, args.cpu_budget,
                                                                      check)
+    elif args.config == "decode-curve":
+        line = {"metric": "Q8 GQA decode step time over context, 8B shape, batch 1, 1 GPU",
+                "unit": "us per step", "points": decode_curve(args, nat, hip)}
     elif args.config == "decode-c1":
         line, check = bench_decode_c1(args, nat, hip)
         if not args.no_cpu:
