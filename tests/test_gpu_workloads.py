@@ -7,11 +7,10 @@ the oracle (the C restatement of the reference's scalar Q8 path):
 * batch-1 decode at the Llama-3-8B shape, context 4096: the fused step
   (RoPE + append + attend, 32 splits of 128 keys);
 * 64 ragged sequences, lengths U[512, 8192] drawn with seed 2024, 16-token
-  pages scattered over the pool, the fused step (2 splits of 4096 keys,
-  longest-first order);
+  pages scattered over the pool, the fused step (one split per sequence and
+  kv head, eight-wave work-groups, longest first);
 * the 70B per-layer shape (64 q / 8 kv heads), batch 16 x 32768 keys, 1 % of
-  the K/V values at +-8 sigma, the fused step (8 splits of 4096 keys, 1024
-  work-groups in two rounds);
+  the K/V values at +-8 sigma, the fused step (4 splits of 8192 keys);
 * the causal prefill of 2048 tokens: the whole cache against the oracle's own
   quantize_row_q8 of the rotated k and v rows, and sampled outputs against
   attend_q8 over that independent cache;
