@@ -568,7 +568,11 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
             for (int t4 = 0; t4 < 4; t4++) {
                 const unsigned char *tb = B + (wt + 16 * t4 + l16) * kGemmBRow + blk * kBlockBytes;
                 bv[t4] = lds_pair(tb + 4 + 8 * lg);
-                xd[t4] = valid ? *reinterpret_cast<const float *>(tb) : 0.0f;
+                // the staged scale is always a real block's (past nb the copies
+                // repeat block nb-1): load it unconditionally and select, so no
+                // branch splits the block's LDS reads from its products
+                const float xv = *reinterpret_cast<const float *>(tb);
+                xd[t4] = valid ? xv : 0.0f;
             }
             // all eight products first, so that each one's latency hides
             // under the others before its results are read
