@@ -84,15 +84,17 @@ struct L3 {
     static constexpr int NT = (NCOL + 15) / 16;         // 16-column tiles of them
     static constexpr int CT = HD / 16;                  // 16-column tiles of the output
     static constexpr int TILE = 2 * kTK * ROW;          // K rows | V rows
-    static constexpr int NCH = TILE / 16;               // 16-byte chunks per tile
-    static constexpr int CPL = (NCH + 63) / 64;         // chunk loads per lane
-    static constexpr int PAGE_CH = kPage * ROW / 16;    // chunks of one page's K (or V) run
+    static constexpr int RUN = kPage * ROW;             // bytes of one page's K (or V) run
+    static constexpr int RUN_FULL = RUN / 1024;         // whole-wave 16-byte copies per run
+    static constexpr int RUN_TAIL = RUN % 1024 / 16;    // lanes of the run's last, partial copy
+    static constexpr int CPL = 4 * (RUN_FULL + (RUN_TAIL > 0));   // copies per tile
     static constexpr int U = G * HD / 4;                // float4 units of a head group's output
     static constexpr int PSTRIDE = (G * (HD + 2) + 3) / 4 * 4;   // floats per partial row
     static constexpr int MERGE = G * (HD + 2) * 4;      // one wave's share of the merge
     static_assert(NB == 1 || NB == 2 || NB == 4, "a head's blocks share one DPP quad");
     static_assert(16 % NB == 0, "column tiles hold whole heads");
-    static_assert(kTK * ROW % 16 == 0 && kPage * ROW % 16 == 0, "16-byte chunks");
+    static_assert(kTK * ROW % 16 == 0 && RUN % 16 == 0, "16-byte chunks");
+    static_assert(TILE == 4 * RUN, "a tile is four page runs");
     static_assert(MERGE <= TILE, "the merge reuses the tile slots");
     static_assert(U % 1 == 0 && HD % 4 == 0, "float4 units");
 };
@@ -180,6 +182,27 @@ __device__ __forceinline__ void dma16(const void *src, unsigned char *dst) {
         "global_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
         : "=&s"(saved)
         : "v"(src), "s"(lds));
+}
+// The same copy from a scalar base address plus each lane's 32-bit offset
+// (the saddr form): a uniform base costs no vector address arithmetic.
+__device__ __forceinline__ void dma16s(const unsigned char *base, uint32_t off, unsigned char *dst) {
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_u8 *)dst;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(base), "s"(lds));
+}
+// 4 bytes per lane, the same way (into LDS at dst + 4*lane).
+__device__ __forceinline__ void dma4s(const unsigned char *base, uint32_t off, unsigned char *dst) {
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_u8 *)dst;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
+        "global_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(base), "s"(lds));
 }
 // Wait until at most N vector memory operations of this wave are outstanding.
 template <int N>
@@ -304,18 +327,12 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
         }
     }
 
-    // Byte offset of this lane's chunk i inside a page's K|V run, and which of
-    // the tile's two pages it comes from: chunk c = lane + 64 i of the tile
-    // image [K page 0 | K page 1 | V page 0 | V page 1].
-    uint32_t coff[CPL];
-    bool csec[CPL];
+    // Each lane's byte offset inside a page run for each copy of the run.
+    // (a 256-byte tail goes as one whole-wave 4-byte copy)
+    constexpr bool kTail4 = L::RUN_TAIL == 16;
+    uint32_t roff[L::RUN_FULL + 1];
 #pragma unroll
-    for (int i = 0; i < CPL; i++) {
-        const int c = min(lane + 64 * i, L::NCH - 1);
-        const int reg = c / L::PAGE_CH;
-        coff[i] = (uint32_t)((reg >> 1) * (int)view.kv_chunk + 16 * (c - reg * L::PAGE_CH));
-        csec[i] = reg & 1;
-    }
+    for (int j = 0; j <= L::RUN_FULL; j++) roff[j] = (uint32_t)(1024 * j + (kTail4 && j == L::RUN_FULL ? 4 : 16) * lane);
     const unsigned char *head0 = view.pool + (size_t)kvh * view.head_run;
     int load_end;   // keys below this are mapped; pages past it are not fetched
 
@@ -324,19 +341,28 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
         if (contig) return lp < a.contig_pages ? a.contig_first + lp : -1;
         return sm.pages[min(max(lp - t_begin / kPage, 0), kMaxSplitPages3 - 1)];
     };
-    // Copy the tile with keys [k0, k0+32) into an LDS slot (CPL copies).  A page
-    // that is unmapped (or past load_end) is read from physical page 0
-    // instead: those keys are masked out.
+    // Copy the tile with keys [k0, k0+32) into an LDS slot (CPL copies): the
+    // image [K page 0 | K page 1 | V page 0 | V page 1] is four contiguous
+    // page runs, each copied from its own scalar base (RUN_FULL whole-wave
+    // copies and one of RUN_TAIL lanes).  A page that is unmapped (or past
+    // load_end) is read from physical page 0 instead: those keys are masked out.
     auto fetch = [&](unsigned char *dst, int k0) {
         int p0 = page_of(k0 / kPage), p1 = page_of(k0 / kPage + 1);
-        p0 = (p0 >= 0 && k0 < load_end) ? p0 : 0;
-        p1 = (p1 >= 0 && k0 + kPage < load_end) ? p1 : 0;
+        p0 = __builtin_amdgcn_readfirstlane((p0 >= 0 && k0 < load_end) ? p0 : 0);
+        p1 = __builtin_amdgcn_readfirstlane((p1 >= 0 && k0 + kPage < load_end) ? p1 : 0);
         const unsigned char *b0 = head0 + (size_t)p0 * view.page_bytes;
         const unsigned char *b1 = head0 + (size_t)p1 * view.page_bytes;
 #pragma unroll
-        for (int i = 0; i < CPL; i++) {
-            const unsigned char *src = (csec[i] ? b1 : b0) + coff[i];
-            if (64 * (i + 1) <= L::NCH || lane + 64 * i < L::NCH) dma16(src, dst + 1024 * i);
+        for (int r = 0; r < 4; r++) {
+            const unsigned char *base = ((r & 1) ? b1 : b0) + (r >> 1) * view.kv_chunk;
+            unsigned char *d = dst + r * L::RUN;
+#pragma unroll
+            for (int j = 0; j < L::RUN_FULL; j++) dma16s(base, roff[j], d + 1024 * j);
+            if constexpr (kTail4) {
+                dma4s(base, roff[L::RUN_FULL], d + 1024 * L::RUN_FULL);
+            } else if constexpr (L::RUN_TAIL > 0) {
+                if (lane < L::RUN_TAIL) dma16s(base, roff[L::RUN_FULL], d + 1024 * L::RUN_FULL);
+            }
         }
     };
 
