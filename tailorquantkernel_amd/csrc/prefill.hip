@@ -9,7 +9,11 @@
 //
 // prefill_stage_kernel — once per (key tile of 32, kv head) over [0, kend):
 //   reads the tile's K and V rows from the paged cache and writes one
-//   contiguous tile image laid out as the MFMA operands want them:
+//   contiguous tile image laid out as the MFMA operands want them (and, in
+//   the same launch, once per (query block, kv head): the block's q rows
+//   after RoPE, quantized exactly as quantize_row_q8 does, as int8 codes and
+//   fp32 scales in the layout prefill_kernel keeps them in LDS, so every
+//   segment of the block copies them instead of re-deriving them):
 //     K codes [key half][block][lane][8 bf16]     (A of the score product)
 //     K scales [key half][block][lane group][4]   (kd of a lane's four keys)
 //     V' hi|lo [column tile][lane][8 bf16]        (A of the P.V product)
@@ -20,8 +24,8 @@
 // prefill_kernel — work-group of 256 threads (4 waves), one kv head, 64*NJ
 //   (query, head) rows = QB = 64*NJ/G consecutive query tokens x the G heads
 //   of the group, in row tiles of 16 queries of one head; wave w owns NJ row
-//   tiles.  q is quantized exactly as quantize_row_q8 does; its codes go to
-//   registers as bf16 (exact), its scales times scale * log2(e) beside them.
+//   tiles.  The block's staged q codes go to registers as bf16 (exact), its
+//   scales times scale * log2(e) beside them.
 //   Key tiles are copied straight into two LDS buffers (global_load_lds), one
 //   tile ahead, one barrier per tile:
 //     S^T = sum over blocks b of (kd_b * qd_b) * D_b, D_b = Kcodes_b .
@@ -147,6 +151,14 @@ __device__ __forceinline__ void dma16(const void *src, unsigned char *dst) {
         : "v"(src), "s"(lds));
 }
 
+// Wait until at most N vector memory operations of this wave are outstanding
+// (the copies above are counted in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt immediate");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
 struct StageArgs {
     PagedView view;
     int seq;
@@ -155,10 +167,96 @@ struct StageArgs {
     unsigned char *img;  // [n_kv][n_tiles][TileImg::BYTES]
     int contig_first;
     int contig_pages;
+    // the q blocks: tokens [pos0, pos0 + n), blocks of QB queries
+    int pos0;
+    int n;
+    int qblocks;
+    int n_q_heads;
+    const float *q;      // [n][n_q_heads][hd], pre-RoPE if cos_t
+    const float *cos_t;  // [n][hd/2] or null
+    const float *sin_t;
+    unsigned char *qimg; // [n_kv][qblocks][PShape::Q_BYTES]
 };
 
-template <int HD>
+template <int HD, int G, int NJ>
+struct PShape {
+    using I = TileImg<HD>;
+    static constexpr int NB = I::NB;
+    static constexpr int RW = 64 * NJ;             // (query, head) rows per work-group
+    static constexpr int QB = RW / G;              // query tokens per work-group
+    static constexpr int QT = QB / 16;             // query tiles per head
+    static constexpr int MT = I::MT;               // output column tiles
+    static constexpr int QCS = HD + 8;             // LDS stride of a q code row
+    static constexpr int Q_BYTES = RW * QCS + RW * NB * 4;   // staged q: codes | scales
+    static_assert(RW % G == 0 && QB % 16 == 0, "whole query tiles");
+    static_assert(Q_BYTES <= I::BYTES, "q staging fits one tile buffer");
+};
+
+// The q rows of query block blk (QB tokens x the G heads of kv head kvh) after
+// RoPE, quantized as quantize_row_q8 does (kernel/quant_x.c:12-33), into the
+// block's staged image: codes [RW][QCS] (row r = 16 nt + query, head nt / QT)
+// then scales [RW][NB].  Task (row r, c) covers q[4c..4c+3] and its
+// rotate-half partner q[HD/2+4c..+3]; every load of the thread's tasks is
+// issued before the first is used.  Rows of tokens past n are zero.
+template <int HD, int G, int NJ>
+__device__ __forceinline__ void stage_q(const StageArgs &a, int kvh, int blk) {
+    using S = PShape<HD, G, NJ>;
+    constexpr int NB = S::NB;
+    constexpr int HALF = HD / 2;
+    constexpr int CPR = HD / 8;                      // tasks per row; 8 | CPR
+    constexpr int TASKS = S::RW * CPR / kThreads;    // per thread
+    static_assert(S::RW * CPR % kThreads == 0, "whole tasks");
+    const int tid = threadIdx.x;
+    const int i0 = blk * S::QB;
+    unsigned char *qc = a.qimg + ((size_t)kvh * a.qblocks + blk) * S::Q_BYTES;
+    float *qd = reinterpret_cast<float *>(qc + S::RW * S::QCS);
+    v4f xl[TASKS], xu[TASKS], cs[TASKS], sn[TASKS];
+#pragma unroll
+    for (int t = 0; t < TASKS; t++) {
+        const int k = tid + kThreads * t;
+        const int r = k / CPR, c = k % CPR;
+        const int nt = r >> 4;
+        const int qi = i0 + (nt % S::QT) * 16 + (r & 15);
+        xl[t] = xu[t] = cs[t] = sn[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (qi < a.n) {
+            const float *head = a.q + ((size_t)qi * a.n_q_heads + (size_t)kvh * G + nt / S::QT) * HD;
+            xl[t] = *reinterpret_cast<const v4f *>(head + 4 * c);
+            xu[t] = *reinterpret_cast<const v4f *>(head + HALF + 4 * c);
+            if (a.cos_t) {
+                cs[t] = *reinterpret_cast<const v4f *>(a.cos_t + (size_t)qi * HALF + 4 * c);
+                sn[t] = *reinterpret_cast<const v4f *>(a.sin_t + (size_t)qi * HALF + 4 * c);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TASKS; t++) {
+        const int k = tid + kThreads * t;
+        const int r = k / CPR, c = k % CPR;
+        float lo[4], up[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (a.cos_t) {
+                lo[i] = rope_lower(xl[t][i], xu[t][i], cs[t][i], sn[t][i]);
+                up[i] = rope_upper(xl[t][i], xu[t][i], cs[t][i], sn[t][i]);
+            } else {
+                lo[i] = xl[t][i];
+                up[i] = xu[t][i];
+            }
+        }
+        const bool leader = (c & 7) == 0;
+        quantize8x4(lo, qd + r * NB + c / 8, qc + r * S::QCS + 4 * c, leader);
+        quantize8x4(up, qd + r * NB + (HALF + 4 * c) / kQK, qc + r * S::QCS + HALF + 4 * c, leader);
+    }
+}
+
+// Grid (n_tiles + qblocks, n_kv): x < n_tiles stages key tile x, the rest
+// stage q block x - n_tiles.
+template <int HD, int G, int NJ>
 __global__ __launch_bounds__(kThreads) void prefill_stage_kernel(StageArgs a) {
+    if ((int)blockIdx.x >= a.n_tiles) {
+        stage_q<HD, G, NJ>(a, blockIdx.y, (int)blockIdx.x - a.n_tiles);
+        return;
+    }
     using I = TileImg<HD>;
     constexpr int ROW = I::ROW;
     constexpr int RDW = kKT * ROW / 4;   // dwords of one tile's K (or V) rows
@@ -233,19 +331,6 @@ __global__ __launch_bounds__(kThreads) void prefill_stage_kernel(StageArgs a) {
     }
 }
 
-template <int HD, int G, int NJ>
-struct PShape {
-    using I = TileImg<HD>;
-    static constexpr int NB = I::NB;
-    static constexpr int RW = 64 * NJ;             // (query, head) rows per work-group
-    static constexpr int QB = RW / G;              // query tokens per work-group
-    static constexpr int QT = QB / 16;             // query tiles per head
-    static constexpr int MT = I::MT;               // output column tiles
-    static constexpr int QCS = HD + 8;             // LDS stride of a q code row
-    static constexpr int Q_BYTES = RW * QCS + RW * NB * 4;
-    static_assert(RW % G == 0 && QB % 16 == 0, "whole query tiles");
-    static_assert(Q_BYTES <= I::BYTES, "q staging fits one tile buffer");
-};
 
 struct PrefillArgs {
     int pos0;
@@ -255,9 +340,7 @@ struct PrefillArgs {
     int n_kv;
     float *partials;     // [n_kv][qblocks][nsp][RW][HD + 4]
     int *counters;       // [n_kv][qblocks] x kCounterStrideP
-    const float *q;      // [n][n_q_heads][hd], pre-RoPE if cos_t
-    const float *cos_t;  // [n][hd/2] or null
-    const float *sin_t;
+    const unsigned char *qimg;   // [n_kv][qblocks][PShape::Q_BYTES] (prefill_stage_kernel)
     float *out;          // [n][n_q_heads][hd]
     int n_q_heads;
     float scale;
@@ -299,55 +382,23 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
         if (I::REM > 0 && 64 * wu < I::REM)
             dma16(src + 16 * (tid + kThreads * I::ROUNDS), buf + 16 * (kThreads * I::ROUNDS + 64 * wu));
     };
-    // the first tile flies while q is quantized (q staging uses tile1)
-    fetch(tile0, kt_begin);
-
-    // ---- q rows: RoPE + quantize_row_q8 into LDS.  Task (row r, c) covers
-    //      q[4c..4c+3] and its rotate-half partner q[HD/2+4c..+3]; every load
-    //      of the thread's tasks is issued before the first is used
-    constexpr int HALF = HD / 2;
-    constexpr int CPR = HD / 8;                      // tasks per row; 8 | CPR
-    constexpr int TASKS = S::RW * CPR / kThreads;    // per thread
-    static_assert(S::RW * CPR % kThreads == 0, "whole tasks");
+    // ---- the block's staged q rows (prefill_stage_kernel) into tile1, then
+    //      the first key tile into tile0; waiting for all but this wave's
+    //      copies of the tile leaves only the tile in flight
     unsigned char *qc = tile1;
     float *qd = reinterpret_cast<float *>(tile1 + S::RW * S::QCS);
-    v4f xl[TASKS], xu[TASKS], cs[TASKS], sn[TASKS];
-#pragma unroll
-    for (int t = 0; t < TASKS; t++) {
-        const int k = tid + kThreads * t;
-        const int r = k / CPR, c = k % CPR;
-        const int nt = r >> 4;
-        const int qi = i0 + (nt % S::QT) * 16 + (r & 15);
-        xl[t] = xu[t] = cs[t] = sn[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-        if (qi < a.n) {
-            const float *head = a.q + ((size_t)qi * a.n_q_heads + (size_t)kvh * G + nt / S::QT) * HD;
-            xl[t] = *reinterpret_cast<const v4f *>(head + 4 * c);
-            xu[t] = *reinterpret_cast<const v4f *>(head + HALF + 4 * c);
-            if (a.cos_t) {
-                cs[t] = *reinterpret_cast<const v4f *>(a.cos_t + (size_t)qi * HALF + 4 * c);
-                sn[t] = *reinterpret_cast<const v4f *>(a.sin_t + (size_t)qi * HALF + 4 * c);
-            }
-        }
+    {
+        constexpr int QCH = S::Q_BYTES / 16;
+        const unsigned char *src = a.qimg + ((size_t)kvh * a.qblocks + blk) * S::Q_BYTES;
+        const int wu = __builtin_amdgcn_readfirstlane(wave);
+        for (int c0 = 64 * wu; c0 < QCH; c0 += kThreads)
+            if (c0 + lane < QCH) dma16(src + 16 * (c0 + lane), tile1 + 16 * c0);
     }
-#pragma unroll
-    for (int t = 0; t < TASKS; t++) {
-        const int k = tid + kThreads * t;
-        const int r = k / CPR, c = k % CPR;
-        float lo[4], up[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            if (a.cos_t) {
-                lo[i] = rope_lower(xl[t][i], xu[t][i], cs[t][i], sn[t][i]);
-                up[i] = rope_upper(xl[t][i], xu[t][i], cs[t][i], sn[t][i]);
-            } else {
-                lo[i] = xl[t][i];
-                up[i] = xu[t][i];
-            }
-        }
-        const bool leader = (c & 7) == 0;
-        quantize8x4(lo, qd + r * NB + c / 8, qc + r * S::QCS + 4 * c, leader);
-        quantize8x4(up, qd + r * NB + (HALF + 4 * c) / kQK, qc + r * S::QCS + HALF + 4 * c, leader);
-    }
+    fetch(tile0, kt_begin);
+    if (I::REM > 0 && 64 * wave < I::REM)
+        wait_vm<I::ROUNDS + 1>();
+    else
+        wait_vm<I::ROUNDS>();
     __syncthreads();
 
     // ---- per-lane B operands: the q codes of query l16, values 32b + 8lg ..
@@ -689,15 +740,17 @@ PrefillPlan plan_prefill(int hd, int g, int n_kv_heads, int pos0, int n) {
     return p;
 }
 
-template <int HD, int G, int NJ>
-hipError_t launch_hd_g(const PrefillArgs &a, int n_kv_heads, hipStream_t s) {
-    const int items = (a.qblocks + 1) / 2 * a.nsp;
-    hipLaunchKernelGGL((prefill_kernel<HD, G, NJ>), dim3(items * n_kv_heads), dim3(kThreads), 0, s, a);
-    return hipGetLastError();
+// Byte offset of the staged q blocks in the image buffer (after the key
+// tiles, 256-byte aligned).
+size_t qimg_offset(int head_dim, int n_kv_heads, int kend) {
+    const size_t tiles = (size_t)(kend + kKT - 1) / kKT;
+    const size_t per = head_dim == 64 ? TileImg<64>::BYTES : TileImg<128>::BYTES;
+    return (tiles * per * (size_t)n_kv_heads + 255) & ~(size_t)255;
 }
 
-template <int HD>
-hipError_t launch_hd(const TqPrefillArgs &t, const PrefillArgs &a, int g, hipStream_t s) {
+// The staging launch (key tiles and q blocks), then the attention.
+template <int HD, int G, int NJ>
+hipError_t launch_hd_g(const TqPrefillArgs &t, const PrefillArgs &a, hipStream_t s) {
     StageArgs st;
     st.view = t.view;
     st.seq = t.seq;
@@ -706,15 +759,31 @@ hipError_t launch_hd(const TqPrefillArgs &t, const PrefillArgs &a, int g, hipStr
     st.img = t.img;
     st.contig_first = t.contig_first;
     st.contig_pages = t.contig_pages;
-    hipLaunchKernelGGL((prefill_stage_kernel<HD>), dim3(a.n_tiles, t.n_kv_heads), dim3(kThreads), 0, s, st);
+    st.pos0 = t.pos0;
+    st.n = t.n;
+    st.qblocks = a.qblocks;
+    st.n_q_heads = t.n_q_heads;
+    st.q = t.q;
+    st.cos_t = t.cos_t;
+    st.sin_t = t.sin_t;
+    st.qimg = const_cast<unsigned char *>(a.qimg);
+    hipLaunchKernelGGL((prefill_stage_kernel<HD, G, NJ>), dim3(a.n_tiles + a.qblocks, t.n_kv_heads), dim3(kThreads),
+                       0, s, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    const int items = (a.qblocks + 1) / 2 * a.nsp;
+    hipLaunchKernelGGL((prefill_kernel<HD, G, NJ>), dim3(items * t.n_kv_heads), dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch_hd(const TqPrefillArgs &t, const PrefillArgs &a, int g, hipStream_t s) {
     const bool wide = prefill_rows(g) == 128;
     switch (g) {
-        case 1: return wide ? launch_hd_g<HD, 1, 2>(a, t.n_kv_heads, s) : launch_hd_g<HD, 1, 1>(a, t.n_kv_heads, s);
-        case 2: return wide ? launch_hd_g<HD, 2, 2>(a, t.n_kv_heads, s) : launch_hd_g<HD, 2, 1>(a, t.n_kv_heads, s);
-        case 4: return wide ? launch_hd_g<HD, 4, 2>(a, t.n_kv_heads, s) : launch_hd_g<HD, 4, 1>(a, t.n_kv_heads, s);
-        case 8: return launch_hd_g<HD, 8, 2>(a, t.n_kv_heads, s);
+        case 1: return wide ? launch_hd_g<HD, 1, 2>(t, a, s) : launch_hd_g<HD, 1, 1>(t, a, s);
+        case 2: return wide ? launch_hd_g<HD, 2, 2>(t, a, s) : launch_hd_g<HD, 2, 1>(t, a, s);
+        case 4: return wide ? launch_hd_g<HD, 4, 2>(t, a, s) : launch_hd_g<HD, 4, 1>(t, a, s);
+        case 8: return launch_hd_g<HD, 8, 2>(t, a, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -734,10 +803,10 @@ void tq_prefill_scratch(int head_dim, int group, int n_kv_heads, int pos0, int n
     *counter_ints = (size_t)n_kv_heads * p.qblocks * kCounterStrideP;
 }
 
-size_t tq_prefill_image_bytes(int head_dim, int n_kv_heads, int kend) {
-    const size_t tiles = (size_t)(kend + kKT - 1) / kKT;
-    const size_t per = head_dim == 64 ? TileImg<64>::BYTES : TileImg<128>::BYTES;
-    return tiles * per * (size_t)n_kv_heads;
+size_t tq_prefill_image_bytes(int head_dim, int group, int n_kv_heads, int pos0, int n) {
+    const PrefillPlan p = plan_prefill(head_dim, group, n_kv_heads, pos0, n);
+    const size_t qrow = head_dim == 64 ? PShape<64, 1, 1>::QCS + 2 * 4 : PShape<128, 1, 1>::QCS + 4 * 4;
+    return qimg_offset(head_dim, n_kv_heads, pos0 + n) + (size_t)n_kv_heads * p.qblocks * p.rows * qrow;
 }
 
 hipError_t tq_launch_prefill(const TqPrefillArgs &t, hipStream_t s) {
@@ -746,14 +815,12 @@ hipError_t tq_launch_prefill(const TqPrefillArgs &t, hipStream_t s) {
     PrefillArgs a;
     a.pos0 = t.pos0;
     a.n = t.n;
-    a.q = t.q;
-    a.cos_t = t.cos_t;
-    a.sin_t = t.sin_t;
     a.out = t.out;
     a.n_q_heads = t.n_q_heads;
     a.scale = t.scale;
     a.n_tiles = (t.pos0 + t.n + kKT - 1) / kKT;
     a.img = t.img;
+    a.qimg = t.img + qimg_offset(t.head_dim, t.n_kv_heads, t.pos0 + t.n);
     const PrefillPlan p = plan_prefill(t.head_dim, g, t.n_kv_heads, t.pos0, t.n);
     a.qblocks = p.qblocks;
     a.nsp = p.nsp;

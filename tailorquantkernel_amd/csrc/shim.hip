@@ -921,7 +921,7 @@ int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d
         seq_contig(kv, seq, &first, &pages);
         t.contig_first = pages > 0 ? first : -1;
         t.contig_pages = pages;
-        int rc = ensure_img(kv, tq_prefill_image_bytes(D.head_dim, D.n_kv_heads, pos0 + n));
+        int rc = ensure_img(kv, tq_prefill_image_bytes(D.head_dim, D.n_q_heads / D.n_kv_heads, D.n_kv_heads, pos0, n));
         if (rc != TQ_HIP_OK) return rc;
         size_t pbytes = 0, cn = 0;
         tq_prefill_scratch(D.head_dim, D.n_q_heads / D.n_kv_heads, D.n_kv_heads, pos0, n, &pbytes, &cn);

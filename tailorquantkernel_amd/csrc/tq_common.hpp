@@ -297,7 +297,7 @@ struct TqPrefillArgs {
     float scale;
     int contig_first;      // as in TqDecodeArgs
     int contig_pages;
-    unsigned char *img;    // tq_prefill_image_bytes() of scratch for the staged key tiles
+    unsigned char *img;    // tq_prefill_image_bytes() of scratch: the staged key tiles and q blocks
     float *partials;       // split-K partials (tq_prefill_scratch bytes)
     int *counters;         // split-K arrival counters, zero between launches
 };
@@ -308,5 +308,5 @@ void tq_prefill_scratch(int head_dim, int group, int n_kv_heads, int pos0, int n
 // The MFMA causal prefill covers head_dim 64/128, groups 1/2/4/8 and keys
 // [0, kend) up to 65536.
 bool tq_prefill_mfma_supported(int head_dim, int group, int kend);
-size_t tq_prefill_image_bytes(int head_dim, int n_kv_heads, int kend);
+size_t tq_prefill_image_bytes(int head_dim, int group, int n_kv_heads, int pos0, int n);
 hipError_t tq_launch_prefill(const TqPrefillArgs &a, hipStream_t s);
