@@ -176,6 +176,10 @@ struct StageArgs {
     const float *cos_t;  // [n][hd/2] or null
     const float *sin_t;
     unsigned char *qimg; // [n_kv][qblocks][PShape::Q_BYTES]
+    // the new K, V rows [n][n_kv][hd] (K pre-RoPE if cos_t), appended here;
+    // null: rows [pos0, pos0 + n) are already in the cache
+    const float *k_new;
+    const float *v_new;
 };
 
 template <int HD, int G, int NJ>
@@ -278,22 +282,97 @@ __global__ __launch_bounds__(kThreads) void prefill_stage_kernel(StageArgs a) {
         page[tid] = p;
     }
     __syncthreads();
+    // Rows of the tile: a new row (position in [pos0, kend) on a mapped page,
+    // with k_new given) is computed here and appended; an older one is read
+    // from the cache; every other row (past the keys, unmapped) is zero so that
+    // no stale scale reaches P.V.
+    const int t0 = kt * kKT;
+    auto fresh = [&](int p, int phys) { return a.k_new && p >= a.pos0 && p < a.kend && phys >= 0; };
     // a page's K (or V) rows are one contiguous run: copy them in CB-byte
-    // pieces, whole rows per piece; rows past the keys (or unmapped) are zero
-    // so that no stale scale reaches P.V
+    // pieces, whole rows per piece
     constexpr int CB = ROW % 16 == 0 ? 16 : 8;
     constexpr int PR = kPage * ROW / CB;   // pieces per page run
     typedef uint32_t piece_t __attribute__((ext_vector_type(CB / 4)));
     for (int i = tid; i < 2 * 2 * PR; i += kThreads) {
         const int kv = i / (2 * PR), pg = (i / PR) & 1, ch = i % PR;
-        const int p = kt * kKT + pg * kPage + (ch * CB) / ROW;
+        const int p = t0 + pg * kPage + (ch * CB) / ROW;
         const int phys = page[pg];
+        if (fresh(p, phys)) continue;
         piece_t x = piece_t(0u);
         if (p < a.kend && phys >= 0)
             x = *reinterpret_cast<const piece_t *>(head_run_ptr(v, phys, kvh) + kv * v.kv_chunk + ch * CB);
         *reinterpret_cast<piece_t *>(reinterpret_cast<unsigned char *>(raw[kv]) + pg * kPage * ROW + ch * CB) = x;
     }
+    // the new rows: store_kv's Q8 branch (model/attention_layer.c:66-90) with
+    // RoPE on K (:188), quantized exactly as quantize_row_q8 into the tile's
+    // LDS rows.  Task (row r, K|V, c) covers x[4c..4c+3] and its rotate-half
+    // partner x[HD/2+4c..+3]; the 8 lanes of a 32-value block share their row,
+    // so a whole block is computed or skipped together.
+    const bool has_new = a.k_new && t0 + kKT > a.pos0 && t0 < a.kend;
+    if (has_new) {
+        constexpr int HALF = HD / 2;
+        constexpr int CPR = HD / 8;
+        constexpr int TPT = kKT * 2 * CPR / kThreads;
+        static_assert(kKT * 2 * CPR % kThreads == 0 && CPR % 8 == 0, "whole tasks, whole blocks");
+        const bool rot = a.cos_t != nullptr;
+        v4f xl[TPT], xu[TPT], cs[TPT], sn[TPT];
+        bool mine[TPT];
+#pragma unroll
+        for (int t = 0; t < TPT; t++) {
+            const int task = tid + kThreads * t;
+            const int r = task / (2 * CPR), kv = (task / CPR) & 1, c = task % CPR;
+            const int p = t0 + r;
+            mine[t] = fresh(p, page[r / kPage]);
+            xl[t] = xu[t] = cs[t] = sn[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (mine[t]) {
+                const size_t row = (size_t)(p - a.pos0);
+                const float *src = (kv ? a.v_new : a.k_new) + (row * v.n_kv_heads + kvh) * HD;
+                xl[t] = *reinterpret_cast<const v4f *>(src + 4 * c);
+                xu[t] = *reinterpret_cast<const v4f *>(src + HALF + 4 * c);
+                if (!kv && rot) {
+                    cs[t] = *reinterpret_cast<const v4f *>(a.cos_t + row * HALF + 4 * c);
+                    sn[t] = *reinterpret_cast<const v4f *>(a.sin_t + row * HALF + 4 * c);
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TPT; t++) {
+            if (!mine[t]) continue;
+            const int task = tid + kThreads * t;
+            const int r = task / (2 * CPR), kv = (task / CPR) & 1, c = task % CPR;
+            float lo[4], up[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                if (!kv && rot) {
+                    lo[i] = rope_lower(xl[t][i], xu[t][i], cs[t][i], sn[t][i]);
+                    up[i] = rope_upper(xl[t][i], xu[t][i], cs[t][i], sn[t][i]);
+                } else {
+                    lo[i] = xl[t][i];
+                    up[i] = xu[t][i];
+                }
+            }
+            unsigned char *row = reinterpret_cast<unsigned char *>(raw[kv]) + r * ROW;
+            const bool leader = (c & 7) == 0;
+            const int bl = (4 * c) / kQK, bu = (HALF + 4 * c) / kQK;
+            quantize8x4(lo, reinterpret_cast<float *>(row + bl * kBlockBytes),
+                        row + bl * kBlockBytes + 4 + (4 * c) % kQK, leader);
+            quantize8x4(up, reinterpret_cast<float *>(row + bu * kBlockBytes),
+                        row + bu * kBlockBytes + 4 + (4 * c) % kQK, leader);
+        }
+    }
     __syncthreads();
+    if (has_new) {
+        // the new rows into the cache, whole rows
+        for (int i = tid; i < 2 * 2 * PR; i += kThreads) {
+            const int kv = i / (2 * PR), pg = (i / PR) & 1, ch = i % PR;
+            const int p = t0 + pg * kPage + (ch * CB) / ROW;
+            const int phys = page[pg];
+            if (!fresh(p, phys)) continue;
+            *reinterpret_cast<piece_t *>(head_run_ptr(v, phys, kvh) + kv * v.kv_chunk + ch * CB) =
+                *reinterpret_cast<const piece_t *>(reinterpret_cast<const unsigned char *>(raw[kv]) + pg * kPage * ROW +
+                                                   ch * CB);
+        }
+    }
     const unsigned char *rk = reinterpret_cast<const unsigned char *>(raw[0]);
     const unsigned char *rv = reinterpret_cast<const unsigned char *>(raw[1]);
     unsigned char *out = a.img + ((size_t)a.n_tiles * kvh + kt) * I::BYTES;
@@ -767,6 +846,8 @@ hipError_t launch_hd_g(const TqPrefillArgs &t, const PrefillArgs &a, hipStream_t
     st.cos_t = t.cos_t;
     st.sin_t = t.sin_t;
     st.qimg = const_cast<unsigned char *>(a.qimg);
+    st.k_new = t.k_new;
+    st.v_new = t.v_new;
     hipLaunchKernelGGL((prefill_stage_kernel<HD, G, NJ>), dim3(a.n_tiles + a.qblocks, t.n_kv_heads), dim3(kThreads),
                        0, s, st);
     hipError_t e = hipGetLastError();

@@ -896,15 +896,21 @@ int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d
     if (n == 1)
         return decode_common(kv, 1, nullptr, nullptr, 0, seq, 0, pos0, pos0 + 1, d_q, d_cos, d_sin, d_k, d_v,
                              d_out, s, seq);
-    TQ_TRY(tq_launch_append(kv->view, n, nullptr, nullptr, seq, pos0, d_k, d_v, d_cos, d_sin,
-                            kv->desc.head_dim, s));
     // the dense kernel restages every key tile of [0, pos0+n): worth it from a
     // few dozen new tokens on; shorter batches attend in the decode form
-    // the dense kernel moves q, cos/sin and out in 16-byte vectors
+    // the dense kernel moves q, cos/sin and out in 16-byte vectors; with 16-byte
+    // aligned k and v its staging launch appends the new rows too
     const bool aligned16 = (((uintptr_t)d_q | (uintptr_t)d_cos | (uintptr_t)d_sin | (uintptr_t)d_out) & 15) == 0;
-    if (prefill_dense() && n >= kPrefillDenseMin && aligned16 &&
-        tq_prefill_mfma_supported(D.head_dim, D.n_q_heads / D.n_kv_heads, pos0 + n)) {
+    const bool dense = prefill_dense() && n >= kPrefillDenseMin && aligned16 &&
+                       tq_prefill_mfma_supported(D.head_dim, D.n_q_heads / D.n_kv_heads, pos0 + n);
+    const bool fused = dense && (((uintptr_t)d_k | (uintptr_t)d_v) & 15) == 0;
+    if (!fused)
+        TQ_TRY(tq_launch_append(kv->view, n, nullptr, nullptr, seq, pos0, d_k, d_v, d_cos, d_sin,
+                                kv->desc.head_dim, s));
+    if (dense) {
         TqPrefillArgs t;
+        t.k_new = fused ? d_k : nullptr;
+        t.v_new = fused ? d_v : nullptr;
         t.view = kv->view;
         t.seq = seq;
         t.pos0 = pos0;

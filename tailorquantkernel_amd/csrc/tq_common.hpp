@@ -286,8 +286,10 @@ struct TqPrefillArgs {
     tq::PagedView view;
     int seq;
     int pos0;
-    int n;                 // tokens pos0 .. pos0+n-1 (already appended)
+    int n;                 // tokens pos0 .. pos0+n-1
     const float *q;        // [n][n_q_heads][hd]
+    const float *k_new;    // [n][n_kv_heads][hd] appended by the launch (K pre-RoPE if cos_t),
+    const float *v_new;    //   or null: already appended
     const float *cos_t;    // [n][hd/2] or null (q already rotated)
     const float *sin_t;
     float *out;            // [n][n_q_heads][hd]

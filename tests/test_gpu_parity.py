@@ -611,6 +611,52 @@ def test_prefill_scattered_pages(nat, oracle):
     kv.close()
 
 
+def test_prefill_unaligned_kv(nat, oracle):
+    """k and v 4 bytes off 16-byte alignment: the dense prefill then appends
+    the new rows in a launch of their own and stages them from the cache, so
+    the cache bytes and the outputs equal those of the aligned call (whose
+    staging launch appends them itself)."""
+    nq, nkv, hd, theta, pos0, n = 16, 4, 128, 5e5, 37, 250
+    nb = hd // QK
+    T = 320
+    lib = nat.load()
+    pre_k = oracle.quantize_row_q8(normal(nkv * T * hd, 41)).reshape(nkv, T, nb)
+    pre_v = oracle.quantize_row_q8(normal(nkv * T * hd, 42)).reshape(nkv, T, nb)
+    q, k, v = normal(n * nq * hd, 43), normal(n * nkv * hd, 44), normal(n * nkv * hd, 45)
+    cos = np.zeros((n, hd // 2), np.float32)
+    sin = np.zeros((n, hd // 2), np.float32)
+    for i in range(n):
+        cos[i], sin[i] = oracle.rope_table(hd, pos0 + i, theta)
+    D = nat.DeviceBuffer.from_numpy
+    pad = np.zeros(1, np.float32)
+    dq, dc, ds = D(q), D(cos), D(sin)
+    results = []
+    for off in (0, 4):
+        kv = nat.PagedKV.single(nq, nkv, hd, T)
+        kv.write(0, 0, pre_k, pre_v)
+        dk = D(np.concatenate([pad, k]) if off else k)
+        dv = D(np.concatenate([pad, v]) if off else v)
+        out = nat.DeviceBuffer(n * nq * hd * 4)
+        nat.check(lib.tq_hip_prefill_async(kv.h, 0, pos0, n, dq.ptr, dk.ptr + off, dv.ptr + off, dc.ptr, ds.ptr,
+                                           out.ptr, kv.stream), "prefill")
+        nat.check(lib.tq_hip_stream_synchronize(kv.stream), "sync")
+        gk, gv = kv.read(0, 0, T)
+        results.append((gk.tobytes(), gv.tobytes(), out.download((n, nq * hd), np.float32)))
+        for b in (dk, dv, out):
+            b.free()
+        kv.close()
+    (ka, va, oa), (kb, vb, ob) = results
+    assert ka == kb and va == vb, "cache bytes of the unaligned call"
+    assert ob.tobytes() == oa.tobytes(), "outputs of the unaligned call"
+    kc, vc = pre_k.reshape(-1).copy(), pre_v.reshape(-1).copy()
+    rc, out_ref = oracle.prefill_qkv(kc, vc, nq, nkv, hd, T, theta, pos0, n, q, k, v)
+    assert rc == 0
+    assert_close(oa, out_ref, "prefill, aligned k/v")
+    assert ka == kc.tobytes() and va == vc.tobytes()
+    for b in (dq, dc, ds):
+        b.free()
+
+
 def test_prefill_c4_sampled(nat, oracle):
     """The 8B-shape causal prefill of 2048 tokens: outputs of sampled tokens
     against attend_q8 of the oracle on the cache the prefill left (token i
