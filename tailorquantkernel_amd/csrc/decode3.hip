@@ -804,7 +804,9 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
 
     // Thread (unit u, split subset sg) sums splits sg, sg + NSG, ... of float4
     // unit u.  The first CL rows are requested together with (m, l), before
-    // the weights are known.
+    // the weights are known; only the rows of real splits are requested (the
+    // others stay 0), the weights of a pass are read together and the sum has
+    // no branch, so one wait covers a pass's loads.
     constexpr int NSG = L::U >= kThreads ? 1 : kThreads / L::U;
     constexpr int TPS = L::U >= kThreads ? kThreads : L::U;
     constexpr int CL = 16;
@@ -823,17 +825,17 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
     float *red = reinterpret_cast<float *>(&slot1[0][0]);     // [NSG][TPS][4]
     for (int u0 = 0; u0 < L::U; u0 += TPS) {
         const int u = u0 + tid % TPS;
+        const float *wt = sm.wts + ((4 * u) / HD) * kMaxSplits3;
         v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
         for (int s0 = 0; s0 < nvalid; s0 += NSG * CL) {
             v4f rows[CL];
 #pragma unroll
             for (int i = 0; i < CL; i++) {
-                // only the rows of real splits are requested
                 const int s = s0 + sg + NSG * i;
-                rows[i] = (active && s < nvalid) ? __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                            prs, (s * L::PSTRIDE + 4 * u) * 4, 0,
-                                                                            kCoherent))
-                                                 : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                rows[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                if (s < nvalid)
+                    rows[i] = __builtin_bit_cast(
+                        v4f, __builtin_amdgcn_raw_buffer_load_b128(prs, (s * L::PSTRIDE + 4 * u) * 4, 0, kCoherent));
             }
             if (u0 == 0 && s0 == 0) {
 #pragma unroll
@@ -849,13 +851,11 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
                 }
                 __syncthreads();
             }
-            const float *wt = sm.wts + ((4 * u) / HD) * kMaxSplits3;
+            float w[CL];
 #pragma unroll
-            for (int i = 0; i < CL; i++) {
-                // rows past nvalid are stale or zero: selected out, never weighted
-                const int s = s0 + sg + NSG * i;
-                if (s < nvalid) acc += wt[min(s, kMaxSplits3 - 1)] * rows[i];
-            }
+            for (int i = 0; i < CL; i++) w[i] = wt[min(s0 + sg + NSG * i, kMaxSplits3 - 1)];
+#pragma unroll
+            for (int i = 0; i < CL; i++) acc += (s0 + sg + NSG * i < nvalid ? w[i] : 0.0f) * rows[i];
         }
         if constexpr (NSG == 1) {
             const int h = (4 * u) / HD;
