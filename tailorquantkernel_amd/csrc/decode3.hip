@@ -762,16 +762,25 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
         single ? a.out : a.partials + pbase * L::PSTRIDE, 0, single ? 0 : a.n_splits * L::PSTRIDE * 4, kBufWord3);
     for (int u = tid; u < L::U; u += kThreads) {
         const int h = (4 * u) / HD, j = 4 * u - h * HD;
+        // every wave's (m, l, o) read at once: one LDS round trip
+        float mws[kWaves], lws[kWaves];
+        v4f ows[kWaves];
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            mws[w] = mw[w * G + h];
+            lws[w] = lw[w * G + h];
+            ows[w] = *reinterpret_cast<const v4f *>(ow + (w * G + h) * HD + j);
+        }
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) M = fmaxf(M, mw[w * G + h]);
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, mws[w]);
         v4f O = v4f{0.0f, 0.0f, 0.0f, 0.0f};
         float Lsum = 0.0f;
 #pragma unroll
         for (int w = 0; w < kWaves; w++) {
-            const float f = __builtin_amdgcn_exp2f(mw[w * G + h] - M);
-            O += f * *reinterpret_cast<const v4f *>(ow + (w * G + h) * HD + j);
-            Lsum += f * lw[w * G + h];
+            const float f = __builtin_amdgcn_exp2f(mws[w] - M);
+            O += f * ows[w];
+            Lsum += f * lws[w];
         }
         if (single) {
             *reinterpret_cast<v4f *>(a.out + (out_row + h) * HD + j) = O / Lsum;
