@@ -214,10 +214,14 @@ __device__ __forceinline__ void stage_q(const StageArgs &a, int kvh, int blk) {
     const int i0 = blk * S::QB;
     unsigned char *qc = a.qimg + ((size_t)kvh * a.qblocks + blk) * S::Q_BYTES;
     float *qd = reinterpret_cast<float *>(qc + S::RW * S::QCS);
-    v4f xl[TASKS], xu[TASKS], cs[TASKS], sn[TASKS];
+    constexpr int TB = TASKS > 4 ? 4 : TASKS;       // tasks whose loads are in flight together
+    static_assert(TASKS % TB == 0, "whole task batches");
 #pragma unroll
-    for (int t = 0; t < TASKS; t++) {
-        const int k = tid + kThreads * t;
+    for (int t0 = 0; t0 < TASKS; t0 += TB) {
+    v4f xl[TB], xu[TB], cs[TB], sn[TB];
+#pragma unroll
+    for (int t = 0; t < TB; t++) {
+        const int k = tid + kThreads * (t0 + t);
         const int r = k / CPR, c = k % CPR;
         const int nt = r >> 4;
         const int qi = i0 + (nt % S::QT) * 16 + (r & 15);
@@ -233,8 +237,8 @@ __device__ __forceinline__ void stage_q(const StageArgs &a, int kvh, int blk) {
         }
     }
 #pragma unroll
-    for (int t = 0; t < TASKS; t++) {
-        const int k = tid + kThreads * t;
+    for (int t = 0; t < TB; t++) {
+        const int k = tid + kThreads * (t0 + t);
         const int r = k / CPR, c = k % CPR;
         float lo[4], up[4];
 #pragma unroll
@@ -250,6 +254,7 @@ __device__ __forceinline__ void stage_q(const StageArgs &a, int kvh, int blk) {
         const bool leader = (c & 7) == 0;
         quantize8x4(lo, qd + r * NB + c / 8, qc + r * S::QCS + 4 * c, leader);
         quantize8x4(up, qd + r * NB + (HALF + 4 * c) / kQK, qc + r * S::QCS + HALF + 4 * c, leader);
+    }
     }
 }
 
