@@ -72,6 +72,7 @@ constexpr int kMaxSplitPages3 = 512;     // page ids a work-group stages (8,192 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;            // log2 headroom before the running max moves
 constexpr int kCoherent = 16;            // cache policy sc1: agent-coherent access
+constexpr int kSystem = 17;              // sc0 sc1: written through to memory, acknowledged at system scope
 constexpr int kBufWord3 = 0x00020000;    // raw buffer descriptor, 32-bit data
 constexpr int kCounterStride = TQ_DECODE_COUNTER_STRIDE;   // ints: one 256-byte line per counter
 constexpr int kSortQ = 128;              // ragged batches up to this many queries go longest first
@@ -757,6 +758,24 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
     const size_t out_row = (size_t)qi * a.n_q_heads + (size_t)kvh * G;
     const size_t pbase = ((size_t)qi * a.n_kv_heads + kvh) * a.n_splits;
     const bool single = a.n_splits == 1;
+    // Float4 f4 / 4 of this (query, kv head)'s G output rows.  With completion
+    // flags the rows are stored through to system scope, every wave waits for
+    // its acknowledgements, and then one lane raises the flag: a host that sees
+    // the flag finds the rows in its memory (and the kernel writes nothing after).
+    const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(a.out + out_row * HD, 0, G * HD * 4, kBufWord3);
+    auto put_out = [&](int f4, v4f val) {
+        if (a.done)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, val), ors, 4 * f4, 0, kSystem);
+        else
+            *reinterpret_cast<v4f *>(a.out + out_row * HD + f4) = val;
+    };
+    auto signal_done = [&]() {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0)
+            __hip_atomic_store(a.done + (size_t)qi * a.n_kv_heads + kvh, a.done_seq, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+    };
     // partial rows of this (query, kv head); accesses past n_splits rows read 0
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
         single ? a.out : a.partials + pbase * L::PSTRIDE, 0, single ? 0 : a.n_splits * L::PSTRIDE * 4, kBufWord3);
@@ -783,7 +802,7 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
             Lsum += f * lws[w];
         }
         if (single) {
-            *reinterpret_cast<v4f *>(a.out + (out_row + h) * HD + j) = O / Lsum;
+            put_out(4 * u, O / Lsum);
         } else {
             // (the buffer intrinsics move raw 32-bit words: floats go through bit casts)
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, O), prs, (split * L::PSTRIDE + 4 * u) * 4,
@@ -796,7 +815,10 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
             }
         }
     }
-    if (single) return;
+    if (single) {
+        if (a.done) signal_done();
+        return;
+    }
     __builtin_amdgcn_s_waitcnt(0);   // the partial is at the point of coherence
     __syncthreads();
 
@@ -867,21 +889,19 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
             for (int i = 0; i < CL; i++) acc += (s0 + sg + NSG * i < nvalid ? w[i] : 0.0f) * rows[i];
         }
         if constexpr (NSG == 1) {
-            const int h = (4 * u) / HD;
-            if (active) *reinterpret_cast<v4f *>(a.out + (out_row + h) * HD + (4 * u - h * HD)) = acc;
+            if (active) put_out(4 * u, acc);
         } else {
             *reinterpret_cast<v4f *>(red + 4 * tid) = acc;
             __syncthreads();
             if (tid < TPS) {
                 v4f r = *reinterpret_cast<const v4f *>(red + 4 * tid);
                 for (int g = 1; g < NSG; g++) r += *reinterpret_cast<const v4f *>(red + 4 * (g * TPS + tid));
-                const int uu = u0 + tid;
-                const int h = (4 * uu) / HD;
-                *reinterpret_cast<v4f *>(a.out + (out_row + h) * HD + (4 * uu - h * HD)) = r;
+                put_out(4 * (u0 + tid), r);
             }
             __syncthreads();
         }
     }
+    if (a.done) signal_done();
 }
 
 template <int HD, int G>

@@ -29,6 +29,8 @@ struct tq_hip_kv {
     unsigned char *stage = nullptr; // device staging for the synchronous calls
     unsigned char *hstage = nullptr;  // its pinned host mirror: one copy in, one out
     size_t stage_bytes = 0;
+    unsigned *hdone = nullptr;      // completion flags in coherent pinned memory
+    unsigned done_seq = 0;          // the value the last flagged call wrote
     unsigned char *img = nullptr;   // prefill key-tile images, grown on demand
     size_t img_bytes = 0;
     float *ppartials = nullptr;     // prefill split-K partials, grown on demand
@@ -279,16 +281,65 @@ struct Stage {
     }
 };
 
-// The synchronous entry points: host inputs are packed into the pinned mirror
-// and moved to the device staging area by one small copy kernel that reads the
-// mirror over the bus (a kernel launch costs less than a copy-engine transfer
-// of a few KB: 12.8 against 8.4 + ~4 us per round trip measured on MI355X,
-// where hipMemcpyAsync hands the copy to another engine and the next launch
-// waits on it).  Outputs of up to kDirectOut bytes are written by the kernel
-// itself into the pinned mirror, which the device sees at the same address,
-// so only the stream synchronization stands between the kernel and the
-// caller; larger outputs come back with one copy.
+// The synchronous entry points: host inputs are packed into the pinned mirror.
+// Up to kDirectIn bytes of them the decode kernel reads there itself, over the
+// bus (its L2 serves the work-groups that share a line); larger inputs are
+// moved to the device staging area first by one small copy kernel (a kernel
+// launch costs less than a copy-engine transfer of a few KB: 12.8 against
+// 8.4 + ~4 us per round trip measured on MI355X, where hipMemcpyAsync hands
+// the copy to another engine and the next launch waits on it).  Outputs of up
+// to kDirectOut bytes are written by the kernel itself into the pinned mirror,
+// which the device sees at the same address; larger outputs come back with one
+// copy.  The MFMA decode then raises one completion flag per (query, kv head)
+// in coherent pinned memory after its rows are acknowledged at system scope,
+// and the host spins on those flags rather than on the stream: 6.1 against
+// 9.5 us for an empty kernel's round trip on MI355X.
+constexpr size_t kDirectIn = 64u << 10;
 constexpr size_t kDirectOut = 64u << 10;
+constexpr int kDoneFlags = 4096;
+
+// Completion flags of one synchronous call: armed by decode_common when the
+// kernel it launches will raise them.
+struct DoneFlags {
+    unsigned *flags = nullptr;
+    unsigned seq = 0;
+    int count = 0;
+    bool armed = false;
+};
+
+int ensure_done(tq_hip_kv *kv) {
+    if (kv->hdone) return TQ_HIP_OK;
+    void *p = nullptr;
+    if (hipHostMalloc(&p, kDoneFlags * sizeof(unsigned), hipHostMallocCoherent) != hipSuccess) return TQ_HIP_ENOMEM;
+    memset(p, 0, kDoneFlags * sizeof(unsigned));
+    kv->hdone = static_cast<unsigned *>(p);
+    kv->done_seq = 0;
+    return TQ_HIP_OK;
+}
+
+// Flags for the next synchronous call on kv (never the value 0 they start at).
+DoneFlags next_done(tq_hip_kv *kv) {
+    DoneFlags d;
+    if (ensure_done(kv) != TQ_HIP_OK) return d;
+    if (++kv->done_seq == 0) kv->done_seq = 1;
+    d.flags = kv->hdone;
+    d.seq = kv->done_seq;
+    return d;
+}
+
+// Until every armed flag holds the call's value, or the stream has drained
+// (flags a query never raises, e.g. one with nothing to attend) or failed.
+int wait_done(tq_hip_kv *kv, const DoneFlags &d) {
+    for (unsigned it = 1;; it++) {
+        bool all = true;
+        for (int i = 0; i < d.count && all; i++) all = __atomic_load_n(d.flags + i, __ATOMIC_ACQUIRE) == d.seq;
+        if (all) return TQ_HIP_OK;
+        if ((it & 255u) == 0) {
+            const hipError_t e = hipStreamQuery(kv->stream);
+            if (e != hipErrorNotReady) return herr(e);
+        }
+    }
+}
 
 __global__ __launch_bounds__(256) void stage_in_kernel(const uint4 *src, uint4 *dst, size_t n) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) dst[i] = src[i];
@@ -309,12 +360,27 @@ int copy_in(tq_hip_kv *kv, size_t bytes) {
 float *out_slot(tq_hip_kv *kv, size_t off, size_t bytes) {
     return reinterpret_cast<float *>((bytes <= kDirectOut ? kv->hstage : kv->stage) + off);
 }
-int copy_out_sync(tq_hip_kv *kv, void *dst, size_t off, size_t bytes) {
+int copy_out_sync(tq_hip_kv *kv, void *dst, size_t off, size_t bytes, const DoneFlags *done = nullptr) {
     if (bytes > kDirectOut)
         TQ_TRY(hipMemcpyAsync(kv->hstage + off, kv->stage + off, bytes, hipMemcpyDeviceToHost, kv->stream));
-    TQ_TRY(hipStreamSynchronize(kv->stream));
+    if (bytes <= kDirectOut && done && done->armed) {
+        const int rc = wait_done(kv, *done);
+        if (rc != TQ_HIP_OK) return rc;
+    } else {
+        TQ_TRY(hipStreamSynchronize(kv->stream));
+    }
     memcpy(dst, kv->hstage + off, bytes);
     return TQ_HIP_OK;
+}
+// The inputs the kernel reads: the pinned mirror itself when they are small
+// (no copy kernel), else their device copy, made here.
+int inputs_at(tq_hip_kv *kv, size_t in_bytes, bool may_read_host, unsigned char **base) {
+    if (may_read_host && in_bytes <= kDirectIn) {
+        *base = kv->hstage;
+        return TQ_HIP_OK;
+    }
+    *base = kv->stage;
+    return copy_in(kv, in_bytes);
 }
 
 int capacity_of(const tq_hip_kv *kv, int seq);
@@ -345,7 +411,8 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
                   int seq_const, int seq_stride, int pos0, int max_len, const float *d_q, const float *d_cos,
                   const float *d_sin, const float *d_k, const float *d_v, float *d_out,
                   hipStream_t s, int contig_seq, const float *q_norm = nullptr,
-                  const float *k_norm = nullptr, float rms_eps = 0.0f, const CallScratch *scratch = nullptr) {
+                  const float *k_norm = nullptr, float rms_eps = 0.0f, const CallScratch *scratch = nullptr,
+                  DoneFlags *done = nullptr) {
     if (n_q <= 0) return TQ_HIP_OK;
     // queries and kv heads are grid dimensions y/z (at most 65535 each)
     if (n_q > 65535 || kv->desc.n_kv_heads > 65535) return TQ_HIP_EINVAL;
@@ -424,6 +491,12 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
             a.partials = kv->partials;
             a.counters = kv->counters;
         }
+    }
+    if (v3 && done && done->flags && (long)n_q * D.n_kv_heads <= kDoneFlags) {
+        a.done = done->flags;
+        a.done_seq = done->seq;
+        done->count = n_q * D.n_kv_heads;
+        done->armed = true;
     }
     return herr(v3 ? tq_launch_decode3(a, waves, s) : tq_launch_decode(a, s));
 }
@@ -680,6 +753,7 @@ void tq_hip_kv_destroy(tq_hip_kv *kv) {
     if (kv->counters) (void)hipFree(kv->counters);
     if (kv->stage) (void)hipFree(kv->stage);
     if (kv->hstage) (void)hipHostFree(kv->hstage);
+    if (kv->hdone) (void)hipHostFree(kv->hdone);
     if (kv->img) (void)hipFree(kv->img);
     if (kv->ppartials) (void)hipFree(kv->ppartials);
     if (kv->pcounters) (void)hipFree(kv->pcounters);
@@ -790,12 +864,12 @@ int tq_hip_kv_append(tq_hip_kv *kv, int seq, int pos, const float *k, const floa
     int rc = ensure_stage(kv, st.used);
     if (rc != TQ_HIP_OK) return rc;
     const hipStream_t s = kv->stream;
-    unsigned char *S = kv->stage;
+    unsigned char *S = nullptr;
     pack(kv, ok_, k, kvb);
     pack(kv, ov, v, kvb);
     pack(kv, oc, cos_t, tb);
     pack(kv, os, sin_t, tb);
-    rc = copy_in(kv, st.used);
+    rc = inputs_at(kv, st.used, true, &S);
     if (rc != TQ_HIP_OK) return rc;
     TQ_TRY(tq_launch_append(kv->view, 1, nullptr, nullptr, seq, pos, (const float *)(S + ok_),
                             (const float *)(S + ov), cos_t ? (const float *)(S + oc) : nullptr,
@@ -867,42 +941,48 @@ int tq_hip_attend(tq_hip_kv *kv, int seq, int pos, const float *q, const float *
     int rc = ensure_stage(kv, st.used);
     if (rc != TQ_HIP_OK) return rc;
     const hipStream_t s = kv->stream;
-    unsigned char *S = kv->stage;
+    unsigned char *S = nullptr;
     pack(kv, oq, q, qb);
     pack(kv, oc, cos_t, tb);
     pack(kv, os, sin_t, tb);
-    rc = copy_in(kv, in_bytes);
+    rc = inputs_at(kv, in_bytes, true, &S);
     if (rc != TQ_HIP_OK) return rc;
+    DoneFlags done;
+    if (qb <= kDirectOut) done = next_done(kv);
     rc = decode_common(kv, 1, nullptr, nullptr, 0, seq, 0, pos, pos + 1, (const float *)(S + oq),
                        cos_t ? (const float *)(S + oc) : nullptr, cos_t ? (const float *)(S + os) : nullptr,
-                       nullptr, nullptr, out_slot(kv, oo, qb), s, seq);
+                       nullptr, nullptr, out_slot(kv, oo, qb), s, seq, nullptr, nullptr, 0.0f, nullptr, &done);
     if (rc != TQ_HIP_OK) return rc;
-    return copy_out_sync(kv, out, oo, qb);
+    return copy_out_sync(kv, out, oo, qb, &done);
 }
 
 // ---- prefill ---------------------------------------------------------------------
 
-int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d_q, const float *d_k,
-                         const float *d_v, const float *d_cos, const float *d_sin, float *d_out,
-                         void *stream) {
-    if (!seq_ok(kv, seq) || !d_q || !d_k || !d_v || !d_out || ((d_cos == nullptr) != (d_sin == nullptr)))
-        return TQ_HIP_EINVAL;
-    // model/attention_layer.c:203-204
-    if (n <= 0 || pos0 < 0 || pos0 + n > capacity_of(kv, seq)) return TQ_HIP_EINVAL;
-    const hipStream_t s = pick(kv, stream);
+namespace {
+// Whether a prefill of n tokens at these pointers takes the dense kernel.
+bool prefill_takes_dense(const tq_hip_kv *kv, int pos0, int n, const float *d_q, const float *d_cos,
+                         const float *d_sin, const float *d_out) {
+    const tq_hip_kv_desc &D = kv->desc;
+    const bool aligned16 = (((uintptr_t)d_q | (uintptr_t)d_cos | (uintptr_t)d_sin | (uintptr_t)d_out) & 15) == 0;
+    return n > 1 && prefill_dense() && n >= kPrefillDenseMin && aligned16 &&
+           tq_prefill_mfma_supported(D.head_dim, D.n_q_heads / D.n_kv_heads, pos0 + n);
+}
+
+// tq_hip_prefill_async; `done` (the synchronous entry point's completion
+// flags) is armed when the decode form runs.
+int prefill_impl(tq_hip_kv *kv, int seq, int pos0, int n, const float *d_q, const float *d_k, const float *d_v,
+                 const float *d_cos, const float *d_sin, float *d_out, hipStream_t s, DoneFlags *done) {
     const tq_hip_kv_desc &D = kv->desc;
     // one token: store_kv + attend as the decode step, one launch
     // (model/attention_layer.c:221-236 with n == 1)
     if (n == 1)
         return decode_common(kv, 1, nullptr, nullptr, 0, seq, 0, pos0, pos0 + 1, d_q, d_cos, d_sin, d_k, d_v,
-                             d_out, s, seq);
+                             d_out, s, seq, nullptr, nullptr, 0.0f, nullptr, done);
     // the dense kernel restages every key tile of [0, pos0+n): worth it from a
     // few dozen new tokens on; shorter batches attend in the decode form
     // the dense kernel moves q, cos/sin and out in 16-byte vectors; with 16-byte
     // aligned k and v its staging launch appends the new rows too
-    const bool aligned16 = (((uintptr_t)d_q | (uintptr_t)d_cos | (uintptr_t)d_sin | (uintptr_t)d_out) & 15) == 0;
-    const bool dense = prefill_dense() && n >= kPrefillDenseMin && aligned16 &&
-                       tq_prefill_mfma_supported(D.head_dim, D.n_q_heads / D.n_kv_heads, pos0 + n);
+    const bool dense = prefill_takes_dense(kv, pos0, n, d_q, d_cos, d_sin, d_out);
     const bool fused = dense && (((uintptr_t)d_k | (uintptr_t)d_v) & 15) == 0;
     if (!fused)
         TQ_TRY(tq_launch_append(kv->view, n, nullptr, nullptr, seq, pos0, d_k, d_v, d_cos, d_sin,
@@ -939,7 +1019,18 @@ int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d
         return herr(tq_launch_prefill(t, s));
     }
     return decode_common(kv, n, nullptr, nullptr, 0, seq, 0, pos0, pos0 + n, d_q, d_cos, d_sin, nullptr, nullptr,
-                         d_out, s, seq);
+                         d_out, s, seq, nullptr, nullptr, 0.0f, nullptr, done);
+}
+}  // namespace
+
+int tq_hip_prefill_async(tq_hip_kv *kv, int seq, int pos0, int n, const float *d_q, const float *d_k,
+                         const float *d_v, const float *d_cos, const float *d_sin, float *d_out,
+                         void *stream) {
+    if (!seq_ok(kv, seq) || !d_q || !d_k || !d_v || !d_out || ((d_cos == nullptr) != (d_sin == nullptr)))
+        return TQ_HIP_EINVAL;
+    // model/attention_layer.c:203-204
+    if (n <= 0 || pos0 < 0 || pos0 + n > capacity_of(kv, seq)) return TQ_HIP_EINVAL;
+    return prefill_impl(kv, seq, pos0, n, d_q, d_k, d_v, d_cos, d_sin, d_out, pick(kv, stream), nullptr);
 }
 
 int tq_hip_prefill(tq_hip_kv *kv, int seq, int pos0, int n, const float *q, const float *k, const float *v,
@@ -957,19 +1048,28 @@ int tq_hip_prefill(tq_hip_kv *kv, int seq, int pos0, int n, const float *q, cons
     int rc = ensure_stage(kv, st.used);
     if (rc != TQ_HIP_OK) return rc;
     const hipStream_t s = kv->stream;
-    unsigned char *S = kv->stage;
     pack(kv, oq, q, qb);
     pack(kv, ok_, k, kvb);
     pack(kv, ov, v, kvb);
     pack(kv, oc, cos_t, tb);
     pack(kv, os, sin_t, tb);
-    rc = copy_in(kv, in_bytes);
+    // the decode form may read its inputs in host memory; the dense kernel
+    // streams them and takes the device copy (the staging offsets are 256-byte
+    // aligned in both, so the choice of form does not depend on it)
+    float *o = out_slot(kv, oo, qb);
+    const bool dense = prefill_takes_dense(kv, pos0, n, reinterpret_cast<const float *>(kv->stage + oq),
+                                           reinterpret_cast<const float *>(kv->stage + oc),
+                                           reinterpret_cast<const float *>(kv->stage + os), o);
+    unsigned char *S = nullptr;
+    rc = inputs_at(kv, in_bytes, !dense, &S);
     if (rc != TQ_HIP_OK) return rc;
-    rc = tq_hip_prefill_async(kv, seq, pos0, n, (const float *)(S + oq), (const float *)(S + ok_),
-                              (const float *)(S + ov), cos_t ? (const float *)(S + oc) : nullptr,
-                              cos_t ? (const float *)(S + os) : nullptr, out_slot(kv, oo, qb), s);
+    DoneFlags done;
+    if (!dense && qb <= kDirectOut) done = next_done(kv);
+    rc = prefill_impl(kv, seq, pos0, n, (const float *)(S + oq), (const float *)(S + ok_), (const float *)(S + ov),
+                      cos_t ? (const float *)(S + oc) : nullptr, cos_t ? (const float *)(S + os) : nullptr, o, s,
+                      &done);
     if (rc != TQ_HIP_OK) return rc;
-    return copy_out_sync(kv, out, oo, qb);
+    return copy_out_sync(kv, out, oo, qb, &done);
 }
 
 

@@ -235,6 +235,11 @@ struct TqDecodeArgs {
     int len_plus;            // step mode passes positions and 1 here
     int contig_first;        // >= 0: every query reads one sequence whose logical
     int contig_pages;        // page lp < contig_pages is physical contig_first + lp
+    // Completion flags for a host that waits on memory instead of the stream
+    // (MFMA kernel only), or null: the rows of (query i, kv head h) are stored
+    // at system scope and acknowledged, then done[i * n_kv_heads + h] = done_seq.
+    unsigned *done;
+    unsigned done_seq;
 };
 
 hipError_t tq_launch_quantize(const float *x, block_q8 *out, int n, hipStream_t s);
