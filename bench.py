@@ -1137,7 +1137,8 @@ def bench_layer_prefill_8b(args, nat, hip):
     parity = {"ok": bool(max(errs) <= 1e-2 and float(np.median(errs)) <= 1e-3), "median_rel_l2": float(np.median(errs)),
               "max_rel_l2": float(max(errs)), "bar": "per-token relative L2 <= 1e-2, median <= 1e-3",
               "against": "oracle attention_layer (bit-exact with the reference's), first 64 tokens"}
-    steps = max(3, args.steps // 400)
+    # at least 100 timed layer steps (about 56 ms), like the other workloads
+    steps = max(100, args.steps // 400)
     ms = timed(hip, stream, steps, step)
     hip.sync()
     weight_bytes = sum(m.nbytes for m in mats)
