@@ -161,6 +161,8 @@ struct GemvArgs {
     unsigned char *xq_out;    // where work-group 0 leaves quantize_row_q8(x), or null
     int n_tok;                // rows of input in this launch (<= T)
     bool q4;                  // the matrices are tiled Q4 (else tiled Q8)
+    bool uni_tiles;           // GEMM: every 128-row tile lies in one segment and every
+                              // segment's codes and scales are under 2 GiB
 };
 
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
@@ -199,6 +201,29 @@ __device__ __forceinline__ void dma4(const void *src, unsigned char *dst) {
         "global_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
         : "=&s"(saved)
         : "v"(src), "s"(lds)
+        : "memory");
+}
+
+// The same copies from a uniform base plus a 32-bit lane offset (the saddr
+// form): no per-lane 64-bit address arithmetic.  base and dst are uniform.
+__device__ __forceinline__ void dma16s(const unsigned char *base, uint32_t off, unsigned char *dst) {
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_u8 *)dst;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(base), "s"(lds)
+        : "memory");
+}
+__device__ __forceinline__ void dma4s(const unsigned char *base, uint32_t off, unsigned char *dst) {
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_u8 *)dst;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\t"
+        "global_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(base), "s"(lds)
         : "memory");
 }
 
@@ -437,8 +462,9 @@ __device__ __forceinline__ long lds_pair(const unsigned char *p) {
 // copy per thread instead of two); each lane turns its 8 bytes into 16 x its
 // 8 codes (low nibbles for k < 16, high for k >= 16), and the int32 products
 // are shifted back by 4 before scaling.
-template <bool BX4, bool Q4>
+template <bool BX4, bool Q4, bool UNI>
 __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
+    static_assert(!UNI || BX4, "uniform copies need whole 16-byte stages");
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -469,6 +495,37 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
         drow = reinterpret_cast<const float *>(w + (size_t)rows * rowb) + (size_t)lr * nb;
     }
 
+    // Copies from uniform bases, when every tile lies in one segment (the
+    // host checks that segment ends fall on tile boundaries and that offsets
+    // fit 32 bits) and every stage is whole (16-byte token rows, nb % 4 == 0):
+    // a stage's four blocks then lie in one 64-block group, the block and
+    // half of each copy are the same for the whole wave, and a copy is a
+    // scalar base (segment, group, block, half) plus this lane's fixed row
+    // offset, with no vector address arithmetic per stage.
+    constexpr bool uni = UNI;
+    const unsigned char *useg = nullptr;   // the tile's segment: codes, then scales at uscale
+    size_t uscale = 0;
+    uint32_t vrow = 0, vdrow = 0, vb[kGemmBRounds];
+    if constexpr (uni) {
+        const bool s0 = row0 < a.seg_end[0], s1 = !s0 && row0 < a.seg_end[1];
+        useg = s0 ? a.seg[0].w : (s1 ? a.seg[1].w : a.seg[2].w);
+        const int rows = s0 ? a.seg[0].rows : (s1 ? a.seg[1].rows : a.seg[2].rows);
+        const int start = s0 ? 0 : (s1 ? a.seg_end[0] : a.seg_end[1]);
+        const int r = row0 + my_row < a.rows_total ? row0 + my_row : a.rows_total - 1;
+        const uint32_t rowb = Q4 ? (uint32_t)cols / 2 : (uint32_t)cols;
+        uscale = (size_t)rows * rowb;
+        vrow = (uint32_t)(r - start) * rowb;
+        vdrow = (uint32_t)(r - start) * (uint32_t)nb * 4u;
+#pragma unroll
+        for (int j = 0; j < kGemmBRounds; j++) {
+            const int c = tid + kGemmThreads * j;
+            const int cc = c < kGemmBChunks ? c : kGemmBChunks - 1;
+            const int tk = cc / 9, piece = cc - 9 * tk;
+            const int t = tok0 + tk < a.n_tok ? tok0 + tk : a.n_tok - 1;
+            vb[j] = (uint32_t)t * (uint32_t)nb * (uint32_t)kBlockBytes + 16u * (uint32_t)piece;
+        }
+    }
+
     // The token rows' sources of this thread's B copies, fixed over the stages
     // (a stage only adds 36 bytes per block to each).
     const unsigned char *bsrc[kGemmBRounds];
@@ -483,8 +540,36 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
         }
     }
 
+    // the same copies from uniform bases (whole stages only)
+    auto issue_uni = [&](int st, unsigned char *buf) {
+        const int b0 = st * kGemmKB;
+        const int g = b0 / kGroupBlocks, i0 = b0 - g * kGroupBlocks;
+        const int n = nb - g * kGroupBlocks < kGroupBlocks ? nb - g * kGroupBlocks : kGroupBlocks;
+        if (Q4) {
+            // chunk tid -> (block tid / 128, row tid % 128): the block is the wave's
+            dma16s(useg + 16 * (b0 + (wave >> 1)), vrow, buf + 16 * 64 * wave);
+        } else {
+#pragma unroll
+            for (int j = 0; j < kGemmA / 16 / kGemmThreads; j++) {
+                const int c = 64 * wave + kGemmThreads * j;   // the wave's first chunk
+                const int blk = c >> 8, half = (c >> 7) & 1;
+                dma16s(useg + g * kGroupBytes + 16 * (i0 + blk) + (half ? 16 * n : 0), vrow, buf + 16 * c);
+            }
+        }
+        dma4s(useg + uscale + 4 * (b0 + (wave >> 1)), vdrow, buf + kGemmA + 4 * 64 * wave);
+#pragma unroll
+        for (int j = 0; j < kGemmBRounds; j++) {
+            const int c = 64 * wave + kGemmThreads * j;
+            if (c < kGemmBChunks) dma16s(a.xq + (size_t)b0 * kBlockBytes, vb[j], buf + kGemmA + kGemmWD + 16 * c);
+        }
+    };
+
     // kGemmCopies direct-to-LDS copies per thread per stage, nothing else
     auto issue = [&](int st, unsigned char *buf) {
+        if constexpr (uni) {
+            issue_uni(st, buf);
+            return;
+        }
         const int b0 = st * kGemmKB;
         if (Q4) {
             // chunk tid -> (block tid / 128, row tid % 128)
@@ -546,7 +631,8 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
         // overlap the first one's scaling
 #pragma unroll 2
         for (int blk = 0; blk < kGemmKB; blk++) {
-            const bool valid = st * kGemmKB + blk < nb;
+            // (with 16-byte token rows every stage is whole)
+            const bool valid = BX4 || st * kGemmKB + blk < nb;
             long av[2], bv[4];
             float wd[2][4], xd[4];
 #pragma unroll
@@ -713,25 +799,39 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t s) {
     const size_t lds = (size_t)kGemmBufs * kGemmStage;
     static bool opted = false;
     if (!opted) {
-        for (const void *f : {(const void *)gemm_q8_kernel<true, false>, (const void *)gemm_q8_kernel<false, false>,
-                              (const void *)gemm_q8_kernel<true, true>, (const void *)gemm_q8_kernel<false, true>}) {
+        for (const void *f :
+             {(const void *)gemm_q8_kernel<true, false, false>, (const void *)gemm_q8_kernel<false, false, false>,
+              (const void *)gemm_q8_kernel<true, true, false>, (const void *)gemm_q8_kernel<false, true, false>,
+              (const void *)gemm_q8_kernel<true, false, true>, (const void *)gemm_q8_kernel<true, true, true>}) {
             const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
             if (e != hipSuccess) return e;
         }
         opted = true;
     }
     const bool bx4 = (((uintptr_t)a.xq & 15) == 0) && a.nb % kGemmKB == 0;
+    GemvArgs u = a;
+    u.uni_tiles = true;
+    for (int i = 0; i < kMaxSegs; i++) {
+        if (a.seg_end[i] < a.rows_total && a.seg_end[i] % kGemmRows != 0) u.uni_tiles = false;
+        const size_t rowb = a.q4 ? (size_t)a.cols / 2 : (size_t)a.cols;
+        if ((size_t)a.seg[i].rows * (rowb + 4 * (size_t)a.nb) >= ((size_t)1 << 31)) u.uni_tiles = false;
+    }
+    if ((size_t)a.n_tok * a.nb * kBlockBytes >= ((size_t)1 << 31)) u.uni_tiles = false;
     const dim3 g((unsigned)grid), b(kGemmThreads);
     if (a.q4) {
-        if (bx4)
-            hipLaunchKernelGGL((gemm_q8_kernel<true, true>), g, b, lds, s, a);
+        if (bx4 && u.uni_tiles)
+            hipLaunchKernelGGL((gemm_q8_kernel<true, true, true>), g, b, lds, s, u);
+        else if (bx4)
+            hipLaunchKernelGGL((gemm_q8_kernel<true, true, false>), g, b, lds, s, u);
         else
-            hipLaunchKernelGGL((gemm_q8_kernel<false, true>), g, b, lds, s, a);
+            hipLaunchKernelGGL((gemm_q8_kernel<false, true, false>), g, b, lds, s, u);
     } else {
-        if (bx4)
-            hipLaunchKernelGGL((gemm_q8_kernel<true, false>), g, b, lds, s, a);
+        if (bx4 && u.uni_tiles)
+            hipLaunchKernelGGL((gemm_q8_kernel<true, false, true>), g, b, lds, s, u);
+        else if (bx4)
+            hipLaunchKernelGGL((gemm_q8_kernel<true, false, false>), g, b, lds, s, u);
         else
-            hipLaunchKernelGGL((gemm_q8_kernel<false, false>), g, b, lds, s, a);
+            hipLaunchKernelGGL((gemm_q8_kernel<false, false, false>), g, b, lds, s, u);
     }
     return hipGetLastError();
 }

@@ -189,9 +189,10 @@ def test_matmul_vs_oracle(nat, oracle, rows, cols, n_tok):
 
 @pytest.mark.parametrize("rows,cols,n_tok", [(256, 512, 16), (1027, 96, 17), (7, 64, 64), (10, 32, 65),
                                              (4096, 4096, 256), (100, 2080, 100), (1024, 8192, 300),
-                                             (6144, 4096, 192)])
+                                             (6144, 4096, 192), (300, 2176, 48)])
 def test_gemm_vs_oracle(nat, oracle, rows, cols, n_tok):
-    """From 16 tokens on the MFMA GEMM runs: ragged row, token and block tails."""
+    """From 16 tokens on the MFMA GEMM runs: ragged row, token and block tails
+    (2176 columns: a last 64-block group of 4 blocks in the tiled layout)."""
     Wq = random_weights(oracle, rows, cols, 3 * rows + cols)
     rng = np.random.default_rng(rows + cols + n_tok)
     x = rng.standard_normal((n_tok, cols)).astype(np.float32)
@@ -239,8 +240,10 @@ def test_unaligned_activation_rows(nat, oracle, cols, n_tok):
 @pytest.mark.parametrize("nq,nkv,hd,hidden,n_tok", [(32, 8, 128, 4096, 1), (32, 8, 128, 4096, 4),
                                                     (8, 2, 64, 256, 3), (6, 2, 32, 160, 1),
                                                     (64, 8, 128, 8192, 1), (32, 8, 128, 4096, 40),
-                                                    (8, 2, 64, 256, 130)])
+                                                    (8, 2, 64, 256, 130), (8, 2, 32, 256, 40)])
 def test_project_qkv_and_output(nat, oracle, nq, nkv, hd, hidden, n_tok):
+    """(8, 2, 32, 256, 40): q/k/v segments end at rows 256, 320 and 384, so a
+    128-row GEMM tile spans two segments (the per-row copy addressing)."""
     lib = nat.load()
     qr, kr = nq * hd, nkv * hd
     wq = random_weights(oracle, qr, hidden, 1)
