@@ -783,11 +783,21 @@ hipError_t launch_gemv(const GemvArgs &a, int tcap, bool xf, int rw, int gc, hip
     }
 }
 
-// From this many tokens on (block_q8 input) the MFMA GEMM runs instead of
-// GEMV launches of up to 8 tokens (TQ_HIP_GEMM_MIN_TOKENS overrides).
-int gemm_min_tokens() {
+// From how many tokens on (block_q8 input) the MFMA GEMM runs instead of GEMV
+// launches of tmax tokens each (TQ_HIP_GEMM_MIN_TOKENS overrides).  A GEMV
+// launch streams the weights once (about 5 TB/s, plus 2 us of launch), so
+// its cost grows with the token count; the GEMM's first round of 128-row
+// tiles costs its K loop, about 0.0183 us per column on MI355X, whatever the
+// token count.  Measured crossovers: 6144 x 4096 between 64 and 96 tokens
+// (77 against 62 us at 64), 28672 x 4096 between 16 and 32, 4096 x 14336
+// between 64 and 96; the model below puts them at 80, 22 and 70.
+int gemm_min_tokens(int rows, int cols, int tmax) {
     const int v = env_int("TQ_HIP_GEMM_MIN_TOKENS", 0);
-    return v > 0 ? v : 16;
+    if (v > 0) return v;
+    const double chunk_us = (double)rows * cols * (kBlockBytes / (double)kQK) / 5.0e6 + 2.0;
+    const double gemm_us = 0.0183 * cols + 2.0;
+    const int n = (int)(tmax * gemm_us / chunk_us) + 1;
+    return n < 16 ? 16 : (n > 256 ? 256 : n);
 }
 
 hipError_t launch_gemm(const GemvArgs &a, hipStream_t s) {
@@ -841,7 +851,7 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t s) {
 // launch quantizes its rows in LDS.
 int run_gemv(GemvArgs a, int n_tok, hipStream_t s) {
     const bool xf = a.x != nullptr;
-    if (!xf && n_tok >= gemm_min_tokens()) {
+    if (!xf && n_tok >= gemm_min_tokens(a.rows_total, a.cols, pick_tokens(a.nb, false))) {
         if ((size_t)n_tok * a.nb > (size_t)INT32_MAX / kBlockBytes) return TQ_HIP_EINVAL;
         a.n_tok = n_tok;
         return herr(launch_gemm(a, s));

@@ -129,7 +129,9 @@ def test_q4_layout_pack_unpack(nat, oracle):
                                              (6144, 4096, 1), (4096, 14336, 1), (28672, 4096, 1), (33, 160, 7),
                                              (64, 2048, 4), (300, 4096, 2), (256, 512, 16), (1000, 1024, 40),
                                              (130, 96, 17), (4096, 4096, 130)])
-def test_q4_matmul(nat, oracle, rows, cols, n_tok):
+def test_q4_matmul(nat, oracle, rows, cols, n_tok, monkeypatch):
+    """From 16 tokens on the GEMM is forced (the default may pick GEMV launches)."""
+    monkeypatch.setenv("TQ_HIP_GEMM_MIN_TOKENS", "16")
     rng = np.random.default_rng(rows + 7 * cols + n_tok)
     W = rng.standard_normal((rows, cols)).astype(np.float32)
     W[rows // 2, :QK] = 0.0

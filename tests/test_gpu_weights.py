@@ -190,21 +190,25 @@ def test_matmul_vs_oracle(nat, oracle, rows, cols, n_tok):
 @pytest.mark.parametrize("rows,cols,n_tok", [(256, 512, 16), (1027, 96, 17), (7, 64, 64), (10, 32, 65),
                                              (4096, 4096, 256), (100, 2080, 100), (1024, 8192, 300),
                                              (6144, 4096, 192), (300, 2176, 48)])
-def test_gemm_vs_oracle(nat, oracle, rows, cols, n_tok):
-    """From 16 tokens on the MFMA GEMM runs: ragged row, token and block tails
-    (2176 columns: a last 64-block group of 4 blocks in the tiled layout)."""
+def test_gemm_vs_oracle(nat, oracle, rows, cols, n_tok, monkeypatch):
+    """The MFMA GEMM (forced from 16 tokens on): ragged row, token and block
+    tails (2176 columns: a last 64-block group of 4 blocks in the tiled
+    layout); then the default choice between the GEMM and GEMV launches."""
     Wq = random_weights(oracle, rows, cols, 3 * rows + cols)
     rng = np.random.default_rng(rows + cols + n_tok)
     x = rng.standard_normal((n_tok, cols)).astype(np.float32)
     xq = quantize_tokens(oracle, x, n_tok, cols)
     M = Matrix(nat, Wq, rows, cols)
-    y = gpu_matmul(nat, M, xq, n_tok)
     ref = oracle.matmul_q8(Wq, xq, rows, cols, n_tok)
+    monkeypatch.setenv("TQ_HIP_GEMM_MIN_TOKENS", "16")
+    y = gpu_matmul(nat, M, xq, n_tok)
     check_matmul(y, ref, Wq, xq, rows, cols, n_tok, f"gemm {rows}x{cols} n_tok={n_tok}")
     # a token's row does not depend on the rest of the batch
     nb = cols // QK
     y16 = gpu_matmul(nat, M, xq[:16 * nb], 16)
     assert y16.tobytes() == y[:16].tobytes()
+    monkeypatch.delenv("TQ_HIP_GEMM_MIN_TOKENS")
+    check_matmul(gpu_matmul(nat, M, xq, n_tok), ref, Wq, xq, rows, cols, n_tok, f"default {rows}x{cols} n_tok={n_tok}")
 
 
 @pytest.mark.parametrize("rw", ["1", "2", "4"])
@@ -220,8 +224,9 @@ def test_rows_per_wave_identical(nat, oracle, rw, monkeypatch):
 
 
 @pytest.mark.parametrize("cols,n_tok", [(96, 3), (128, 20), (4096, 40)])
-def test_unaligned_activation_rows(nat, oracle, cols, n_tok):
+def test_unaligned_activation_rows(nat, oracle, cols, n_tok, monkeypatch):
     """block_q8 activations at a 4-byte (not 16-byte) aligned address (GEMV and GEMM)."""
+    monkeypatch.setenv("TQ_HIP_GEMM_MIN_TOKENS", "16")
     rows = 300
     Wq = random_weights(oracle, rows, cols, 77)
     xq = quantize_tokens(oracle, fill_random(n_tok * cols, 78, 1.0), n_tok, cols)
