@@ -163,6 +163,9 @@ struct GemvArgs {
     bool q4;                  // the matrices are tiled Q4 (else tiled Q8)
     bool uni_tiles;           // GEMM: every 128-row tile lies in one segment and every
                               // segment's codes and scales are under 2 GiB
+    float *part;              // GEMM split-K partial tiles [ksplit][n_tok][rows_total], or null
+    size_t part_floats;       // their capacity
+    int ksplit;               // GEMM: K splits of this launch (1: none)
 };
 
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
@@ -472,11 +475,17 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
     const int cols = a.cols, nb = a.nb;
     const int n_tt = (a.n_tok + kGemmToks - 1) / kGemmToks;
     const int n_rt = (a.rows_total + kGemmRows - 1) / kGemmRows;
-    const int k = blockIdx.x >> 3;
-    const int rt = (k / n_tt) * 8 + (blockIdx.x & 7), tt = k % n_tt;
+    // split ks of ksplit takes the ks-th run of stages; the grid repeats the
+    // tile order once per split (a multiple of 8 work-groups each, so the XCD
+    // of a tile is the same in every split)
+    const int g0 = gridDim.x / a.ksplit;
+    const int bx = blockIdx.x % g0, ks = blockIdx.x / g0;
+    const int k = bx >> 3;
+    const int rt = (k / n_tt) * 8 + (bx & 7), tt = k % n_tt;
     if (rt >= n_rt) return;   // the padding of the last row of XCD groups
     const int row0 = rt * kGemmRows, tok0 = tt * kGemmToks;
     const int stages = (nb + kGemmKB - 1) / kGemmKB;
+    const int st_begin = ks * stages / a.ksplit, st_end = (ks + 1) * stages / a.ksplit;
     const int wr = 32 * (wave & 3), wt = 64 * (wave >> 2);
 
     // A chunk c = tid + 512 j -> (block c / 256, half (c / 128) & 1, row c % 128):
@@ -620,12 +629,12 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
 
     // Two buffers (73.7 KB, so two work-groups share a CU): stage st+1 is
     // copied while stage st is multiplied.
-    issue(0, smem);
-    for (int st = 0; st < stages; st++) {
-        unsigned char *buf = smem + (st & 1) * kGemmStage;
+    issue(st_begin, smem);
+    for (int st = st_begin; st < st_end; st++) {
+        unsigned char *buf = smem + ((st - st_begin) & 1) * kGemmStage;
         wait_vm<0>();      // this wave's copies of stage st have landed
         __syncthreads();   // stage st is in LDS everywhere; stage st-1's buffer is free
-        if (st + 1 < stages) issue(st + 1, smem + ((st + 1) & 1) * kGemmStage);
+        if (st + 1 < st_end) issue(st + 1, smem + ((st + 1 - st_begin) & 1) * kGemmStage);
         const unsigned char *A = buf, *WD = buf + kGemmA, *B = buf + kGemmA + kGemmWD;
         // two blocks at a time: the second block's LDS reads and products
         // overlap the first one's scaling
@@ -680,7 +689,22 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
     }
 
     // y[t][r]: lane (l16, lg) holds rows 4lg..4lg+3 of each 16-row tile for
-    // token l16 of each 16-token tile.
+    // token l16 of each 16-token tile.  A split writes its partial instead.
+    if (a.ksplit > 1) {
+        float *p = a.part + (size_t)ks * a.n_tok * a.rows_total;
+#pragma unroll
+        for (int r2 = 0; r2 < 2; r2++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = row0 + wr + 16 * r2 + 4 * lg + i;
+#pragma unroll
+                for (int t4 = 0; t4 < 4; t4++) {
+                    const int t = tok0 + wt + 16 * t4 + l16;
+                    if (r < a.rows_total && t < a.n_tok) p[(size_t)t * a.rows_total + r] = acc[r2][t4][i];
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int r2 = 0; r2 < 2; r2++) {
 #pragma unroll
@@ -697,6 +721,22 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
                 if (t < a.n_tok) y[(size_t)t * rows + lr] = acc[r2][t4][i];
             }
         }
+    }
+}
+
+// The split-K sum: y of (token t, row r) is the splits' partials added in
+// split order (the same order on every launch).
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemvArgs a) {
+    const size_t total = (size_t)a.n_tok * a.rows_total;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+        float acc = a.part[i];
+        for (int s = 1; s < a.ksplit; s++) acc += a.part[(size_t)s * total + i];
+        const int t = (int)(i / a.rows_total), r = (int)(i - (size_t)t * a.rows_total);
+        const bool s0 = r < a.seg_end[0], s1 = !s0 && r < a.seg_end[1];
+        float *y = s0 ? a.seg[0].y : (s1 ? a.seg[1].y : a.seg[2].y);
+        const int rows = s0 ? a.seg[0].rows : (s1 ? a.seg[1].rows : a.seg[2].rows);
+        const int lr = r - (s0 ? 0 : (s1 ? a.seg_end[0] : a.seg_end[1]));
+        y[(size_t)t * rows + lr] = acc;
     }
 }
 
@@ -800,11 +840,11 @@ int gemm_min_tokens(int rows, int cols, int tmax) {
     return n < 16 ? 16 : (n > 256 ? 256 : n);
 }
 
-hipError_t launch_gemm(const GemvArgs &a, hipStream_t s) {
+hipError_t launch_gemm(const GemvArgs &a, int ksplit, hipStream_t s) {
     const int n_rt = (a.rows_total + kGemmRows - 1) / kGemmRows;
     const int n_tt = (a.n_tok + kGemmToks - 1) / kGemmToks;
     const long groups = ((long)n_rt + 7) / 8;   // row tiles per XCD, rounded up
-    const long grid = groups * 8 * n_tt;
+    const long grid = groups * 8 * n_tt * ksplit;
     if (grid > INT32_MAX) return hipErrorInvalidValue;
     const size_t lds = (size_t)kGemmBufs * kGemmStage;
     static bool opted = false;
@@ -820,6 +860,7 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t s) {
     }
     const bool bx4 = (((uintptr_t)a.xq & 15) == 0) && a.nb % kGemmKB == 0;
     GemvArgs u = a;
+    u.ksplit = ksplit;
     u.uni_tiles = true;
     for (int i = 0; i < kMaxSegs; i++) {
         if (a.seg_end[i] < a.rows_total && a.seg_end[i] % kGemmRows != 0) u.uni_tiles = false;
@@ -843,7 +884,29 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t s) {
         else
             hipLaunchKernelGGL((gemm_q8_kernel<false, false, false>), g, b, lds, s, u);
     }
+    if (ksplit > 1) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const size_t total = (size_t)a.n_tok * a.rows_total;
+        const size_t blocks = (total + 255) / 256 < 2048 ? (total + 255) / 256 : 2048;
+        hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, u);
+    }
     return hipGetLastError();
+}
+
+// Split-K GEMM for a few tokens (one 128-token tile): the row tiles alone
+// leave most of the 256 CUs idle and each runs the whole K loop, so K is cut
+// into S runs of stages, enough for about 512 work-groups (two per CU), each
+// writing a partial tile that one more launch sums in split order.
+constexpr int kSplitTargetWgs = 512;
+
+int gemm_ksplit(int rows, int cols, int n_tok) {
+    if (n_tok < 16 || n_tok > kGemmToks) return 1;
+    const long wgs = ((long)(rows + kGemmRows - 1) / kGemmRows + 7) / 8 * 8;
+    const int stages = (cols / kQK + kGemmKB - 1) / kGemmKB;
+    long sp = (kSplitTargetWgs + wgs - 1) / wgs;
+    if (sp > stages) sp = stages;
+    return sp < 2 ? 1 : (int)sp;
 }
 
 // Runs the matmul over all tokens: one GEMM launch for many block_q8 rows,
@@ -851,10 +914,14 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t s) {
 // launch quantizes its rows in LDS.
 int run_gemv(GemvArgs a, int n_tok, hipStream_t s) {
     const bool xf = a.x != nullptr;
-    if (!xf && n_tok >= gemm_min_tokens(a.rows_total, a.cols, pick_tokens(a.nb, false))) {
+    // with a workspace for the partials, a few tokens take the split-K GEMM
+    const int ksplit = xf || !a.part ? 1 : gemm_ksplit(a.rows_total, a.cols, n_tok);
+    const bool split = ksplit > 1 && (size_t)ksplit * n_tok * a.rows_total <= a.part_floats &&
+                       env_int("TQ_HIP_GEMM_SPLIT", 1) != 0;
+    if (!xf && (split || n_tok >= gemm_min_tokens(a.rows_total, a.cols, pick_tokens(a.nb, false)))) {
         if ((size_t)n_tok * a.nb > (size_t)INT32_MAX / kBlockBytes) return TQ_HIP_EINVAL;
         a.n_tok = n_tok;
-        return herr(launch_gemm(a, s));
+        return herr(launch_gemm(a, split ? ksplit : 1, s));
     }
     const int tmax = pick_tokens(a.nb, xf);
     if (tmax == 0) return TQ_HIP_EINVAL;
@@ -1006,7 +1073,8 @@ int tq_hip_project_output_q4(const void *wo, int rows, int cols, const float *at
 }  // extern "C"
 
 int tq_project_qkv_fmt(bool q4, const void *wq, const void *wk, const void *wv, int q_rows, int kv_rows, int hidden,
-                    const float *xn, int n_tok, block_q8 *xq_ws, float *q, float *k, float *v, void *stream) {
+                    const float *xn, int n_tok, block_q8 *xq_ws, float *q, float *k, float *v, void *stream,
+                    float *part, size_t part_floats) {
     if (!shape_ok(q_rows, hidden) || kv_rows <= 0 || n_tok <= 0 || !wq || !wk || !wv || !xn ||
         !xq_ws || !q || !k || !v || !aligned(wq, 16) || !aligned(wk, 16) || !aligned(wv, 16) ||
         !aligned(xn, 4) || !aligned(xq_ws, 4) || !aligned(q, 4) || !aligned(k, 4) || !aligned(v, 4))
@@ -1030,11 +1098,13 @@ int tq_project_qkv_fmt(bool q4, const void *wq, const void *wk, const void *wv, 
     a.seg_end[1] = q_rows + kv_rows;
     a.seg_end[2] = q_rows + 2 * kv_rows;
     a.rows_total = a.seg_end[2];
+    a.part = part;
+    a.part_floats = part_floats;
     return run_gemv(a, n_tok, s);
 }
 
 int tq_project_output_fmt(bool q4, const void *wo, int rows, int cols, const float *attn, int n_tok,
-                       block_q8 *xq_ws, float *out, void *stream) {
+                       block_q8 *xq_ws, float *out, void *stream, float *part, size_t part_floats) {
     if (!shape_ok(rows, cols) || n_tok <= 0 || !wo || !attn || !xq_ws || !out || !aligned(wo, 16) ||
         !aligned(attn, 4) || !aligned(xq_ws, 4) || !aligned(out, 4))
         return TQ_HIP_EINVAL;
@@ -1053,12 +1123,23 @@ int tq_project_output_fmt(bool q4, const void *wo, int rows, int cols, const flo
     a.seg[0] = GemvSeg{(const unsigned char *)wo, out, rows};
     a.seg_end[0] = a.seg_end[1] = a.seg_end[2] = rows;
     a.rows_total = rows;
+    a.part = part;
+    a.part_floats = part_floats;
     return run_gemv(a, n_tok, s);
+}
+
+// Partial floats a split-K GEMM of rows x cols needs for any token count up
+// to n_cap (only one 128-token tile is ever split).
+size_t tq_gemm_partial_floats(int rows, int cols, int n_cap) {
+    if (rows <= 0 || cols <= 0 || n_cap < 16) return 0;
+    const int n = n_cap < kGemmToks ? n_cap : kGemmToks;
+    return (size_t)gemm_ksplit(rows, cols, n) * n * rows;
 }
 
 extern "C" {
 
-static size_t mlp_ws(int hidden, int inter, int n, size_t *off_gate, size_t *off_up, size_t *off_xq) {
+static size_t mlp_ws(int hidden, int inter, int n, size_t *off_gate, size_t *off_up, size_t *off_xq,
+                     size_t *off_part, size_t *part_floats) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     size_t o = 0;
     *off_gate = o;
@@ -1067,6 +1148,11 @@ static size_t mlp_ws(int hidden, int inter, int n, size_t *off_gate, size_t *off
     o += al((size_t)n * inter * 4);
     *off_xq = o;
     o += al((size_t)n * (size_t)(hidden > inter ? hidden : inter) / kQK * kBlockBytes);
+    // split-K partials of the gate/up and the down matmuls (one at a time)
+    const size_t pg = tq_gemm_partial_floats(2 * inter, hidden, n), pd = tq_gemm_partial_floats(hidden, inter, n);
+    *part_floats = pg > pd ? pg : pd;
+    *off_part = o;
+    o += al(*part_floats * 4);
     return o;
 }
 
@@ -1078,8 +1164,8 @@ static bool mlp_ok(const tq_hip_mlp_weights *w, int n) {
 
 size_t tq_hip_mlp_ws_bytes(const tq_hip_mlp_weights *w, int n) {
     if (!mlp_ok(w, n)) return 0;
-    size_t a, b, c;
-    return mlp_ws(w->hidden, w->inter, n, &a, &b, &c);
+    size_t a, b, c, d, e;
+    return mlp_ws(w->hidden, w->inter, n, &a, &b, &c, &d, &e);
 }
 
 int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn, float *d_out, void *d_ws,
@@ -1087,10 +1173,11 @@ int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn
     if (!mlp_ok(w, n) || !d_xn || !d_out || !d_ws || !aligned(d_ws, 16) || !aligned(d_xn, 4) ||
         !aligned(d_out, 4))
         return TQ_HIP_EINVAL;
-    size_t og, ou, ox;
-    if (ws_bytes < mlp_ws(w->hidden, w->inter, n, &og, &ou, &ox)) return TQ_HIP_EINVAL;
+    size_t og, ou, ox, op, pf;
+    if (ws_bytes < mlp_ws(w->hidden, w->inter, n, &og, &ou, &ox, &op, &pf)) return TQ_HIP_EINVAL;
     unsigned char *ws = (unsigned char *)d_ws;
     float *gate = (float *)(ws + og), *up = (float *)(ws + ou);
+    float *part = (float *)(ws + op);
     block_q8 *xq = (block_q8 *)(ws + ox);
     const hipStream_t s = (hipStream_t)stream;
     // model/mlp.c:9-11: quantize xn, then the gate and up matmuls in one launch
@@ -1111,6 +1198,8 @@ int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn
     a.seg_end[0] = w->inter;
     a.seg_end[1] = a.seg_end[2] = 2 * w->inter;
     a.rows_total = 2 * w->inter;
+    a.part = part;
+    a.part_floats = pf;
     int rc = run_gemv(a, n, s);
     if (rc != TQ_HIP_OK) return rc;
     // :12-13 silu_mul, then quantize the hidden rows (fused)
@@ -1124,6 +1213,8 @@ int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn
     d.seg_end[0] = d.seg_end[1] = d.seg_end[2] = w->hidden;
     d.rows_total = w->hidden;
     d.xq = (const unsigned char *)xq;
+    d.part = part;
+    d.part_floats = pf;
     return run_gemv(d, n, s);
 }
 

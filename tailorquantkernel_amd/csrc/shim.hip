@@ -1076,7 +1076,8 @@ int tq_hip_prefill(tq_hip_kv *kv, int seq, int pos0, int n, const float *q, cons
 // ---- the whole attention layer -------------------------------------------
 
 static size_t layer_ws(const tq_hip_kv_desc &D, int hidden, int n_q, size_t *off_q, size_t *off_k,
-                       size_t *off_v, size_t *off_attn, size_t *off_xq) {
+                       size_t *off_v, size_t *off_attn, size_t *off_xq, size_t *off_part = nullptr,
+                       size_t *part_floats = nullptr) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const size_t qd = (size_t)D.n_q_heads * D.head_dim, kd = (size_t)D.n_kv_heads * D.head_dim;
     const size_t widest = (size_t)(hidden > (int)qd ? hidden : (int)qd);
@@ -1091,6 +1092,13 @@ static size_t layer_ws(const tq_hip_kv_desc &D, int hidden, int n_q, size_t *off
     o += al((size_t)n_q * qd * 4);
     *off_xq = o;
     o += al((size_t)n_q * widest / QK * sizeof(block_q8));
+    // split-K partials of the q/k/v and the output matmuls (one at a time)
+    const size_t pq = tq_gemm_partial_floats((int)(qd + 2 * kd), hidden, n_q);
+    const size_t po = tq_gemm_partial_floats(hidden, (int)qd, n_q);
+    const size_t pf = pq > po ? pq : po;
+    if (off_part) *off_part = o;
+    if (part_floats) *part_floats = pf;
+    o += al(pf * 4);
     return o;
 }
 
@@ -1114,21 +1122,22 @@ int tq_hip_attention_layer_async(tq_hip_kv *kv, const tq_hip_attn_weights *w, in
         !w->wq || !w->wk || !w->wv || !w->wo || !w->q_norm || !w->k_norm)
         return TQ_HIP_EINVAL;
     const tq_hip_kv_desc &D = kv->desc;
-    size_t oq, ok, ov, oa, ox;
-    if (ws_bytes < layer_ws(D, w->hidden, n_q, &oq, &ok, &ov, &oa, &ox)) return TQ_HIP_EINVAL;
+    size_t oq, ok, ov, oa, ox, op, pf;
+    if (ws_bytes < layer_ws(D, w->hidden, n_q, &oq, &ok, &ov, &oa, &ox, &op, &pf)) return TQ_HIP_EINVAL;
     unsigned char *ws = (unsigned char *)d_ws;
     float *q = (float *)(ws + oq), *k = (float *)(ws + ok), *v = (float *)(ws + ov);
     float *attn = (float *)(ws + oa);
     block_q8 *xq = (block_q8 *)(ws + ox);
+    float *part = (float *)(ws + op);
     const int qd = D.n_q_heads * D.head_dim, kd = D.n_kv_heads * D.head_dim;
     void *s = (void *)pick(kv, stream);
     const bool q4 = w->format == TQ_HIP_FORMAT_Q4;
-    int rc = tq_project_qkv_fmt(q4, w->wq, w->wk, w->wv, qd, kd, w->hidden, d_xn, n_q, xq, q, k, v, s);
+    int rc = tq_project_qkv_fmt(q4, w->wq, w->wk, w->wv, qd, kd, w->hidden, d_xn, n_q, xq, q, k, v, s, part, pf);
     if (rc != TQ_HIP_OK) return rc;
     rc = tq_hip_decode_step_norm_async(kv, n_q, d_seq, d_pos, max_pos, q, k, v, w->q_norm, w->k_norm,
                                        w->rms_eps, d_cos, d_sin, attn, s);
     if (rc != TQ_HIP_OK) return rc;
-    return tq_project_output_fmt(q4, w->wo, w->hidden, qd, attn, n_q, xq, d_out, s);
+    return tq_project_output_fmt(q4, w->wo, w->hidden, qd, attn, n_q, xq, d_out, s, part, pf);
 }
 
 int tq_hip_attention_layer_batch_async(tq_hip_kv *kv, const tq_hip_attn_weights *w, int seq, int pos0,
@@ -1141,18 +1150,19 @@ int tq_hip_attention_layer_batch_async(tq_hip_kv *kv, const tq_hip_attn_weights 
     // model/attention_layer.c:203-204
     if (pos0 < 0 || pos0 + n > capacity_of(kv, seq)) return TQ_HIP_EINVAL;
     const tq_hip_kv_desc &D = kv->desc;
-    size_t oq, ok, ov, oa, ox;
-    if (ws_bytes < layer_ws(D, w->hidden, n, &oq, &ok, &ov, &oa, &ox)) return TQ_HIP_EINVAL;
+    size_t oq, ok, ov, oa, ox, op, pf;
+    if (ws_bytes < layer_ws(D, w->hidden, n, &oq, &ok, &ov, &oa, &ox, &op, &pf)) return TQ_HIP_EINVAL;
     unsigned char *ws = (unsigned char *)d_ws;
     float *q = (float *)(ws + oq), *k = (float *)(ws + ok), *v = (float *)(ws + ov);
     float *attn = (float *)(ws + oa);
     block_q8 *xq = (block_q8 *)(ws + ox);
+    float *part = (float *)(ws + op);
     const int qd = D.n_q_heads * D.head_dim, kd = D.n_kv_heads * D.head_dim;
     const hipStream_t hs = pick(kv, stream);
     void *s = (void *)hs;
     // :213-218 quantize every row, then the batched q/k/v projections
     const bool q4 = w->format == TQ_HIP_FORMAT_Q4;
-    int rc = tq_project_qkv_fmt(q4, w->wq, w->wk, w->wv, qd, kd, w->hidden, d_xn, n, xq, q, k, v, s);
+    int rc = tq_project_qkv_fmt(q4, w->wq, w->wk, w->wv, qd, kd, w->hidden, d_xn, n, xq, q, k, v, s, part, pf);
     if (rc != TQ_HIP_OK) return rc;
     // :227-228 norm_heads on every token's q and k rows
     TQ_TRY(tq_launch_rmsnorm_rows(q, w->q_norm, q, n * D.n_q_heads, D.head_dim, w->rms_eps, hs));
@@ -1161,7 +1171,7 @@ int tq_hip_attention_layer_batch_async(tq_hip_kv *kv, const tq_hip_attn_weights 
     rc = tq_hip_prefill_async(kv, seq, pos0, n, q, k, v, d_cos, d_sin, attn, s);
     if (rc != TQ_HIP_OK) return rc;
     // :238-241 quantize the attention rows, then the batched output projection
-    return tq_project_output_fmt(q4, w->wo, w->hidden, qd, attn, n, xq, d_out, s);
+    return tq_project_output_fmt(q4, w->wo, w->hidden, qd, attn, n, xq, d_out, s, part, pf);
 }
 
 }  // extern "C"

@@ -255,10 +255,15 @@ hipError_t tq_launch_silu_quant(const float *gate, const float *up, block_q8 *hq
 
 // tq_hip_project_qkv / tq_hip_project_output over tiled Q8 (q4 false) or
 // tiled Q4 (q4 true) matrices; TQ_HIP_* codes.
+// part / part_floats: room for split-K partials (tq_gemm_partial_floats),
+// or null: a few tokens then take GEMV launches or the unsplit GEMM.
 int tq_project_qkv_fmt(bool q4, const void *wq, const void *wk, const void *wv, int q_rows, int kv_rows, int hidden,
-                       const float *xn, int n_tok, block_q8 *xq_ws, float *q, float *k, float *v, void *stream);
+                       const float *xn, int n_tok, block_q8 *xq_ws, float *q, float *k, float *v, void *stream,
+                       float *part = nullptr, size_t part_floats = 0);
 int tq_project_output_fmt(bool q4, const void *wo, int rows, int cols, const float *attn, int n_tok,
-                          block_q8 *xq_ws, float *out, void *stream);
+                          block_q8 *xq_ws, float *out, void *stream, float *part = nullptr, size_t part_floats = 0);
+// Partial floats the split-K GEMM of a rows x cols matrix needs for up to n_cap tokens.
+size_t tq_gemm_partial_floats(int rows, int cols, int n_cap);
 // In place allowed (out == x); n <= 8191.
 hipError_t tq_launch_rmsnorm_rows(const float *x, const float *w, float *out, int n_rows, int n, float eps,
                                   hipStream_t s);

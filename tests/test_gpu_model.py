@@ -115,6 +115,14 @@ def test_mlp_layer(nat, oracle, hidden, inter, n, skew):
         assert rel_l2(out[t], ref) <= 1e-5
 
 
+def test_mlp_layer_split_k_off(nat, oracle, monkeypatch):
+    """20 rows take the split-K GEMM (partials in the workspace, summed in
+    split order); with it switched off they take the unsplit launches, under
+    the same bars."""
+    monkeypatch.setenv("TQ_HIP_GEMM_SPLIT", "0")
+    test_mlp_layer(nat, oracle, 512, 1024, 20, 0)
+
+
 def test_add_rmsnorm(nat, oracle):
     lib = nat.load()
     # 1024-thread kernel holding 1, 2, 4 and 8 float4 per thread, and the

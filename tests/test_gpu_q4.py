@@ -218,3 +218,39 @@ def test_q4_embed_lookup(nat, oracle):
     for i, t in enumerate(toks):
         assert got[i].tobytes() == oracle.embed_lookup_q4(E, vocab, hidden, int(t))[1].tobytes()
     assert blocks4(1).itemsize == 20
+
+
+@pytest.mark.parametrize("split", ["1", "0"])
+def test_q4_mlp_split_k(nat, oracle, split, monkeypatch):
+    """A Q4 MLP over 20 rows: with split-K on, the gate/up and down matmuls
+    take the split GEMM (partials in the workspace, summed in split order);
+    off, the unsplit launches.  gate/up against the oracle's Q4 matmul of the
+    quantized rows, down against the oracle's Q4 matmul of the GPU's own
+    hidden rows, both within the matmul bar."""
+    monkeypatch.setenv("TQ_HIP_GEMM_SPLIT", split)
+    import ctypes as C
+    from oracle.binding import BLOCK_Q8
+    lib = nat.load()
+    hidden, inter, n = 512, 1024, 20
+    rng = np.random.default_rng(20)
+    wg = oracle.pack_matrix_q4(rng.standard_normal((inter, hidden)).astype(np.float32) * 0.1)
+    wu = oracle.pack_matrix_q4(rng.standard_normal((inter, hidden)).astype(np.float32) * 0.1)
+    wd = oracle.pack_matrix_q4(rng.standard_normal((hidden, inter)).astype(np.float32) * 0.1)
+    G, U, D = Matrix4(nat, wg, inter, hidden), Matrix4(nat, wu, inter, hidden), Matrix4(nat, wd, hidden, inter)
+    w = nat.MlpWeights(G.buf.ptr, U.buf.ptr, D.buf.ptr, hidden, inter, nat.FORMAT_Q4)
+    wsb = lib.tq_hip_mlp_ws_bytes(C.byref(w), n)
+    ws = nat.DeviceBuffer(wsb)
+    xn = (rng.standard_normal(n * hidden) * 2).astype(np.float32)
+    dx, dout = dev(nat, xn), nat.DeviceBuffer(n * hidden * 4)
+    nat.check(lib.tq_hip_mlp_layer_async(C.byref(w), n, dx.ptr, dout.ptr, ws.ptr, wsb, None), "mlp")
+    sync(nat)
+    out = dout.download((n, hidden), np.float32)
+    raw = ws.download((wsb,), np.uint8)
+    al = lambda b: (b + 255) & ~255
+    gate = raw[:n * inter * 4].view(np.float32).reshape(n, inter)
+    up = raw[al(n * inter * 4):al(n * inter * 4) + n * inter * 4].view(np.float32).reshape(n, inter)
+    hq = raw[2 * al(n * inter * 4):2 * al(n * inter * 4) + n * inter // QK * 36].view(BLOCK_Q8)
+    xq = quantize_tokens(oracle, xn, n, hidden)
+    check_matmul(gate, oracle.matmul_q4(wg, xq, inter, hidden, n), wg, xq, inter, hidden, n, "gate")
+    check_matmul(up, oracle.matmul_q4(wu, xq, inter, hidden, n), wu, xq, inter, hidden, n, "up")
+    check_matmul(out, oracle.matmul_q4(wd, hq, hidden, inter, n), wd, hq, hidden, inter, n, "down")
