@@ -894,17 +894,22 @@ hipError_t launch_gemm(const GemvArgs &a, int ksplit, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Split-K GEMM for a few tokens (one 128-token tile): the row tiles alone
-// leave most of the 256 CUs idle and each runs the whole K loop, so K is cut
-// into S runs of stages, enough for about 512 work-groups (two per CU), each
-// writing a partial tile that one more launch sums in split order.
-constexpr int kSplitTargetWgs = 512;
+// Split-K GEMM while the tiles alone leave CUs of the 256 idle (each tile
+// then runs the whole K loop): K is cut into S runs of stages, as many as
+// keep the grid within one round of 512 work-groups (two per CU), each split
+// writing a partial tile that one more launch sums in split order.  The 8B
+// MLP over 16 / 64 / 256 / 512 rows: 130 / 141 / 272 / 481 us against
+// 134 / 325 / 427 / 570 without.
+constexpr int kSplitWgs = 512;
 
 int gemm_ksplit(int rows, int cols, int n_tok) {
-    if (n_tok < 16 || n_tok > kGemmToks) return 1;
-    const long wgs = ((long)(rows + kGemmRows - 1) / kGemmRows + 7) / 8 * 8;
+    if (n_tok < 16) return 1;
+    const long wgs = ((long)(rows + kGemmRows - 1) / kGemmRows + 7) / 8 * 8 * ((n_tok + kGemmToks - 1) / kGemmToks);
+    // once every CU holds a tile, splitting adds occupancy but not CUs, and
+    // the partials' traffic outweighs it (4,096 x 14,336 at 1,024 tokens)
+    if (wgs >= kSplitWgs / 2) return 1;
     const int stages = (cols / kQK + kGemmKB - 1) / kGemmKB;
-    long sp = (kSplitTargetWgs + wgs - 1) / wgs;
+    long sp = kSplitWgs / wgs;
     if (sp > stages) sp = stages;
     return sp < 2 ? 1 : (int)sp;
 }
@@ -1129,11 +1134,18 @@ int tq_project_output_fmt(bool q4, const void *wo, int rows, int cols, const flo
 }
 
 // Partial floats a split-K GEMM of rows x cols needs for any token count up
-// to n_cap (only one 128-token tile is ever split).
+// to n_cap: the largest S * n over the token-tile counts that still split.
 size_t tq_gemm_partial_floats(int rows, int cols, int n_cap) {
     if (rows <= 0 || cols <= 0 || n_cap < 16) return 0;
-    const int n = n_cap < kGemmToks ? n_cap : kGemmToks;
-    return (size_t)gemm_ksplit(rows, cols, n) * n * rows;
+    size_t most = 0;
+    for (int tiles = 1; (long)(tiles - 1) * kGemmToks < n_cap; tiles++) {
+        const int n = n_cap < tiles * kGemmToks ? n_cap : tiles * kGemmToks;
+        const int sp = gemm_ksplit(rows, cols, n);
+        if (sp < 2) break;
+        const size_t need = (size_t)sp * n * rows;
+        if (need > most) most = need;
+    }
+    return most;
 }
 
 extern "C" {
