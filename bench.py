@@ -1430,23 +1430,30 @@ def bench_forward_8b(args, nat, hip, fmt="q8"):
 
     A.tq_dev_ctx_free(C.byref(ctx))
 
-    # prefill: 2048 tokens from an empty context, tq_dev_prefill
+    # prefill from an empty context, tq_dev_prefill: 2048 tokens, and 256 (a
+    # prompt short enough that the batched matmuls split K)
+    def prefill_ms(n_pf, runs):
+        toks = rng.integers(0, vocab, n_pf).astype(np.int32)
+        out = []
+        for rep in range(runs):
+            cpf = attn.DevCtx()
+            assert A.tq_dev_ctx_init(C.byref(cpf), C.byref(model), n_pf) == 0
+            hip.sync()
+            e0, e1 = hip.event(), hip.event()
+            hip.record(e0, cpf.stream)
+            rc = A.tq_dev_prefill(C.byref(cpf), toks.ctypes.data, n_pf)
+            hip.record(e1, cpf.stream)
+            if rc != 0:
+                raise RuntimeError(f"tq_dev_prefill: {rc}")
+            out.append(hip.elapsed_ms(e0, e1))
+            A.tq_dev_ctx_free(C.byref(cpf))
+        return out
+
     n_pf = 2048
-    toks = rng.integers(0, vocab, n_pf).astype(np.int32)
-    pf_ms = []
-    for rep in range(3):
-        cpf = attn.DevCtx()
-        assert A.tq_dev_ctx_init(C.byref(cpf), C.byref(model), n_pf) == 0
-        hip.sync()
-        e0, e1 = hip.event(), hip.event()
-        hip.record(e0, cpf.stream)
-        rc = A.tq_dev_prefill(C.byref(cpf), toks.ctypes.data, n_pf)
-        hip.record(e1, cpf.stream)
-        if rc != 0:
-            raise RuntimeError(f"tq_dev_prefill: {rc}")
-        pf_ms.append(hip.elapsed_ms(e0, e1))
-        A.tq_dev_ctx_free(C.byref(cpf))
+    pf_ms = prefill_ms(n_pf, 3)
     pf = float(np.median(pf_ms[1:]))
+    pf256_ms = prefill_ms(256, 5)
+    pf256 = float(np.median(pf256_ms[1:]))
 
     kv_bytes = nl * T * nkv * 2 * nb * BLOCK_BYTES
     step_bytes = nl * layer_bytes + embed_bytes + kv_bytes + mbytes(1, hidden)
@@ -1471,6 +1478,9 @@ def bench_forward_8b(args, nat, hip, fmt="q8"):
                          "what": "tq_dev_prefill of 2048 tokens on an empty 32-layer context (one "
                                  "tq_dev_forward_batch call of 2048 tokens, logits of the last token); median "
                                  "of the runs after the first"},
+        "prefill_256": {"ms": pf256, "tokens_per_s": 256e3 / pf256, "runs_ms": pf256_ms,
+                        "what": "tq_dev_prefill of 256 tokens on an empty 32-layer context (the batched "
+                                "matmuls split K); median of the runs after the first"},
         "parity": parity,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
