@@ -17,14 +17,21 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // gate and up, one dword of codes per lane.  Rows are contiguous, so blocks
 // never straddle two of them; whole 8-lane groups stay together, as
 // quantize8x4's DPP steps need.
+// scales non-null: the block-major split layout of quantize8_kernel over
+// rows of nb blocks.
 __global__ __launch_bounds__(256) void silu_quant8_kernel(const float *__restrict__ gate,
                                                           const float *__restrict__ up,
-                                                          unsigned char *__restrict__ hq, long nblocks) {
+                                                          unsigned char *__restrict__ hq, long nblocks,
+                                                          float *__restrict__ scales, int nb) {
 #pragma clang fp contract(off)
     const long k = (long)blockIdx.x * 256 + threadIdx.x;
-    const long tb = k >> 3;
-    if (tb >= nblocks) return;
+    const long gi = k >> 3;
+    if (gi >= nblocks) return;
     const int e = (int)(k & 7);
+    // split layout: block-major order (consecutive groups, consecutive rows of
+    // one block), so the code stores coalesce
+    const long n = scales ? nblocks / nb : 1, bq = scales ? gi / n : 0, tq = scales ? gi - bq * n : 0;
+    const long tb = scales ? tq * nb + bq : gi;
     const float4 g4 = *reinterpret_cast<const float4 *>(gate + tb * kQK + 4 * e);
     const float4 u4 = *reinterpret_cast<const float4 *>(up + tb * kQK + 4 * e);
     const float g[4] = {g4.x, g4.y, g4.z, g4.w}, u[4] = {u4.x, u4.y, u4.z, u4.w};
@@ -34,8 +41,12 @@ __global__ __launch_bounds__(256) void silu_quant8_kernel(const float *__restric
         const float sig = 1.0f / (1.0f + expf(-g[i]));
         h[i] = g[i] * sig * u[i];
     }
-    unsigned char *blk = hq + tb * kBlockBytes;
-    quantize8x4(h, reinterpret_cast<float *>(blk), blk + 4 + 4 * e, e == 0);
+    if (scales) {
+        quantize8x4(h, scales + bq * n + tq, hq + ((2 * bq + (e >> 2)) * n + tq) * 16 + 4 * (e & 3), e == 0);
+    } else {
+        unsigned char *blk = hq + tb * kBlockBytes;
+        quantize8x4(h, reinterpret_cast<float *>(blk), blk + 4 + 4 * e, e == 0);
+    }
 }
 
 // x += y (when y is given), then xn = rmsnorm(x) with `weight`: one
@@ -265,7 +276,17 @@ hipError_t tq_launch_silu_quant(const float *gate, const float *up, block_q8 *hq
     // aligned workspace (tq_hip_mlp_layer_async checks it)
     if ((((uintptr_t)gate | (uintptr_t)up) & 15) || ((uintptr_t)hq & 3)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(silu_quant8_kernel, dim3((unsigned)((nblocks * 8 + 255) / 256)), dim3(256), 0, s, gate, up,
-                       reinterpret_cast<unsigned char *>(hq), nblocks);
+                       reinterpret_cast<unsigned char *>(hq), nblocks, (float *)nullptr, 1);
+    return hipGetLastError();
+}
+
+hipError_t tq_launch_silu_quant_split(const float *gate, const float *up, unsigned char *hq, int rows, int cols,
+                                      hipStream_t s) {
+    const long nblocks = (long)rows * (cols / kQK);
+    if (nblocks <= 0) return hipSuccess;
+    if (cols % kQK || (((uintptr_t)gate | (uintptr_t)up | (uintptr_t)hq) & 15)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(silu_quant8_kernel, dim3((unsigned)((nblocks * 8 + 255) / 256)), dim3(256), 0, s, gate, up, hq,
+                       nblocks, reinterpret_cast<float *>(hq + nblocks * kQK), cols / kQK);
     return hipGetLastError();
 }
 

@@ -25,16 +25,32 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float *__restrict__
 // The same with 8 lanes x 4 values per block: one float4 load and one dword
 // of codes per lane (16-byte aligned x).  Whole 8-lane groups stay together
 // (256 is a multiple of 8), as quantize8x4's DPP steps need.
+// scales null: block_q8 blocks at out.  Else the split layout the batched
+// matmul reads, block-major over the n = nblocks / nb rows: for block b of
+// row t, codes 0-15 at out + ((2b) n + t) 16, codes 16-31 at
+// out + ((2b + 1) n + t) 16, the scale at scales[b n + t].
 __global__ __launch_bounds__(256) void quantize8_kernel(const float *__restrict__ x, unsigned char *__restrict__ out,
-                                                        long nblocks) {
+                                                        long nblocks, float *__restrict__ scales, int nb) {
     const long k = (long)blockIdx.x * 256 + threadIdx.x;
-    const long tb = k >> 3;
-    if (tb >= nblocks) return;
+    const long g = k >> 3;
+    if (g >= nblocks) return;
     const int e = (int)(k & 7);
+    if (scales) {
+        // block-major: consecutive 8-lane groups take consecutive rows of one
+        // block, so a wave's code stores are two contiguous 128-byte runs
+        const long n = nblocks / nb, b = g / n, t = g - b * n;
+        const float4 v = *reinterpret_cast<const float4 *>(x + (t * nb + b) * kQK + 4 * e);
+        const float xv[4] = {v.x, v.y, v.z, v.w};
+        quantize8x4(xv, scales + b * n + t, out + ((2 * b + (e >> 2)) * n + t) * 16 + 4 * (e & 3), e == 0);
+        return;
+    }
+    const long tb = g;
     const float4 v = *reinterpret_cast<const float4 *>(x + tb * kQK + 4 * e);
     const float xv[4] = {v.x, v.y, v.z, v.w};
-    unsigned char *blk = out + tb * kBlockBytes;
-    quantize8x4(xv, reinterpret_cast<float *>(blk), blk + 4 + 4 * e, e == 0);
+    {
+        unsigned char *blk = out + tb * kBlockBytes;
+        quantize8x4(xv, reinterpret_cast<float *>(blk), blk + 4 + 4 * e, e == 0);
+    }
 }
 
 // One thread per (head, pair i < hd/2): reads both halves, writes both.
@@ -157,10 +173,19 @@ hipError_t tq_launch_quantize(const float *x, block_q8 *out, int n, hipStream_t 
     if (nblocks <= 0) return hipSuccess;
     if ((((uintptr_t)x & 15) | ((uintptr_t)out & 3)) == 0)
         hipLaunchKernelGGL(quantize8_kernel, dim3(grid_for((long)nblocks * 8)), dim3(256), 0, s, x,
-                           reinterpret_cast<unsigned char *>(out), (long)nblocks);
+                           reinterpret_cast<unsigned char *>(out), (long)nblocks, (float *)nullptr, 1);
     else
         hipLaunchKernelGGL(quantize_kernel, dim3(grid_for((long)nblocks * kQK)), dim3(256), 0, s, x,
                            reinterpret_cast<unsigned char *>(out), nblocks);
+    return hipGetLastError();
+}
+
+hipError_t tq_launch_quantize_split(const float *x, unsigned char *out, int rows, int cols, hipStream_t s) {
+    const long nblocks = (long)rows * (cols / kQK);
+    if (nblocks <= 0) return hipSuccess;
+    if (cols % kQK || (((uintptr_t)x | (uintptr_t)out) & 15)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(quantize8_kernel, dim3(grid_for(nblocks * 8)), dim3(256), 0, s, x, out, nblocks,
+                       reinterpret_cast<float *>(out + nblocks * kQK), cols / kQK);
     return hipGetLastError();
 }
 

@@ -166,6 +166,8 @@ struct GemvArgs {
     float *part;              // GEMM split-K partial tiles [ksplit][n_tok][rows_total], or null
     size_t part_floats;       // their capacity
     int ksplit;               // GEMM: K splits of this launch (1: none)
+    bool xs;                  // GEMM: xq holds the block-major split layout of
+                              // tq_launch_quantize_split instead of block_q8 rows
 };
 
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
@@ -449,6 +451,8 @@ constexpr int kGemmBChunks = kGemmB / 16;                       // 1,152 16-byte
 constexpr int kGemmBRounds = (kGemmBChunks + kGemmThreads - 1) / kGemmThreads;   // 3
 constexpr int kGemmStage = kGemmA + kGemmWD + kGemmB;           // 36,864 (16-byte multiple)
 constexpr int kGemmBWords = kGemmB / 4;                         // 4,608 dword copies
+constexpr int kGemmXsCodes = kGemmKB * kQK * kGemmToks;          // 16,384: split-layout codes, then scales
+static_assert(kGemmXsCodes + kGemmKB * kGemmToks * 4 == kGemmB, "the split layout fills the token stage");
 static_assert(kGemmBChunks % 64 == 0 && (kGemmBRounds - 1) * kGemmThreads < kGemmBChunks,
               "the last B round's copies past the tile are whole waves");
 static_assert(kGemmA / 16 % kGemmThreads == 0 && kGemmWD / 4 % kGemmThreads == 0 &&
@@ -465,9 +469,10 @@ __device__ __forceinline__ long lds_pair(const unsigned char *p) {
 // copy per thread instead of two); each lane turns its 8 bytes into 16 x its
 // 8 codes (low nibbles for k < 16, high for k >= 16), and the int32 products
 // are shifted back by 4 before scaling.
-template <bool BX4, bool Q4, bool UNI>
+template <bool BX4, bool Q4, bool UNI, bool XS>
 __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
     static_assert(!UNI || BX4, "uniform copies need whole 16-byte stages");
+    static_assert(!XS || UNI, "the split layout is copied from uniform bases");
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -525,13 +530,22 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
         uscale = (size_t)rows * rowb;
         vrow = (uint32_t)(r - start) * rowb;
         vdrow = (uint32_t)(r - start) * (uint32_t)nb * 4u;
-#pragma unroll
-        for (int j = 0; j < kGemmBRounds; j++) {
-            const int c = tid + kGemmThreads * j;
-            const int cc = c < kGemmBChunks ? c : kGemmBChunks - 1;
-            const int tk = cc / 9, piece = cc - 9 * tk;
+        if constexpr (XS) {
+            // every copy of this lane is for token 64 (wave & 1) + lane of the
+            // tile: its 16-byte half-block and its scale in the block-major runs
+            const int tk = 64 * (wave & 1) + lane;
             const int t = tok0 + tk < a.n_tok ? tok0 + tk : a.n_tok - 1;
-            vb[j] = (uint32_t)t * (uint32_t)nb * (uint32_t)kBlockBytes + 16u * (uint32_t)piece;
+            vb[0] = 16u * (uint32_t)t;
+            vb[1] = 4u * (uint32_t)t;
+        } else {
+#pragma unroll
+            for (int j = 0; j < kGemmBRounds; j++) {
+                const int c = tid + kGemmThreads * j;
+                const int cc = c < kGemmBChunks ? c : kGemmBChunks - 1;
+                const int tk = cc / 9, piece = cc - 9 * tk;
+                const int t = tok0 + tk < a.n_tok ? tok0 + tk : a.n_tok - 1;
+                vb[j] = (uint32_t)t * (uint32_t)nb * (uint32_t)kBlockBytes + 16u * (uint32_t)piece;
+            }
         }
     }
 
@@ -566,10 +580,27 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
             }
         }
         dma4s(useg + uscale + 4 * (b0 + (wave >> 1)), vdrow, buf + kGemmA + 4 * 64 * wave);
+        if constexpr (XS) {
+            // codes: chunk c -> (block c / 256, half (c / 128) & 1, token c % 128),
+            // the same [block][half][row] 16-byte layout as the weights, one
+            // contiguous KiB per wave; scales: dword c -> (block c / 128, token c % 128)
+            const size_t n16 = 16 * (size_t)a.n_tok;
 #pragma unroll
-        for (int j = 0; j < kGemmBRounds; j++) {
-            const int c = 64 * wave + kGemmThreads * j;
-            if (c < kGemmBChunks) dma16s(a.xq + (size_t)b0 * kBlockBytes, vb[j], buf + kGemmA + kGemmWD + 16 * c);
+            for (int j = 0; j < kGemmA / 16 / kGemmThreads; j++) {
+                const int c = 64 * wave + kGemmThreads * j;
+                const int blk = c >> 8, half = (c >> 7) & 1;
+                dma16s(a.xq + (size_t)(2 * (b0 + blk) + half) * n16 + 16 * tok0, vb[0] - 16u * (uint32_t)tok0,
+                       buf + kGemmA + kGemmWD + 16 * c);
+            }
+            dma4s(a.xq + (size_t)a.n_tok * cols + 4 * ((size_t)(b0 + (wave >> 1)) * a.n_tok + tok0),
+                  vb[1] - 4u * (uint32_t)tok0, buf + kGemmA + kGemmWD + kGemmXsCodes + 4 * 64 * wave);
+        } else {
+#pragma unroll
+            for (int j = 0; j < kGemmBRounds; j++) {
+                const int c = 64 * wave + kGemmThreads * j;
+                if (c < kGemmBChunks)
+                    dma16s(a.xq + (size_t)b0 * kBlockBytes, vb[j], buf + kGemmA + kGemmWD + 16 * c);
+            }
         }
     };
 
@@ -661,13 +692,19 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
             }
 #pragma unroll
             for (int t4 = 0; t4 < 4; t4++) {
-                const unsigned char *tb = B + (wt + 16 * t4 + l16) * kGemmBRow + blk * kBlockBytes;
-                bv[t4] = lds_pair(tb + 4 + 8 * lg);
-                // the staged scale is always a real block's (past nb the copies
-                // repeat block nb-1): load it unconditionally and select, so no
-                // branch splits the block's LDS reads from its products
-                const float xv = *reinterpret_cast<const float *>(tb);
-                xd[t4] = valid ? xv : 0.0f;
+                if constexpr (XS) {
+                    // 8-byte reads of 16-byte rows: no bank conflicts, as for A
+                    bv[t4] = lds_pair(B + ((blk * 2 + (lg >> 1)) * kGemmToks + wt + 16 * t4 + l16) * 16 + 8 * (lg & 1));
+                    xd[t4] = *reinterpret_cast<const float *>(B + kGemmXsCodes + (blk * kGemmToks + wt + 16 * t4 + l16) * 4);
+                } else {
+                    const unsigned char *tb = B + (wt + 16 * t4 + l16) * kGemmBRow + blk * kBlockBytes;
+                    bv[t4] = lds_pair(tb + 4 + 8 * lg);
+                    // the staged scale is always a real block's (past nb the copies
+                    // repeat block nb-1): load it unconditionally and select, so no
+                    // branch splits the block's LDS reads from its products
+                    const float xv = *reinterpret_cast<const float *>(tb);
+                    xd[t4] = valid ? xv : 0.0f;
+                }
             }
             // all eight products first, so that each one's latency hides
             // under the others before its results are read
@@ -840,6 +877,17 @@ int gemm_min_tokens(int rows, int cols, int tmax) {
     return n < 16 ? 16 : (n > 256 ? 256 : n);
 }
 
+// Every 128-row tile inside one segment (segment ends on tile boundaries) and
+// 32-bit copy offsets: the uniform-base copies apply.
+bool gemm_uniform(const GemvArgs &a) {
+    for (int i = 0; i < kMaxSegs; i++) {
+        if (a.seg_end[i] < a.rows_total && a.seg_end[i] % kGemmRows != 0) return false;
+        const size_t rowb = a.q4 ? (size_t)a.cols / 2 : (size_t)a.cols;
+        if ((size_t)a.seg[i].rows * (rowb + 4 * (size_t)a.nb) >= ((size_t)1 << 31)) return false;
+    }
+    return (size_t)a.n_tok * a.nb * kBlockBytes < ((size_t)1 << 31);
+}
+
 hipError_t launch_gemm(const GemvArgs &a, int ksplit, hipStream_t s) {
     const int n_rt = (a.rows_total + kGemmRows - 1) / kGemmRows;
     const int n_tt = (a.n_tok + kGemmToks - 1) / kGemmToks;
@@ -849,10 +897,14 @@ hipError_t launch_gemm(const GemvArgs &a, int ksplit, hipStream_t s) {
     const size_t lds = (size_t)kGemmBufs * kGemmStage;
     static bool opted = false;
     if (!opted) {
-        for (const void *f :
-             {(const void *)gemm_q8_kernel<true, false, false>, (const void *)gemm_q8_kernel<false, false, false>,
-              (const void *)gemm_q8_kernel<true, true, false>, (const void *)gemm_q8_kernel<false, true, false>,
-              (const void *)gemm_q8_kernel<true, false, true>, (const void *)gemm_q8_kernel<true, true, true>}) {
+        for (const void *f : {(const void *)gemm_q8_kernel<true, false, false, false>,
+                              (const void *)gemm_q8_kernel<false, false, false, false>,
+                              (const void *)gemm_q8_kernel<true, true, false, false>,
+                              (const void *)gemm_q8_kernel<false, true, false, false>,
+                              (const void *)gemm_q8_kernel<true, false, true, false>,
+                              (const void *)gemm_q8_kernel<true, true, true, false>,
+                              (const void *)gemm_q8_kernel<true, false, true, true>,
+                              (const void *)gemm_q8_kernel<true, true, true, true>}) {
             const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
             if (e != hipSuccess) return e;
         }
@@ -861,28 +913,27 @@ hipError_t launch_gemm(const GemvArgs &a, int ksplit, hipStream_t s) {
     const bool bx4 = (((uintptr_t)a.xq & 15) == 0) && a.nb % kGemmKB == 0;
     GemvArgs u = a;
     u.ksplit = ksplit;
-    u.uni_tiles = true;
-    for (int i = 0; i < kMaxSegs; i++) {
-        if (a.seg_end[i] < a.rows_total && a.seg_end[i] % kGemmRows != 0) u.uni_tiles = false;
-        const size_t rowb = a.q4 ? (size_t)a.cols / 2 : (size_t)a.cols;
-        if ((size_t)a.seg[i].rows * (rowb + 4 * (size_t)a.nb) >= ((size_t)1 << 31)) u.uni_tiles = false;
-    }
-    if ((size_t)a.n_tok * a.nb * kBlockBytes >= ((size_t)1 << 31)) u.uni_tiles = false;
+    u.uni_tiles = gemm_uniform(a);
+    if (a.xs && !(bx4 && u.uni_tiles)) return hipErrorInvalidValue;   // the caller's plan and this disagree
     const dim3 g((unsigned)grid), b(kGemmThreads);
     if (a.q4) {
-        if (bx4 && u.uni_tiles)
-            hipLaunchKernelGGL((gemm_q8_kernel<true, true, true>), g, b, lds, s, u);
+        if (a.xs)
+            hipLaunchKernelGGL((gemm_q8_kernel<true, true, true, true>), g, b, lds, s, u);
+        else if (bx4 && u.uni_tiles)
+            hipLaunchKernelGGL((gemm_q8_kernel<true, true, true, false>), g, b, lds, s, u);
         else if (bx4)
-            hipLaunchKernelGGL((gemm_q8_kernel<true, true, false>), g, b, lds, s, u);
+            hipLaunchKernelGGL((gemm_q8_kernel<true, true, false, false>), g, b, lds, s, u);
         else
-            hipLaunchKernelGGL((gemm_q8_kernel<false, true, false>), g, b, lds, s, u);
+            hipLaunchKernelGGL((gemm_q8_kernel<false, true, false, false>), g, b, lds, s, u);
     } else {
-        if (bx4 && u.uni_tiles)
-            hipLaunchKernelGGL((gemm_q8_kernel<true, false, true>), g, b, lds, s, u);
+        if (a.xs)
+            hipLaunchKernelGGL((gemm_q8_kernel<true, false, true, true>), g, b, lds, s, u);
+        else if (bx4 && u.uni_tiles)
+            hipLaunchKernelGGL((gemm_q8_kernel<true, false, true, false>), g, b, lds, s, u);
         else if (bx4)
-            hipLaunchKernelGGL((gemm_q8_kernel<true, false, false>), g, b, lds, s, u);
+            hipLaunchKernelGGL((gemm_q8_kernel<true, false, false, false>), g, b, lds, s, u);
         else
-            hipLaunchKernelGGL((gemm_q8_kernel<false, false, false>), g, b, lds, s, u);
+            hipLaunchKernelGGL((gemm_q8_kernel<false, false, false, false>), g, b, lds, s, u);
     }
     if (ksplit > 1) {
         const hipError_t e = hipGetLastError();
@@ -914,20 +965,41 @@ int gemm_ksplit(int rows, int cols, int n_tok) {
     return sp < 2 ? 1 : (int)sp;
 }
 
+// The GEMM launch run_gemv makes over n_tok rows of block_q8 input (its K
+// split count), or 0 for GEMV launches.  With a workspace for the partials a
+// few tokens take the split-K GEMM; otherwise the cost model decides.
+int gemm_plan(const GemvArgs &a, int n_tok) {
+    if (a.x != nullptr) return 0;
+    const int ksplit = a.part ? gemm_ksplit(a.rows_total, a.cols, n_tok) : 1;
+    const bool split = ksplit > 1 && (size_t)ksplit * n_tok * a.rows_total <= a.part_floats &&
+                       env_int("TQ_HIP_GEMM_SPLIT", 1) != 0;
+    if (split) return ksplit;
+    return n_tok >= gemm_min_tokens(a.rows_total, a.cols, pick_tokens(a.nb, false)) ? 1 : 0;
+}
+
+// Whether the matmul's input should be quantized into the split layout:
+// internal callers (a partials workspace) whose launch is a GEMM with
+// uniform-base copies over whole stages, xq 16-byte aligned
+// (TQ_HIP_GEMM_XS=0 keeps block_q8 rows).
+bool xs_layout(const GemvArgs &a, int n_tok, const void *xq) {
+    if (!a.part || a.x || ((uintptr_t)xq & 15) || a.nb % kGemmKB || env_int("TQ_HIP_GEMM_XS", 1) == 0) return false;
+    GemvArgs t = a;
+    t.n_tok = n_tok;
+    return gemm_plan(a, n_tok) > 0 && gemm_uniform(t);
+}
+
 // Runs the matmul over all tokens: one GEMM launch for many block_q8 rows,
 // else GEMV launches of up to tmax tokens.  With fp32 input (a.x) each GEMV
 // launch quantizes its rows in LDS.
 int run_gemv(GemvArgs a, int n_tok, hipStream_t s) {
     const bool xf = a.x != nullptr;
-    // with a workspace for the partials, a few tokens take the split-K GEMM
-    const int ksplit = xf || !a.part ? 1 : gemm_ksplit(a.rows_total, a.cols, n_tok);
-    const bool split = ksplit > 1 && (size_t)ksplit * n_tok * a.rows_total <= a.part_floats &&
-                       env_int("TQ_HIP_GEMM_SPLIT", 1) != 0;
-    if (!xf && (split || n_tok >= gemm_min_tokens(a.rows_total, a.cols, pick_tokens(a.nb, false)))) {
+    const int plan = gemm_plan(a, n_tok);
+    if (plan > 0) {
         if ((size_t)n_tok * a.nb > (size_t)INT32_MAX / kBlockBytes) return TQ_HIP_EINVAL;
         a.n_tok = n_tok;
-        return herr(launch_gemm(a, split ? ksplit : 1, s));
+        return herr(launch_gemm(a, plan, s));
     }
+    if (a.xs) return TQ_HIP_EINVAL;   // the split layout is for the GEMM only
     const int tmax = pick_tokens(a.nb, xf);
     if (tmax == 0) return TQ_HIP_EINVAL;
     const int rw = pick_rw(a.rows_total);
@@ -1077,6 +1149,24 @@ int tq_hip_project_output_q4(const void *wo, int rows, int cols, const float *at
 
 }  // extern "C"
 
+// The matmul input of a (segments, workspace set): one or two rows quantized
+// inside the GEMV launch; else quantize_row_q8 of every row into the
+// workspace first, as block_q8 rows or, for a GEMM that reads it, in the
+// split layout.
+int quantize_input(GemvArgs &a, const float *x, int n_tok, int cols, void *xq_ws, hipStream_t s) {
+    if (fuse_quantize(x, n_tok, a.nb)) {
+        a.x = x;
+        a.xq_out = (unsigned char *)xq_ws;
+        return TQ_HIP_OK;
+    }
+    a.xs = xs_layout(a, n_tok, xq_ws);
+    const hipError_t e = a.xs ? tq_launch_quantize_split(x, (unsigned char *)xq_ws, n_tok, cols, s)
+                              : tq_launch_quantize(x, (block_q8 *)xq_ws, n_tok * cols, s);
+    if (e != hipSuccess) return herr(e);
+    a.xq = (const unsigned char *)xq_ws;
+    return TQ_HIP_OK;
+}
+
 int tq_project_qkv_fmt(bool q4, const void *wq, const void *wk, const void *wv, int q_rows, int kv_rows, int hidden,
                     const float *xn, int n_tok, block_q8 *xq_ws, float *q, float *k, float *v, void *stream,
                     float *part, size_t part_floats) {
@@ -1088,14 +1178,6 @@ int tq_project_qkv_fmt(bool q4, const void *wq, const void *wk, const void *wv, 
     GemvArgs a;
     init_args(a, hidden);
     a.q4 = q4;
-    if (fuse_quantize(xn, n_tok, a.nb)) {
-        a.x = xn;
-        a.xq_out = (unsigned char *)xq_ws;
-    } else {
-        const hipError_t e = tq_launch_quantize(xn, xq_ws, n_tok * hidden, s);
-        if (e != hipSuccess) return herr(e);
-        a.xq = (const unsigned char *)xq_ws;
-    }
     a.seg[0] = GemvSeg{(const unsigned char *)wq, q, q_rows};
     a.seg[1] = GemvSeg{(const unsigned char *)wk, k, kv_rows};
     a.seg[2] = GemvSeg{(const unsigned char *)wv, v, kv_rows};
@@ -1105,7 +1187,8 @@ int tq_project_qkv_fmt(bool q4, const void *wq, const void *wk, const void *wv, 
     a.rows_total = a.seg_end[2];
     a.part = part;
     a.part_floats = part_floats;
-    return run_gemv(a, n_tok, s);
+    const int rc = quantize_input(a, xn, n_tok, hidden, xq_ws, s);
+    return rc != TQ_HIP_OK ? rc : run_gemv(a, n_tok, s);
 }
 
 int tq_project_output_fmt(bool q4, const void *wo, int rows, int cols, const float *attn, int n_tok,
@@ -1117,20 +1200,13 @@ int tq_project_output_fmt(bool q4, const void *wo, int rows, int cols, const flo
     GemvArgs a;
     init_args(a, cols);
     a.q4 = q4;
-    if (fuse_quantize(attn, n_tok, a.nb)) {
-        a.x = attn;
-        a.xq_out = (unsigned char *)xq_ws;
-    } else {
-        const hipError_t e = tq_launch_quantize(attn, xq_ws, n_tok * cols, s);
-        if (e != hipSuccess) return herr(e);
-        a.xq = (const unsigned char *)xq_ws;
-    }
     a.seg[0] = GemvSeg{(const unsigned char *)wo, out, rows};
     a.seg_end[0] = a.seg_end[1] = a.seg_end[2] = rows;
     a.rows_total = rows;
     a.part = part;
     a.part_floats = part_floats;
-    return run_gemv(a, n_tok, s);
+    const int rc = quantize_input(a, attn, n_tok, cols, xq_ws, s);
+    return rc != TQ_HIP_OK ? rc : run_gemv(a, n_tok, s);
 }
 
 // Partial floats a split-K GEMM of rows x cols needs for any token count up
@@ -1197,14 +1273,6 @@ int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn
     GemvArgs a;
     init_args(a, w->hidden);
     a.q4 = q4;
-    if (fuse_quantize(d_xn, n, a.nb)) {
-        a.x = d_xn;
-        a.xq_out = (unsigned char *)xq;
-    } else {
-        const hipError_t e = tq_launch_quantize(d_xn, xq, n * w->hidden, s);
-        if (e != hipSuccess) return herr(e);
-        a.xq = (const unsigned char *)xq;
-    }
     a.seg[0] = GemvSeg{(const unsigned char *)w->wgate, gate, w->inter};
     a.seg[1] = GemvSeg{(const unsigned char *)w->wup, up, w->inter};
     a.seg_end[0] = w->inter;
@@ -1212,21 +1280,24 @@ int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn
     a.rows_total = 2 * w->inter;
     a.part = part;
     a.part_floats = pf;
-    int rc = run_gemv(a, n, s);
+    int rc = quantize_input(a, d_xn, n, w->hidden, xq, s);
+    if (rc == TQ_HIP_OK) rc = run_gemv(a, n, s);
     if (rc != TQ_HIP_OK) return rc;
-    // :12-13 silu_mul, then quantize the hidden rows (fused)
-    hipError_t e = tq_launch_silu_quant(gate, up, xq, (long)n * w->inter, s);
-    if (e != hipSuccess) return herr(e);
-    // :14 the down matmul
+    // :14 the down matmul, over :12-13 silu_mul with the hidden rows
+    // quantized in the same launch (block_q8 rows, or the split layout)
     GemvArgs d;
     init_args(d, w->inter);
     d.q4 = q4;
     d.seg[0] = GemvSeg{(const unsigned char *)w->wdown, d_out, w->hidden};
     d.seg_end[0] = d.seg_end[1] = d.seg_end[2] = w->hidden;
     d.rows_total = w->hidden;
-    d.xq = (const unsigned char *)xq;
     d.part = part;
     d.part_floats = pf;
+    d.xs = xs_layout(d, n, xq);
+    const hipError_t e = d.xs ? tq_launch_silu_quant_split(gate, up, (unsigned char *)xq, n, w->inter, s)
+                              : tq_launch_silu_quant(gate, up, xq, (long)n * w->inter, s);
+    if (e != hipSuccess) return herr(e);
+    d.xq = (const unsigned char *)xq;
     return run_gemv(d, n, s);
 }
 

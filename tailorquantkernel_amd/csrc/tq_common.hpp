@@ -252,6 +252,14 @@ hipError_t tq_launch_accum(const float *w, size_t w_stride, int g, const block_q
 hipError_t tq_launch_softmax(float *x, int n, int rows, size_t stride, hipStream_t s);
 // h = silu(g) * u of n floats (rows of whole blocks), quantized to hq.
 hipError_t tq_launch_silu_quant(const float *gate, const float *up, block_q8 *hq, long n, hipStream_t s);
+// The same quantizations of rows x cols values into the split layout the
+// batched matmul reads, block-major: for block b of row t its codes 0-15 at
+// out + ((2b) rows + t) 16 and 16-31 at out + ((2b + 1) rows + t) 16, then
+// the fp32 scales at out + rows * cols as [b][t]; cols % 32 == 0, every
+// pointer 16-byte aligned.
+hipError_t tq_launch_quantize_split(const float *x, unsigned char *out, int rows, int cols, hipStream_t s);
+hipError_t tq_launch_silu_quant_split(const float *gate, const float *up, unsigned char *hq, int rows, int cols,
+                                      hipStream_t s);
 
 // tq_hip_project_qkv / tq_hip_project_output over tiled Q8 (q4 false) or
 // tiled Q4 (q4 true) matrices; TQ_HIP_* codes.

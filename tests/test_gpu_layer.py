@@ -424,3 +424,31 @@ def test_attention_layer_batch(nat, oracle, calls):
                                                       ws.ptr, wsb, None) == native.EINVAL
     assert max(errs) <= 1e-2 and np.median(errs) <= 1e-3, (np.median(errs), max(errs))
     kv.close()
+
+
+@pytest.mark.parametrize("n", [40, 130])
+def test_attention_layer_batch_xs(nat, oracle, n, monkeypatch):
+    """The batched layer's q/k/v and output GEMMs read the quantized rows in
+    the split layout or as block_q8 rows: bit-identical outputs and cache."""
+    lib = nat.load()
+    nq, nkv, hd, hidden, theta, eps = 8, 2, 128, 1024, 5e5, 1e-6
+    T = 160
+    w, dims = layer_weights(oracle, nq, nkv, hd, hidden, 6)
+    L = DeviceLayer(nat, w, dims, hidden, eps)
+    xn = normal(n * hidden, 60)
+    cs = [oracle.rope_table(hd, p, theta) for p in range(n)]
+    dx, dc, ds = dev(nat, xn), dev(nat, np.concatenate([c for c, _ in cs])), dev(nat, np.concatenate([s for _, s in cs]))
+    results = []
+    for xs in ("1", "0"):
+        monkeypatch.setenv("TQ_HIP_GEMM_XS", xs)
+        kv = nat.PagedKV.single(nq, nkv, hd, T)
+        wsb = lib.tq_hip_attention_layer_ws_bytes(kv.h, C_ref(L.w), n)
+        ws = nat.DeviceBuffer(wsb)
+        dout = nat.DeviceBuffer(n * hidden * 4)
+        nat.check(lib.tq_hip_attention_layer_batch_async(kv.h, C_ref(L.w), 0, 0, n, dx.ptr, dc.ptr, ds.ptr,
+                                                         dout.ptr, ws.ptr, wsb, None), "attention_layer_batch")
+        nat.check(lib.tq_hip_stream_synchronize(kv.stream), "sync")
+        gk, gv = kv.read(0, 0, n)
+        results.append((dout.download((n, hidden), np.float32).tobytes(), gk.tobytes(), gv.tobytes()))
+        kv.close()
+    assert results[0] == results[1]

@@ -76,9 +76,13 @@ def tiled(nat, Wq, rows, cols):
 @pytest.mark.parametrize("hidden,inter,n,skew", [(256, 640, 1, 0), (256, 640, 2, 0), (128, 320, 3, 0),
                                                  (512, 1024, 20, 0), (256, 640, 1, 4), (128, 320, 3, 4),
                                                  (512, 1024, 20, 4)])
-def test_mlp_layer(nat, oracle, hidden, inter, n, skew):
+def test_mlp_layer(nat, oracle, hidden, inter, n, skew, monkeypatch):
     """skew=4: xn sits 4 bytes past a 16-byte boundary, so its rows are
-    quantized by the one-value-per-lane kernel before the matmuls."""
+    quantized by the one-value-per-lane kernel before the matmuls.  The
+    quantized rows are read back from the workspace as block_q8 rows, so the
+    split layout a GEMM would read is switched off here (test_mlp_layer_xs
+    checks that it changes no bit of the output)."""
+    monkeypatch.setenv("TQ_HIP_GEMM_XS", "0")
     lib = nat.load()
     rng = np.random.default_rng(hidden + n)
     wg = oracle.pack_matrix_q8(rng.standard_normal((inter, hidden)).astype(np.float32) * 0.1)
@@ -120,7 +124,35 @@ def test_mlp_layer_split_k_off(nat, oracle, monkeypatch):
     split order); with it switched off they take the unsplit launches, under
     the same bars."""
     monkeypatch.setenv("TQ_HIP_GEMM_SPLIT", "0")
-    test_mlp_layer(nat, oracle, 512, 1024, 20, 0)
+    test_mlp_layer(nat, oracle, 512, 1024, 20, 0, monkeypatch)
+
+
+@pytest.mark.parametrize("fmt,n", [("q8", 20), ("q8", 130), ("q4", 20), ("q8", 300)])
+def test_mlp_layer_xs(nat, oracle, fmt, n, monkeypatch):
+    """The GEMM reads the quantized rows either as block_q8 rows or in the
+    split layout (codes apart from scales, conflict-free LDS reads): the same
+    codes, scales and products in the same order, so the MLP output is
+    bit-identical either way (split-K and unsplit GEMMs, Q8 and Q4)."""
+    lib = nat.load()
+    hidden, inter = 512, 1024
+    rng = np.random.default_rng(n)
+    pack = oracle.pack_matrix_q4 if fmt == "q4" else oracle.pack_matrix_q8
+    wg = pack(rng.standard_normal((inter, hidden)).astype(np.float32) * 0.1)
+    wu = pack(rng.standard_normal((inter, hidden)).astype(np.float32) * 0.1)
+    wd = pack(rng.standard_normal((hidden, inter)).astype(np.float32) * 0.1)
+    q4 = fmt == "q4"
+    G, U, Dn = tiled(nat, wg, inter, hidden), tiled(nat, wu, inter, hidden), tiled(nat, wd, hidden, inter)
+    w = nat.MlpWeights(G.ptr, U.ptr, Dn.ptr, hidden, inter, nat.FORMAT_Q4 if q4 else nat.FORMAT_Q8)
+    wsb = lib.tq_hip_mlp_ws_bytes(C.byref(w), n)
+    ws = nat.DeviceBuffer(wsb)
+    dx, dout = dev(nat, normal(n * hidden, 9) * 2), nat.DeviceBuffer(n * hidden * 4)
+    outs = []
+    for xs in ("1", "0"):
+        monkeypatch.setenv("TQ_HIP_GEMM_XS", xs)
+        nat.check(lib.tq_hip_mlp_layer_async(C.byref(w), n, dx.ptr, dout.ptr, ws.ptr, wsb, None), "mlp")
+        sync(nat)
+        outs.append(dout.download((n, hidden), np.float32))
+    assert outs[0].tobytes() == outs[1].tobytes()
 
 
 def test_add_rmsnorm(nat, oracle):
