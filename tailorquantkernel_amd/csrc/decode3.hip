@@ -420,12 +420,19 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
 #pragma clang fp contract(off)
             const float *src = lane < G ? stq + lane * HD : stk;
             float sum = 0.0f;
-            for (int i = 0; i < HD; i += 4) {
-                const v4f v = *reinterpret_cast<const v4f *>(src + i);
-                sum += v.x * v.x;
-                sum += v.y * v.y;
-                sum += v.z * v.z;
-                sum += v.w * v.w;
+            // eight loads in flight, then their adds in element order: the
+            // chain waits on LDS HD / 32 times, not HD / 4
+            for (int i0 = 0; i0 < HD; i0 += 32) {
+                v4f v[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = *reinterpret_cast<const v4f *>(src + i0 + 4 * j);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    sum += v[j].x * v[j].x;
+                    sum += v[j].y * v[j].y;
+                    sum += v[j].z * v[j].z;
+                    sum += v[j].w * v[j].w;
+                }
             }
             stinv[lane] = 1.0f / sqrtf(a.rms_eps + sum / (float)HD);
         }
