@@ -471,6 +471,11 @@ int decode_common(tq_hip_kv *kv, int n_q, const int32_t *d_seq, const int32_t *d
     // stay ahead (234 against 240 us at 16 x 32k tokens).
     const int g = D.n_q_heads / D.n_kv_heads;
     int waves = n_q > 1 && g <= 4 ? 8 : 4;
+    // one query over at most 256 keys: eight waves of one 32-key tile each in
+    // one work-group per kv head, with no split-K combine (its store, counter
+    // and pull cost more than the tiles: 8B shape at 256 keys 7.1 -> 6.2 us,
+    // 8q/2kv/hd64 6.6 -> 5.3 us; from 384 keys on the splits win)
+    if (n_q == 1 && max_len <= 8 * 32) waves = 8;
     if (decode3_waves_env()) waves = decode3_waves_env();
     if (v3)
         plan_splits3(kv, n_q, max_len, waves, &a.split_tokens, &a.n_splits);
