@@ -180,7 +180,39 @@ struct StageArgs {
     // null: rows [pos0, pos0 + n) are already in the cache
     const float *k_new;
     const float *v_new;
+    // RMSNorm weights of q and of the new K rows (applied before RoPE), or null
+    const float *q_norm;
+    const float *k_norm;
+    float rms_eps;
 };
+
+// 1 / rms of an hd-value row, as model/rmsnorm.c:4-12 computes it: the
+// squares summed serially in element order, then a correctly rounded sqrt and
+// divide; eight 16-byte loads in flight at a time.
+template <int HD>
+__device__ __forceinline__ float row_inv_rms(const float *row, float eps) {
+#pragma clang fp contract(off)
+    float sum = 0.0f;
+    for (int i0 = 0; i0 < HD; i0 += 32) {
+        v4f v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = *reinterpret_cast<const v4f *>(row + i0 + 4 * j);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            sum += v[j].x * v[j].x;
+            sum += v[j].y * v[j].y;
+            sum += v[j].z * v[j].z;
+            sum += v[j].w * v[j].w;
+        }
+    }
+    return 1.0f / sqrtf(eps + sum / (float)HD);
+}
+
+// (x * inv) * w, rounded as model/rmsnorm.c:14-18 does, on four values.
+__device__ __forceinline__ v4f norm4(v4f x, float inv, v4f w) {
+#pragma clang fp contract(off)
+    return v4f{x.x * inv * w.x, x.y * inv * w.y, x.z * inv * w.z, x.w * inv * w.w};
+}
 
 template <int HD, int G, int NJ>
 struct PShape {
@@ -214,6 +246,19 @@ __device__ __forceinline__ void stage_q(const StageArgs &a, int kvh, int blk) {
     const int i0 = blk * S::QB;
     unsigned char *qc = a.qimg + ((size_t)kvh * a.qblocks + blk) * S::Q_BYTES;
     float *qd = reinterpret_cast<float *>(qc + S::RW * S::QCS);
+    // with q_norm: 1/rms of each of the RW rows, one row per thread
+    __shared__ float inv_s[S::RW];
+    if (a.q_norm) {
+        static_assert(S::RW <= kThreads, "one row per thread");
+        if (tid < S::RW) {
+            const int r = tid, nt = r >> 4;
+            const int qi = i0 + (nt % S::QT) * 16 + (r & 15);
+            inv_s[r] = qi < a.n ? row_inv_rms<HD>(a.q + ((size_t)qi * a.n_q_heads + (size_t)kvh * G + nt / S::QT) * HD,
+                                                  a.rms_eps)
+                                : 0.0f;
+        }
+        __syncthreads();
+    }
     constexpr int TB = TASKS > 4 ? 4 : TASKS;       // tasks whose loads are in flight together
     static_assert(TASKS % TB == 0, "whole task batches");
 #pragma unroll
@@ -234,6 +279,16 @@ __device__ __forceinline__ void stage_q(const StageArgs &a, int kvh, int blk) {
                 cs[t] = *reinterpret_cast<const v4f *>(a.cos_t + (size_t)qi * HALF + 4 * c);
                 sn[t] = *reinterpret_cast<const v4f *>(a.sin_t + (size_t)qi * HALF + 4 * c);
             }
+        }
+    }
+    if (a.q_norm) {
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const int k = tid + kThreads * (t0 + t);
+            const int r = k / CPR, c = k % CPR;
+            const float inv = inv_s[r];
+            xl[t] = norm4(xl[t], inv, *reinterpret_cast<const v4f *>(a.q_norm + 4 * c));
+            xu[t] = norm4(xu[t], inv, *reinterpret_cast<const v4f *>(a.q_norm + HALF + 4 * c));
         }
     }
 #pragma unroll
@@ -314,6 +369,17 @@ __global__ __launch_bounds__(kThreads) void prefill_stage_kernel(StageArgs a) {
     // partner x[HD/2+4c..+3]; the 8 lanes of a 32-value block share their row,
     // so a whole block is computed or skipped together.
     const bool has_new = a.k_new && t0 + kKT > a.pos0 && t0 < a.kend;
+    // with k_norm: 1/rms of each new K row of the tile, one row per thread
+    __shared__ float kinv_s[kKT];
+    if (has_new && a.k_norm) {
+        if (tid < kKT) {
+            const int p = t0 + tid;
+            kinv_s[tid] = fresh(p, page[tid / kPage])
+                              ? row_inv_rms<HD>(a.k_new + ((size_t)(p - a.pos0) * v.n_kv_heads + kvh) * HD, a.rms_eps)
+                              : 0.0f;
+        }
+        __syncthreads();
+    }
     if (has_new) {
         constexpr int HALF = HD / 2;
         constexpr int CPR = HD / 8;
@@ -334,6 +400,10 @@ __global__ __launch_bounds__(kThreads) void prefill_stage_kernel(StageArgs a) {
                 const float *src = (kv ? a.v_new : a.k_new) + (row * v.n_kv_heads + kvh) * HD;
                 xl[t] = *reinterpret_cast<const v4f *>(src + 4 * c);
                 xu[t] = *reinterpret_cast<const v4f *>(src + HALF + 4 * c);
+                if (!kv && a.k_norm) {
+                    xl[t] = norm4(xl[t], kinv_s[r], *reinterpret_cast<const v4f *>(a.k_norm + 4 * c));
+                    xu[t] = norm4(xu[t], kinv_s[r], *reinterpret_cast<const v4f *>(a.k_norm + HALF + 4 * c));
+                }
                 if (!kv && rot) {
                     cs[t] = *reinterpret_cast<const v4f *>(a.cos_t + row * HALF + 4 * c);
                     sn[t] = *reinterpret_cast<const v4f *>(a.sin_t + row * HALF + 4 * c);
@@ -853,6 +923,9 @@ hipError_t launch_hd_g(const TqPrefillArgs &t, const PrefillArgs &a, hipStream_t
     st.qimg = const_cast<unsigned char *>(a.qimg);
     st.k_new = t.k_new;
     st.v_new = t.v_new;
+    st.q_norm = t.q_norm;
+    st.k_norm = t.k_norm;
+    st.rms_eps = t.rms_eps;
     hipLaunchKernelGGL((prefill_stage_kernel<HD, G, NJ>), dim3(a.n_tiles + a.qblocks, t.n_kv_heads), dim3(kThreads),
                        0, s, st);
     hipError_t e = hipGetLastError();

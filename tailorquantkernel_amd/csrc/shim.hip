@@ -974,9 +974,12 @@ bool prefill_takes_dense(const tq_hip_kv *kv, int pos0, int n, const float *d_q,
 }
 
 // tq_hip_prefill_async; `done` (the synchronous entry point's completion
-// flags) is armed when the decode form runs.
+// flags) is armed when the decode form runs.  With q_norm / k_norm (16-byte
+// aligned) the staging launch normalizes q and the new K rows itself; only
+// the dense form with the fused append takes them (check prefill_fuses_norm).
 int prefill_impl(tq_hip_kv *kv, int seq, int pos0, int n, const float *d_q, const float *d_k, const float *d_v,
-                 const float *d_cos, const float *d_sin, float *d_out, hipStream_t s, DoneFlags *done) {
+                 const float *d_cos, const float *d_sin, float *d_out, hipStream_t s, DoneFlags *done,
+                 const float *q_norm = nullptr, const float *k_norm = nullptr, float rms_eps = 0.0f) {
     const tq_hip_kv_desc &D = kv->desc;
     // one token: store_kv + attend as the decode step, one launch
     // (model/attention_layer.c:221-236 with n == 1)
@@ -993,9 +996,13 @@ int prefill_impl(tq_hip_kv *kv, int seq, int pos0, int n, const float *d_q, cons
         TQ_TRY(tq_launch_append(kv->view, n, nullptr, nullptr, seq, pos0, d_k, d_v, d_cos, d_sin,
                                 kv->desc.head_dim, s));
     if (dense) {
+        if (q_norm && !fused) return TQ_HIP_EINVAL;   // the caller checks prefill_fuses_norm first
         TqPrefillArgs t;
         t.k_new = fused ? d_k : nullptr;
         t.v_new = fused ? d_v : nullptr;
+        t.q_norm = q_norm;
+        t.k_norm = k_norm;
+        t.rms_eps = rms_eps;
         t.view = kv->view;
         t.seq = seq;
         t.pos0 = pos0;
@@ -1023,8 +1030,21 @@ int prefill_impl(tq_hip_kv *kv, int seq, int pos0, int n, const float *d_q, cons
         t.counters = kv->pcounters;
         return herr(tq_launch_prefill(t, s));
     }
+    if (q_norm) return TQ_HIP_EINVAL;
     return decode_common(kv, n, nullptr, nullptr, 0, seq, 0, pos0, pos0 + n, d_q, d_cos, d_sin, nullptr, nullptr,
                          d_out, s, seq, nullptr, nullptr, 0.0f, nullptr, done);
+}
+
+// Whether a prefill with these pointers takes the dense form with the append
+// in its staging launch, which can normalize q and K too
+// (TQ_HIP_PREFILL_FUSED_NORM=0 keeps the separate norm launches).
+bool prefill_fuses_norm(const tq_hip_kv *kv, int pos0, int n, const float *d_q, const float *d_k, const float *d_v,
+                        const float *d_cos, const float *d_sin, const float *d_out, const float *q_norm,
+                        const float *k_norm) {
+    const char *e = getenv("TQ_HIP_PREFILL_FUSED_NORM");
+    const bool on = !(e && e[0] == '0');
+    return on && prefill_takes_dense(kv, pos0, n, d_q, d_cos, d_sin, d_out) &&
+           (((uintptr_t)d_k | (uintptr_t)d_v | (uintptr_t)q_norm | (uintptr_t)k_norm) & 15) == 0;
 }
 }  // namespace
 
@@ -1169,11 +1189,17 @@ int tq_hip_attention_layer_batch_async(tq_hip_kv *kv, const tq_hip_attn_weights 
     const bool q4 = w->format == TQ_HIP_FORMAT_Q4;
     int rc = tq_project_qkv_fmt(q4, w->wq, w->wk, w->wv, qd, kd, w->hidden, d_xn, n, xq, q, k, v, s, part, pf);
     if (rc != TQ_HIP_OK) return rc;
-    // :227-228 norm_heads on every token's q and k rows
-    TQ_TRY(tq_launch_rmsnorm_rows(q, w->q_norm, q, n * D.n_q_heads, D.head_dim, w->rms_eps, hs));
-    TQ_TRY(tq_launch_rmsnorm_rows(k, w->k_norm, k, n * D.n_kv_heads, D.head_dim, w->rms_eps, hs));
-    // :230-235 RoPE, store_kv and causal attention for the n tokens
-    rc = tq_hip_prefill_async(kv, seq, pos0, n, q, k, v, d_cos, d_sin, attn, s);
+    // :227-228 norm_heads on every token's q and k rows: in the prefill's
+    // staging launch where it takes them, else two row launches
+    if (prefill_fuses_norm(kv, pos0, n, q, k, v, d_cos, d_sin, attn, w->q_norm, w->k_norm)) {
+        // :230-235 RoPE, store_kv and causal attention for the n tokens
+        rc = prefill_impl(kv, seq, pos0, n, q, k, v, d_cos, d_sin, attn, hs, nullptr, w->q_norm, w->k_norm,
+                          w->rms_eps);
+    } else {
+        TQ_TRY(tq_launch_rmsnorm_rows(q, w->q_norm, q, n * D.n_q_heads, D.head_dim, w->rms_eps, hs));
+        TQ_TRY(tq_launch_rmsnorm_rows(k, w->k_norm, k, n * D.n_kv_heads, D.head_dim, w->rms_eps, hs));
+        rc = tq_hip_prefill_async(kv, seq, pos0, n, q, k, v, d_cos, d_sin, attn, s);
+    }
     if (rc != TQ_HIP_OK) return rc;
     // :238-241 quantize the attention rows, then the batched output projection
     return tq_project_output_fmt(q4, w->wo, w->hidden, qd, attn, n, xq, d_out, s, part, pf);

@@ -320,6 +320,12 @@ struct TqPrefillArgs {
     unsigned char *img;    // tq_prefill_image_bytes() of scratch: the staged key tiles and q blocks
     float *partials;       // split-K partials (tq_prefill_scratch bytes)
     int *counters;         // split-K arrival counters, zero between launches
+    // RMSNorm weights [hd] of the q heads and of the new K rows, applied by the
+    // staging launch before RoPE (model/attention_layer.c:227-228), or null: q
+    // and k_new are already normalized.  k_norm needs k_new.
+    const float *q_norm;
+    const float *k_norm;
+    float rms_eps;
 };
 // Scratch the prefill of tokens [pos0, pos0+n) needs beyond the image: split-K
 // partials (bytes) and arrival counters (ints, zero-initialised by the caller).

@@ -366,13 +366,16 @@ def ws_views(raw, nq, nkv, hd, hidden, n):
 
 
 @pytest.mark.parametrize("calls", [[(0, 40), (40, 24)], [(0, 8), (8, 1), (9, 17)], [(0, 130)]])
-def test_attention_layer_batch(nat, oracle, calls):
+def test_attention_layer_batch(nat, oracle, calls, monkeypatch):
     """attention_layer_batch on the device, checked link by link from its own
     intermediates (left in the workspace): the normalized q/k against the
     oracle's projections + rmsnorm, the attention and the cache against the
     oracle's prefill started from the GPU's normalized q/k/v (cache bit-exact),
     the output against the oracle's output projection of the GPU's attention;
-    and end to end against an independent oracle run."""
+    and end to end against an independent oracle run.  The norm runs as its
+    own launches here, so that the workspace holds the normalized rows
+    (test_attention_layer_batch_fused_norm checks the fused form against it)."""
+    monkeypatch.setenv("TQ_HIP_PREFILL_FUSED_NORM", "0")
     from oracle.binding import BLOCK_Q8
     lib = nat.load()
     nq, nkv, hd, hidden, theta, eps = 8, 2, 128, 1024, 5e5, 1e-6
@@ -441,6 +444,36 @@ def test_attention_layer_batch_xs(nat, oracle, n, monkeypatch):
     results = []
     for xs in ("1", "0"):
         monkeypatch.setenv("TQ_HIP_GEMM_XS", xs)
+        kv = nat.PagedKV.single(nq, nkv, hd, T)
+        wsb = lib.tq_hip_attention_layer_ws_bytes(kv.h, C_ref(L.w), n)
+        ws = nat.DeviceBuffer(wsb)
+        dout = nat.DeviceBuffer(n * hidden * 4)
+        nat.check(lib.tq_hip_attention_layer_batch_async(kv.h, C_ref(L.w), 0, 0, n, dx.ptr, dc.ptr, ds.ptr,
+                                                         dout.ptr, ws.ptr, wsb, None), "attention_layer_batch")
+        nat.check(lib.tq_hip_stream_synchronize(kv.stream), "sync")
+        gk, gv = kv.read(0, 0, n)
+        results.append((dout.download((n, hidden), np.float32).tobytes(), gk.tobytes(), gv.tobytes()))
+        kv.close()
+    assert results[0] == results[1]
+
+
+@pytest.mark.parametrize("n", [40, 130])
+def test_attention_layer_batch_fused_norm(nat, oracle, n, monkeypatch):
+    """The q/k RMSNorm of attention_layer_batch either in the prefill's staging
+    launch (the default where the dense prefill appends) or as two row launches
+    (TQ_HIP_PREFILL_FUSED_NORM=0): the same serial sums and roundings, so the
+    outputs and every cache byte are identical."""
+    lib = nat.load()
+    nq, nkv, hd, hidden, theta, eps = 8, 2, 128, 1024, 5e5, 1e-6
+    T = 160
+    w, dims = layer_weights(oracle, nq, nkv, hd, hidden, 7)
+    L = DeviceLayer(nat, w, dims, hidden, eps)
+    xn = normal(n * hidden, 70)
+    cs = [oracle.rope_table(hd, p, theta) for p in range(n)]
+    dx, dc, ds = dev(nat, xn), dev(nat, np.concatenate([c for c, _ in cs])), dev(nat, np.concatenate([s for _, s in cs]))
+    results = []
+    for fused in ("1", "0"):
+        monkeypatch.setenv("TQ_HIP_PREFILL_FUSED_NORM", fused)
         kv = nat.PagedKV.single(nq, nkv, hd, T)
         wsb = lib.tq_hip_attention_layer_ws_bytes(kv.h, C_ref(L.w), n)
         ws = nat.DeviceBuffer(wsb)
