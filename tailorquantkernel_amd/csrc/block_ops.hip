@@ -37,10 +37,7 @@ __global__ __launch_bounds__(256) void silu_quant8_kernel(const float *__restric
     const float g[4] = {g4.x, g4.y, g4.z, g4.w}, u[4] = {u4.x, u4.y, u4.z, u4.w};
     float h[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float sig = 1.0f / (1.0f + expf(-g[i]));
-        h[i] = g[i] * sig * u[i];
-    }
+    for (int i = 0; i < 4; i++) h[i] = silu_mul(g[i], u[i]);
     if (scales) {
         quantize8x4(h, scales + bq * n + tq, hq + ((2 * bq + (e >> 2)) * n + tq) * 16 + 4 * (e & 3), e == 0);
     } else {

@@ -168,6 +168,10 @@ struct GemvArgs {
     int ksplit;               // GEMM: K splits of this launch (1: none)
     bool xs;                  // GEMM: xq holds the block-major split layout of
                               // tq_launch_quantize_split instead of block_q8 rows
+    unsigned char *hq;        // GEMM over the MLP's gate (segment 0) and up (segment 1)
+                              // matrices: each tile pairs 64 rows of both, and the
+                              // epilogue writes silu_mul + quantize_row_q8 of the
+                              // hidden rows in the split layout here instead of y
 };
 
 typedef __attribute__((address_space(3))) unsigned char lds_u8;
@@ -523,9 +527,18 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
     if constexpr (uni) {
         const bool s0 = row0 < a.seg_end[0], s1 = !s0 && row0 < a.seg_end[1];
         useg = s0 ? a.seg[0].w : (s1 ? a.seg[1].w : a.seg[2].w);
-        const int rows = s0 ? a.seg[0].rows : (s1 ? a.seg[1].rows : a.seg[2].rows);
-        const int start = s0 ? 0 : (s1 ? a.seg_end[0] : a.seg_end[1]);
-        const int r = row0 + my_row < a.rows_total ? row0 + my_row : a.rows_total - 1;
+        int rows = s0 ? a.seg[0].rows : (s1 ? a.seg[1].rows : a.seg[2].rows);
+        int start = s0 ? 0 : (s1 ? a.seg_end[0] : a.seg_end[1]);
+        int r = row0 + my_row < a.rows_total ? row0 + my_row : a.rows_total - 1;
+        if (a.hq) {
+            // paired tile rt: rows 64 rt.. of the gate matrix, then the same
+            // rows of the up matrix.  A wave's copies all lie in one half
+            // (row tid % 128 = 64 (wave & 1) + lane), so its base stays uniform.
+            useg = (wave & 1) ? a.seg[1].w : a.seg[0].w;
+            rows = a.seg[0].rows;
+            start = 0;
+            r = 64 * rt + lane;
+        }
         const uint32_t rowb = Q4 ? (uint32_t)cols / 2 : (uint32_t)cols;
         uscale = (size_t)rows * rowb;
         vrow = (uint32_t)(r - start) * rowb;
@@ -727,6 +740,44 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(GemvArgs a) {
 
     // y[t][r]: lane (l16, lg) holds rows 4lg..4lg+3 of each 16-row tile for
     // token l16 of each 16-token tile.  A split writes its partial instead.
+    if (UNI && XS && a.hq) {
+        // the paired tile's gate (rows 0-63) and up (rows 64-127) values meet
+        // in LDS as [token][row] with 132-float token rows (a float4 store of
+        // 16 tokens then covers all 64 banks); then h = silu(g) * u of the
+        // tile's two 32-row blocks, quantized as silu_quant8_kernel does, 8
+        // lanes x 4 values per (block, token), written in the split layout
+        // (codes of block b, token t at ((2b + half) n + t) 16, scales [b][t]
+        // after the n * inter code bytes)
+        constexpr int kHs = kGemmRows + 4;
+        static_assert(kGemmToks * kHs * 4 <= kGemmBufs * kGemmStage, "the fp32 tile fits the stage buffers");
+        float *hs = reinterpret_cast<float *>(smem);
+        __syncthreads();   // every wave is done with the last stage
+#pragma unroll
+        for (int r2 = 0; r2 < 2; r2++)
+#pragma unroll
+            for (int t4 = 0; t4 < 4; t4++)
+                *reinterpret_cast<float4 *>(hs + (wt + 16 * t4 + l16) * kHs + wr + 16 * r2 + 4 * lg) =
+                    make_float4(acc[r2][t4][0], acc[r2][t4][1], acc[r2][t4][2], acc[r2][t4][3]);
+        __syncthreads();
+        const int n = a.n_tok, inter = a.seg[0].rows;
+        float *scales = reinterpret_cast<float *>(a.hq + (size_t)n * inter);
+        // (block, token) units in block-major order: consecutive units are
+        // consecutive tokens, so a wave's code stores are 128 contiguous bytes
+#pragma unroll
+        for (int j = 0; j < 2 * kGemmToks * 8 / kGemmThreads; j++) {
+            const int q = tid + kGemmThreads * j;
+            const int e = q & 7, bl = q >> 10, tk = (q >> 3) & (kGemmToks - 1);
+            const int t = tok0 + tk;
+            if (t >= n) continue;   // whole 8-lane groups share t
+            const float4 g4 = *reinterpret_cast<const float4 *>(hs + tk * kHs + 32 * bl + 4 * e);
+            const float4 u4 = *reinterpret_cast<const float4 *>(hs + tk * kHs + 64 + 32 * bl + 4 * e);
+            const float h[4] = {silu_mul(g4.x, u4.x), silu_mul(g4.y, u4.y), silu_mul(g4.z, u4.z),
+                                silu_mul(g4.w, u4.w)};
+            const size_t gb = 2 * (size_t)rt + bl;
+            quantize8x4(h, scales + gb * n + t, a.hq + ((2 * gb + (e >> 2)) * n + t) * 16 + 4 * (e & 3), e == 0);
+        }
+        return;
+    }
     if (a.ksplit > 1) {
         float *p = a.part + (size_t)ks * a.n_tok * a.rows_total;
 #pragma unroll
@@ -919,6 +970,11 @@ hipError_t launch_gemm(const GemvArgs &a, int ksplit, hipStream_t s) {
     u.ksplit = ksplit;
     u.uni_tiles = gemm_uniform(a);
     if (a.xs && !(bx4 && u.uni_tiles)) return hipErrorInvalidValue;   // the caller's plan and this disagree
+    // paired gate/up tiles: one unsplit split-layout GEMM over two segments
+    // of equal rows, a multiple of 64
+    if (a.hq && (ksplit != 1 || !a.xs || a.seg[0].rows != a.seg[1].rows || a.seg[0].rows % 64 != 0 ||
+                 a.rows_total != 2 * a.seg[0].rows))
+        return hipErrorInvalidValue;
     const dim3 g((unsigned)grid), b(kGemmThreads);
     if (a.q4) {
         if (a.xs)
@@ -1285,10 +1341,8 @@ int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn
     a.part = part;
     a.part_floats = pf;
     int rc = quantize_input(a, d_xn, n, w->hidden, xq, s);
-    if (rc == TQ_HIP_OK) rc = run_gemv(a, n, s);
     if (rc != TQ_HIP_OK) return rc;
-    // :14 the down matmul, over :12-13 silu_mul with the hidden rows
-    // quantized in the same launch (block_q8 rows, or the split layout)
+    // :14 the down matmul, over :12-13 silu_mul with the hidden rows quantized
     GemvArgs d;
     init_args(d, w->inter);
     d.q4 = q4;
@@ -1297,6 +1351,23 @@ int tq_hip_mlp_layer_async(const tq_hip_mlp_weights *w, int n, const float *d_xn
     d.rows_total = w->hidden;
     d.part = part;
     d.part_floats = pf;
+    // When the gate/up matmul is one unsplit GEMM over the split layout and
+    // the down matmul reads the split layout too, the gate/up tiles pair 64
+    // rows of both matrices and their epilogue writes the quantized hidden
+    // rows (into the gate rows' space, which they then no longer need);
+    // otherwise gate and up rows go to the workspace and one more launch
+    // forms them (block_q8 rows, or the split layout).  TQ_HIP_MLP_FUSED=0
+    // keeps the separate launch.
+    const bool fused = a.xs && gemm_plan(a, n) == 1 && xs_layout(d, n, gate) &&
+                       env_int("TQ_HIP_MLP_FUSED", 1) != 0;
+    if (fused) a.hq = (unsigned char *)gate;
+    rc = run_gemv(a, n, s);
+    if (rc != TQ_HIP_OK) return rc;
+    if (fused) {
+        d.xs = true;
+        d.xq = (const unsigned char *)gate;
+        return run_gemv(d, n, s);
+    }
     d.xs = xs_layout(d, n, xq);
     const hipError_t e = d.xs ? tq_launch_silu_quant_split(gate, up, (unsigned char *)xq, n, w->inter, s)
                               : tq_launch_silu_quant(gate, up, xq, (long)n * w->inter, s);

@@ -148,6 +148,15 @@ __device__ __forceinline__ void quantize8x4(const float (&x)[4], float *d_out, u
     *reinterpret_cast<uint32_t *>(codes) = w;
 }
 
+// h = silu(g) * u with silu(x) = x * (1 / (1 + expf(-x))) (model/silu.c:6-18,
+// model/mlp.c:12-13), evaluated left to right with no contraction: every
+// kernel that forms the MLP's hidden rows uses this one definition.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+    const float sig = 1.0f / (1.0f + expf(-g));
+    return g * sig * u;
+}
+
 // ---------------------------------------------------------------------------
 // RoPE, rotate-half pairing i <-> i + hd/2 (model/rope.c:14-22):
 //   lower half: x0*c - x1*s      upper half: x0*s + x1*c

@@ -155,6 +155,59 @@ def test_mlp_layer_xs(nat, oracle, fmt, n, monkeypatch):
     assert outs[0].tobytes() == outs[1].tobytes()
 
 
+@pytest.mark.parametrize("fmt,hidden,inter,n,split", [("q8", 512, 1024, 130, "0"), ("q8", 512, 1024, 300, "0"),
+                                                     ("q4", 512, 1024, 300, "0"), ("q8", 512, 4096, 520, "1")])
+def test_mlp_layer_fused(nat, oracle, fmt, hidden, inter, n, split, monkeypatch):
+    """An unsplit gate/up GEMM pairs 64 rows of both matrices per tile and
+    its epilogue forms the down matmul's input itself: silu_mul of the same
+    fp32 gate and up values, quantized as the separate launch does.  The
+    hidden rows it leaves in the workspace (the gate rows' space) equal byte
+    for byte the separate launch's (TQ_HIP_MLP_FUSED=0), which also proves
+    that the fused path ran; the output is bit-identical; and the output of
+    the first and last token is within the matmul bar of the oracle's down
+    projection of those rows.  Ragged token counts (130, 300, 520), Q8 and
+    Q4; split "0" forces the unsplit GEMM at small counts, at 520 tokens over
+    4096 rows it is the default plan (the down matmul still splits K)."""
+    lib = nat.load()
+    monkeypatch.setenv("TQ_HIP_GEMM_SPLIT", split)
+    rng = np.random.default_rng(inter + n)
+    q4 = fmt == "q4"
+    pack = oracle.pack_matrix_q4 if q4 else oracle.pack_matrix_q8
+    wg = pack(rng.standard_normal((inter, hidden)).astype(np.float32) * 0.1)
+    wu = pack(rng.standard_normal((inter, hidden)).astype(np.float32) * 0.1)
+    wd = pack(rng.standard_normal((hidden, inter)).astype(np.float32) * 0.1)
+    G, U, Dn = tiled(nat, wg, inter, hidden), tiled(nat, wu, inter, hidden), tiled(nat, wd, hidden, inter)
+    w = nat.MlpWeights(G.ptr, U.ptr, Dn.ptr, hidden, inter, nat.FORMAT_Q4 if q4 else nat.FORMAT_Q8)
+    wsb = lib.tq_hip_mlp_ws_bytes(C.byref(w), n)
+    ws = nat.DeviceBuffer(wsb)
+    dx, dout = dev(nat, normal(n * hidden, 11) * 2), nat.DeviceBuffer(n * hidden * 4)
+    al = lambda b: (b + 255) & ~255
+    hq_bytes = n * inter + n * (inter // QK) * 4
+    outs, hqs = [], []
+    for fused in ("1", "0"):
+        monkeypatch.setenv("TQ_HIP_MLP_FUSED", fused)
+        nat.check(lib.tq_hip_mlp_layer_async(C.byref(w), n, dx.ptr, dout.ptr, ws.ptr, wsb, None), "mlp")
+        sync(nat)
+        outs.append(dout.download((n, hidden), np.float32))
+        raw = ws.download((wsb,), np.uint8)
+        off = 0 if fused == "1" else 2 * al(n * inter * 4)
+        hqs.append(raw[off:off + hq_bytes].copy())
+    assert hqs[0].tobytes() == hqs[1].tobytes()
+    assert outs[0].tobytes() == outs[1].tobytes()
+    # the split layout back to block_q8 rows: codes of block b, token t at
+    # ((2b + half) n + t) 16, scales [b][t] after the n * inter code bytes
+    nbi = inter // QK
+    codes = hqs[0][:n * inter].view(np.int8).reshape(nbi, 2, n, 16)
+    scales = hqs[0][n * inter:].view(np.float32).reshape(nbi, n)
+    for t in (0, n - 1):
+        rows = np.zeros(nbi, BLOCK_Q8)
+        rows["d"] = scales[:, t]
+        rows["q"] = codes[:, :, t, :].reshape(nbi, QK)
+        mm = oracle.matmul_q4 if q4 else oracle.matmul_q8
+        ref = mm(wd, rows, hidden, inter, 1)[0]
+        assert rel_l2(outs[0][t], ref) <= 1e-5
+
+
 def test_add_rmsnorm(nat, oracle):
     lib = nat.load()
     # 1024-thread kernel holding 1, 2, 4 and 8 float4 per thread, and the
