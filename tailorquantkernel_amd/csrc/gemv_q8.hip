@@ -1269,6 +1269,36 @@ int tq_project_output_fmt(bool q4, const void *wo, int rows, int cols, const flo
     return rc != TQ_HIP_OK ? rc : run_gemv(a, n_tok, s);
 }
 
+static void output_args(GemvArgs &a, bool q4, const void *wo, int rows, int cols, float *out, float *part,
+                        size_t part_floats) {
+    init_args(a, cols);
+    a.q4 = q4;
+    a.seg[0] = GemvSeg{(const unsigned char *)wo, out, rows};
+    a.seg_end[0] = a.seg_end[1] = a.seg_end[2] = rows;
+    a.rows_total = rows;
+    a.part = part;
+    a.part_floats = part_floats;
+}
+
+bool tq_project_output_takes_xs(bool q4, const void *wo, int rows, int cols, int n_tok, const void *xq_ws,
+                                float *part, size_t part_floats) {
+    if (!shape_ok(rows, cols) || n_tok <= 2 || !wo || !xq_ws || !aligned(wo, 16)) return false;
+    GemvArgs a;
+    output_args(a, q4, wo, rows, cols, nullptr, part, part_floats);
+    return xs_layout(a, n_tok, xq_ws);
+}
+
+int tq_project_output_xs(bool q4, const void *wo, int rows, int cols, const void *xq_ws, int n_tok, float *out,
+                         void *stream, float *part, size_t part_floats) {
+    if (!out || !aligned(out, 4) || !tq_project_output_takes_xs(q4, wo, rows, cols, n_tok, xq_ws, part, part_floats))
+        return TQ_HIP_EINVAL;
+    GemvArgs a;
+    output_args(a, q4, wo, rows, cols, out, part, part_floats);
+    a.xs = true;
+    a.xq = (const unsigned char *)xq_ws;
+    return run_gemv(a, n_tok, (hipStream_t)stream);
+}
+
 // Partial floats a split-K GEMM of rows x cols needs for any token count up
 // to n_cap: the largest S * n over the token-tile counts that still split.
 size_t tq_gemm_partial_floats(int rows, int cols, int n_cap) {

@@ -496,6 +496,7 @@ struct PrefillArgs {
     int *counters;       // [n_kv][qblocks] x kCounterStrideP
     const unsigned char *qimg;   // [n_kv][qblocks][PShape::Q_BYTES] (prefill_stage_kernel)
     float *out;          // [n][n_q_heads][hd]
+    unsigned char *out_xs;   // or, when set, the rows quantized in the split layout
     int n_q_heads;
     float scale;
     int n_tiles;         // tiles per kv head in the image buffer
@@ -718,6 +719,52 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
 #pragma unroll
     for (int j = 0; j < NJ; j++) lrow[j] = xrow_sum(lsum[j]);
     auto store_out = [&]() {
+        if (a.out_xs) {
+            // quantize_row_q8 of each row: block b of a head is columns
+            // 32b..32b+31, tiles m = 2b (codes 0-15) and 2b+1 (codes 16-31),
+            // 8 values in each of the 4 lanes of the query (lanes l16 + 16 lg);
+            // the absmax as quantize8x4 takes it (|x|, NaN and -0 as 0, an
+            // exact max), then the same scale, inverse and codes as a
+            // separate quantize launch over the stored rows
+            const size_t nrows = (size_t)a.n, cols = (size_t)a.n_q_heads * HD;
+            float *xd = reinterpret_cast<float *>(a.out_xs + nrows * cols);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const float inv = 1.0f / lrow[j];
+                const int nt = wave * NJ + j;
+                const int g = nt / S::QT;
+                const int qi = i0 + (nt % S::QT) * 16 + l16;
+#pragma unroll
+                for (int b = 0; b < HD / kQK; b++) {
+                    const v4f x0 = o[2 * b][j] * inv, x1 = o[2 * b + 1][j] * inv;
+                    float m = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float a0 = x0[i] < 0.0f ? -x0[i] : x0[i];
+                        const float a1 = x1[i] < 0.0f ? -x1[i] : x1[i];
+                        m = fmaxf(m, a0 > 0.0f ? a0 : 0.0f);
+                        m = fmaxf(m, a1 > 0.0f ? a1 : 0.0f);
+                    }
+                    m = fmaxf(m, __shfl_xor(m, 16));
+                    m = fmaxf(m, __shfl_xor(m, 32));
+                    const float d = quant_scale(m);
+                    const float qinv = quant_inverse(d);
+                    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        w0 |= quant_code(x0[i], qinv) << (8 * i);
+                        w1 |= quant_code(x1[i], qinv) << (8 * i);
+                    }
+                    if (qi < a.n) {
+                        const size_t gb = (size_t)(kvh * G + g) * (HD / kQK) + b;
+                        *reinterpret_cast<uint32_t *>(a.out_xs + ((2 * gb) * nrows + qi) * 16 + 4 * lg) = w0;
+                        *reinterpret_cast<uint32_t *>(a.out_xs + ((2 * gb + 1) * nrows + qi) * 16 + 4 * lg) = w1;
+                        if (lg == 0) xd[gb * nrows + qi] = d;
+                    }
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
             const float inv = 1.0f / lrow[j];
@@ -975,6 +1022,7 @@ hipError_t tq_launch_prefill(const TqPrefillArgs &t, hipStream_t s) {
     a.pos0 = t.pos0;
     a.n = t.n;
     a.out = t.out;
+    a.out_xs = t.out_xs;
     a.n_q_heads = t.n_q_heads;
     a.scale = t.scale;
     a.n_tiles = (t.pos0 + t.n + kKT - 1) / kKT;

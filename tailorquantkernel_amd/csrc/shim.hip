@@ -979,11 +979,12 @@ bool prefill_takes_dense(const tq_hip_kv *kv, int pos0, int n, const float *d_q,
 // the dense form with the fused append takes them (check prefill_fuses_norm).
 int prefill_impl(tq_hip_kv *kv, int seq, int pos0, int n, const float *d_q, const float *d_k, const float *d_v,
                  const float *d_cos, const float *d_sin, float *d_out, hipStream_t s, DoneFlags *done,
-                 const float *q_norm = nullptr, const float *k_norm = nullptr, float rms_eps = 0.0f) {
+                 const float *q_norm = nullptr, const float *k_norm = nullptr, float rms_eps = 0.0f,
+                 unsigned char *out_xs = nullptr) {
     const tq_hip_kv_desc &D = kv->desc;
     // one token: store_kv + attend as the decode step, one launch
     // (model/attention_layer.c:221-236 with n == 1)
-    if (n == 1)
+    if (n == 1 && !out_xs)
         return decode_common(kv, 1, nullptr, nullptr, 0, seq, 0, pos0, pos0 + 1, d_q, d_cos, d_sin, d_k, d_v,
                              d_out, s, seq, nullptr, nullptr, 0.0f, nullptr, done);
     // the dense kernel restages every key tile of [0, pos0+n): worth it from a
@@ -992,6 +993,7 @@ int prefill_impl(tq_hip_kv *kv, int seq, int pos0, int n, const float *d_q, cons
     // aligned k and v its staging launch appends the new rows too
     const bool dense = prefill_takes_dense(kv, pos0, n, d_q, d_cos, d_sin, d_out);
     const bool fused = dense && (((uintptr_t)d_k | (uintptr_t)d_v) & 15) == 0;
+    if (out_xs && !fused) return TQ_HIP_EINVAL;   // only the dense kernel quantizes its rows
     if (!fused)
         TQ_TRY(tq_launch_append(kv->view, n, nullptr, nullptr, seq, pos0, d_k, d_v, d_cos, d_sin,
                                 kv->desc.head_dim, s));
@@ -1003,6 +1005,7 @@ int prefill_impl(tq_hip_kv *kv, int seq, int pos0, int n, const float *d_q, cons
         t.q_norm = q_norm;
         t.k_norm = k_norm;
         t.rms_eps = rms_eps;
+        t.out_xs = out_xs;
         t.view = kv->view;
         t.seq = seq;
         t.pos0 = pos0;
@@ -1192,9 +1195,17 @@ int tq_hip_attention_layer_batch_async(tq_hip_kv *kv, const tq_hip_attn_weights 
     // :227-228 norm_heads on every token's q and k rows: in the prefill's
     // staging launch where it takes them, else two row launches
     if (prefill_fuses_norm(kv, pos0, n, q, k, v, d_cos, d_sin, attn, w->q_norm, w->k_norm)) {
-        // :230-235 RoPE, store_kv and causal attention for the n tokens
+        // :230-235 RoPE, store_kv and causal attention for the n tokens; when
+        // the output projection is a GEMM over the split layout, the prefill
+        // quantizes its rows straight into that layout (:238's quantization,
+        // TQ_HIP_PREFILL_QUANT_OUT=0 keeps the fp32 rows and a separate launch)
+        const char *e = getenv("TQ_HIP_PREFILL_QUANT_OUT");
+        const bool qout = !(e && e[0] == '0') &&
+                          tq_project_output_takes_xs(q4, w->wo, w->hidden, qd, n, xq, part, pf);
         rc = prefill_impl(kv, seq, pos0, n, q, k, v, d_cos, d_sin, attn, hs, nullptr, w->q_norm, w->k_norm,
-                          w->rms_eps);
+                          w->rms_eps, qout ? (unsigned char *)xq : nullptr);
+        if (rc != TQ_HIP_OK) return rc;
+        if (qout) return tq_project_output_xs(q4, w->wo, w->hidden, qd, xq, n, d_out, s, part, pf);
     } else {
         TQ_TRY(tq_launch_rmsnorm_rows(q, w->q_norm, q, n * D.n_q_heads, D.head_dim, w->rms_eps, hs));
         TQ_TRY(tq_launch_rmsnorm_rows(k, w->k_norm, k, n * D.n_kv_heads, D.head_dim, w->rms_eps, hs));

@@ -279,6 +279,14 @@ int tq_project_qkv_fmt(bool q4, const void *wq, const void *wk, const void *wv, 
                        float *part = nullptr, size_t part_floats = 0);
 int tq_project_output_fmt(bool q4, const void *wo, int rows, int cols, const float *attn, int n_tok,
                           block_q8 *xq_ws, float *out, void *stream, float *part = nullptr, size_t part_floats = 0);
+// Whether tq_project_output_fmt over n_tok rows (with this workspace and
+// partials) quantizes its input into the split layout for a GEMM; then
+// tq_project_output_xs runs the same projection from rows a producer already
+// left in that layout at xq_ws.
+bool tq_project_output_takes_xs(bool q4, const void *wo, int rows, int cols, int n_tok, const void *xq_ws,
+                                float *part, size_t part_floats);
+int tq_project_output_xs(bool q4, const void *wo, int rows, int cols, const void *xq_ws, int n_tok, float *out,
+                         void *stream, float *part, size_t part_floats);
 // Partial floats the split-K GEMM of a rows x cols matrix needs for up to n_cap tokens.
 size_t tq_gemm_partial_floats(int rows, int cols, int n_cap);
 // In place allowed (out == x); n <= 8191.
@@ -335,6 +343,11 @@ struct TqPrefillArgs {
     const float *q_norm;
     const float *k_norm;
     float rms_eps;
+    // Or null: the attention rows go to out as fp32.  Set, they are not stored
+    // as fp32; each row's quantize_row_q8 goes here instead, in the split
+    // layout tq_launch_quantize_split writes for n rows of n_q_heads * hd
+    // values (the batched output projection's input).
+    unsigned char *out_xs;
 };
 // Scratch the prefill of tokens [pos0, pos0+n) needs beyond the image: split-K
 // partials (bytes) and arrival counters (ints, zero-initialised by the caller).

@@ -458,6 +458,51 @@ def test_attention_layer_batch_xs(nat, oracle, n, monkeypatch):
 
 
 @pytest.mark.parametrize("n", [40, 130])
+def test_attention_layer_batch_quant_out(nat, oracle, n, monkeypatch):
+    """Where the output projection is a GEMM over the split layout, the
+    prefill quantizes its attention rows straight into that layout (the same
+    absmax, scale and codes as a separate quantize launch over the fp32 rows)
+    and stores no fp32 rows: with TQ_HIP_PREFILL_QUANT_OUT on and off, the
+    quantized rows in the workspace, the outputs and every cache byte are
+    identical, and with it on the fp32 attention rows' space keeps the bytes
+    it held before the call (nothing was written there)."""
+    lib = nat.load()
+    nq, nkv, hd, hidden, theta, eps = 8, 2, 128, 1024, 5e5, 1e-6
+    T = 160
+    w, dims = layer_weights(oracle, nq, nkv, hd, hidden, 9)
+    L = DeviceLayer(nat, w, dims, hidden, eps)
+    xn = normal(n * hidden, 71)
+    cs = [oracle.rope_table(hd, p, theta) for p in range(n)]
+    dx, dc, ds = dev(nat, xn), dev(nat, np.concatenate([c for c, _ in cs])), dev(nat, np.concatenate([s for _, s in cs]))
+    al = lambda b: (b + 255) & ~255
+    qd, kd = nq * hd, nkv * hd
+    oa = al(n * qd * 4) + 2 * al(n * kd * 4)
+    ox = oa + al(n * qd * 4)
+    xq_bytes = n * qd // QK * 36
+    results = []
+    for on in ("1", "0"):
+        monkeypatch.setenv("TQ_HIP_PREFILL_QUANT_OUT", on)
+        kv = nat.PagedKV.single(nq, nkv, hd, T)
+        wsb = lib.tq_hip_attention_layer_ws_bytes(kv.h, C_ref(L.w), n)
+        ws = nat.DeviceBuffer(wsb)
+        ws.upload(np.full(wsb, 0xA5, np.uint8))
+        dout = nat.DeviceBuffer(n * hidden * 4)
+        nat.check(lib.tq_hip_attention_layer_batch_async(kv.h, C_ref(L.w), 0, 0, n, dx.ptr, dc.ptr, ds.ptr,
+                                                         dout.ptr, ws.ptr, wsb, None), "attention_layer_batch")
+        nat.check(lib.tq_hip_stream_synchronize(kv.stream), "sync")
+        gk, gv = kv.read(0, 0, n)
+        raw = ws.download((wsb,), np.uint8)
+        if on == "1":
+            assert (raw[oa:oa + n * qd * 4] == 0xA5).all()
+        else:
+            assert not (raw[oa:oa + n * qd * 4] == 0xA5).all()
+        results.append((dout.download((n, hidden), np.float32).tobytes(), gk.tobytes(), gv.tobytes(),
+                        raw[ox:ox + xq_bytes].tobytes()))
+        kv.close()
+    assert results[0] == results[1]
+
+
+@pytest.mark.parametrize("n", [40, 130])
 def test_attention_layer_batch_fused_norm(nat, oracle, n, monkeypatch):
     """The q/k RMSNorm of attention_layer_batch either in the prefill's staging
     launch (the default where the dense prefill appends) or as two row launches
