@@ -457,17 +457,18 @@ def test_attention_layer_batch_xs(nat, oracle, n, monkeypatch):
     assert results[0] == results[1]
 
 
-@pytest.mark.parametrize("n", [40, 130])
-def test_attention_layer_batch_quant_out(nat, oracle, n, monkeypatch):
+@pytest.mark.parametrize("n,hd", [(40, 128), (130, 128), (130, 64)])
+def test_attention_layer_batch_quant_out(nat, oracle, n, hd, monkeypatch):
     """Where the output projection is a GEMM over the split layout, the
     prefill quantizes its attention rows straight into that layout (the same
     absmax, scale and codes as a separate quantize launch over the fp32 rows)
     and stores no fp32 rows: with TQ_HIP_PREFILL_QUANT_OUT on and off, the
     quantized rows in the workspace, the outputs and every cache byte are
     identical, and with it on the fp32 attention rows' space keeps the bytes
-    it held before the call (nothing was written there)."""
+    it held before the call (nothing was written there).  Head dims 128 and 64
+    (four and two 32-column blocks per head)."""
     lib = nat.load()
-    nq, nkv, hd, hidden, theta, eps = 8, 2, 128, 1024, 5e5, 1e-6
+    nq, nkv, hidden, theta, eps = 8, 2, 1024, 5e5, 1e-6
     T = 160
     w, dims = layer_weights(oracle, nq, nkv, hd, hidden, 9)
     L = DeviceLayer(nat, w, dims, hidden, eps)
