@@ -390,7 +390,10 @@ int tq_hip_attention_layer_async(tq_hip_kv *kv, const tq_hip_attn_weights *w, in
  * rows of d_xn [n][hidden] (the MFMA GEMM from 16 rows on), the per-head
  * RMSNorm of q and k (tq_hip_rmsnorm_rows), RoPE + KV append + causal
  * attention (tq_hip_prefill_async; d_cos/d_sin [n][head_dim/2] or NULL),
- * project_output into d_out [n][hidden].  d_ws: tq_hip_attention_layer_ws_bytes
+ * project_output into d_out [n][hidden].  Where the prefill runs its dense
+ * kernel, the q/k norm happens in its staging launch and, for a GEMM output
+ * projection, the attention rows are quantized in its store (the same bytes;
+ * the workspace then holds no fp32 attention rows).  d_ws: tq_hip_attention_layer_ws_bytes
  * bytes for n tokens, 16-byte aligned.  Returns -1 (TQ_HIP_EINVAL) for n <= 0
  * or a range past the sequence's pages before any launch, as
  * attention_layer_batch does (:203-204). */
