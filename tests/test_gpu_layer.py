@@ -503,6 +503,59 @@ def test_attention_layer_batch_quant_out(nat, oracle, n, hd, monkeypatch):
     assert results[0] == results[1]
 
 
+def test_attention_layer_batch_quant_out_split(nat, oracle, monkeypatch):
+    """The quantized store after the split path: a second chunk of 130 tokens
+    at position 1000 gives the prefill's query blocks about 35 key tiles each,
+    so their segments merge (the last to arrive sums the partials) before the
+    rows are stored.  Both chunks with TQ_HIP_PREFILL_QUANT_OUT on and off:
+    the second chunk's output, its quantized rows and the whole cache are
+    identical."""
+    lib = nat.load()
+    nq, nkv, hd, hidden, theta, eps = 8, 2, 128, 1024, 5e5, 1e-6
+    n1, n2 = 1000, 130
+    T = n1 + n2 + 16
+    w, dims = layer_weights(oracle, nq, nkv, hd, hidden, 13)
+    L = DeviceLayer(nat, w, dims, hidden, eps)
+    xn = normal((n1 + n2) * hidden, 72)
+    cs = [oracle.rope_table(hd, p, theta) for p in range(n1 + n2)]
+    cos_all = np.concatenate([c for c, _ in cs])
+    sin_all = np.concatenate([s for _, s in cs])
+    half = hd // 2
+    al = lambda b: (b + 255) & ~255
+    qd, kd = nq * hd, nkv * hd
+    results = []
+    for on in ("1", "0"):
+        monkeypatch.setenv("TQ_HIP_PREFILL_QUANT_OUT", on)
+        kv = nat.PagedKV.single(nq, nkv, hd, T)
+        wsb = lib.tq_hip_attention_layer_ws_bytes(kv.h, C_ref(L.w), n1)
+        ws = nat.DeviceBuffer(wsb)
+        out = []
+        for pos0, n in ((0, n1), (n1, n2)):
+            dx = dev(nat, xn[pos0 * hidden:(pos0 + n) * hidden])
+            dc = dev(nat, cos_all[pos0 * half:(pos0 + n) * half])
+            ds = dev(nat, sin_all[pos0 * half:(pos0 + n) * half])
+            dout = nat.DeviceBuffer(n * hidden * 4)
+            if pos0:
+                ws.upload(np.full(wsb, 0xA5, np.uint8))
+            nat.check(lib.tq_hip_attention_layer_batch_async(kv.h, C_ref(L.w), 0, pos0, n, dx.ptr, dc.ptr, ds.ptr,
+                                                             dout.ptr, ws.ptr, wsb, None), "attention_layer_batch")
+            nat.check(lib.tq_hip_stream_synchronize(kv.stream), "sync")
+            out.append(dout.download((n, hidden), np.float32).tobytes())
+        raw = ws.download((wsb,), np.uint8)
+        # the second call's fp32 attention rows: not written with the store on
+        oa = al(n2 * qd * 4) + 2 * al(n2 * kd * 4)
+        assert (raw[oa:oa + n2 * qd * 4] == 0xA5).all() == (on == "1")
+        ox = al(n2 * qd * 4) + 2 * al(n2 * kd * 4) + al(n2 * qd * 4)
+        ox_n1 = al(n1 * qd * 4) + 2 * al(n1 * kd * 4) + al(n1 * qd * 4)
+        # the layout offsets follow the call's n: the second call's xq region
+        assert ox <= ox_n1
+        gk, gv = kv.read(0, 0, n1 + n2)
+        results.append((out, raw[ox:ox + n2 * qd // QK * 36].tobytes(), gk.tobytes(), gv.tobytes()))
+        kv.close()
+    assert results[0][0] == results[1][0]
+    assert results[0][1:] == results[1][1:]
+
+
 @pytest.mark.parametrize("n", [40, 130])
 def test_attention_layer_batch_fused_norm(nat, oracle, n, monkeypatch):
     """The q/k RMSNorm of attention_layer_batch either in the prefill's staging
