@@ -246,10 +246,40 @@ __device__ __forceinline__ void stage_q(const StageArgs &a, int kvh, int blk) {
     const int i0 = blk * S::QB;
     unsigned char *qc = a.qimg + ((size_t)kvh * a.qblocks + blk) * S::Q_BYTES;
     float *qd = reinterpret_cast<float *>(qc + S::RW * S::QCS);
+    constexpr int TB = TASKS > 4 ? 4 : TASKS;       // tasks whose loads are in flight together
+    static_assert(TASKS % TB == 0, "whole task batches");
+    static_assert(kThreads % CPR == 0, "a thread's tasks share their columns");
+    v4f xl[TB], xu[TB], cs[TB], sn[TB];
+    auto load_batch = [&](int t0) {
+#pragma unroll
+        for (int t = 0; t < TB; t++) {
+            const int k = tid + kThreads * (t0 + t);
+            const int r = k / CPR, c = k % CPR;
+            const int nt = r >> 4;
+            const int qi = i0 + (nt % S::QT) * 16 + (r & 15);
+            xl[t] = xu[t] = cs[t] = sn[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (qi < a.n) {
+                const float *head = a.q + ((size_t)qi * a.n_q_heads + (size_t)kvh * G + nt / S::QT) * HD;
+                xl[t] = *reinterpret_cast<const v4f *>(head + 4 * c);
+                xu[t] = *reinterpret_cast<const v4f *>(head + HALF + 4 * c);
+                if (a.cos_t) {
+                    cs[t] = *reinterpret_cast<const v4f *>(a.cos_t + (size_t)qi * HALF + 4 * c);
+                    sn[t] = *reinterpret_cast<const v4f *>(a.sin_t + (size_t)qi * HALF + 4 * c);
+                }
+            }
+        }
+    };
+    // the first batch's loads and this thread's norm weights (every task of a
+    // thread has the same columns) are in flight while the norms are taken
+    load_batch(0);
     // with q_norm: 1/rms of each of the RW rows, one row per thread
     __shared__ float inv_s[S::RW];
+    v4f wlo = v4f{0.0f, 0.0f, 0.0f, 0.0f}, whi = wlo;
     if (a.q_norm) {
         static_assert(S::RW <= kThreads, "one row per thread");
+        const int c = tid % CPR;
+        wlo = *reinterpret_cast<const v4f *>(a.q_norm + 4 * c);
+        whi = *reinterpret_cast<const v4f *>(a.q_norm + HALF + 4 * c);
         if (tid < S::RW) {
             const int r = tid, nt = r >> 4;
             const int qi = i0 + (nt % S::QT) * 16 + (r & 15);
@@ -259,36 +289,16 @@ __device__ __forceinline__ void stage_q(const StageArgs &a, int kvh, int blk) {
         }
         __syncthreads();
     }
-    constexpr int TB = TASKS > 4 ? 4 : TASKS;       // tasks whose loads are in flight together
-    static_assert(TASKS % TB == 0, "whole task batches");
 #pragma unroll
     for (int t0 = 0; t0 < TASKS; t0 += TB) {
-    v4f xl[TB], xu[TB], cs[TB], sn[TB];
-#pragma unroll
-    for (int t = 0; t < TB; t++) {
-        const int k = tid + kThreads * (t0 + t);
-        const int r = k / CPR, c = k % CPR;
-        const int nt = r >> 4;
-        const int qi = i0 + (nt % S::QT) * 16 + (r & 15);
-        xl[t] = xu[t] = cs[t] = sn[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-        if (qi < a.n) {
-            const float *head = a.q + ((size_t)qi * a.n_q_heads + (size_t)kvh * G + nt / S::QT) * HD;
-            xl[t] = *reinterpret_cast<const v4f *>(head + 4 * c);
-            xu[t] = *reinterpret_cast<const v4f *>(head + HALF + 4 * c);
-            if (a.cos_t) {
-                cs[t] = *reinterpret_cast<const v4f *>(a.cos_t + (size_t)qi * HALF + 4 * c);
-                sn[t] = *reinterpret_cast<const v4f *>(a.sin_t + (size_t)qi * HALF + 4 * c);
-            }
-        }
-    }
+    if (t0 > 0) load_batch(t0);
     if (a.q_norm) {
 #pragma unroll
         for (int t = 0; t < TB; t++) {
             const int k = tid + kThreads * (t0 + t);
-            const int r = k / CPR, c = k % CPR;
-            const float inv = inv_s[r];
-            xl[t] = norm4(xl[t], inv, *reinterpret_cast<const v4f *>(a.q_norm + 4 * c));
-            xu[t] = norm4(xu[t], inv, *reinterpret_cast<const v4f *>(a.q_norm + HALF + 4 * c));
+            const float inv = inv_s[k / CPR];
+            xl[t] = norm4(xl[t], inv, wlo);
+            xu[t] = norm4(xu[t], inv, whi);
         }
     }
 #pragma unroll
@@ -369,17 +379,9 @@ __global__ __launch_bounds__(kThreads) void prefill_stage_kernel(StageArgs a) {
     // partner x[HD/2+4c..+3]; the 8 lanes of a 32-value block share their row,
     // so a whole block is computed or skipped together.
     const bool has_new = a.k_new && t0 + kKT > a.pos0 && t0 < a.kend;
-    // with k_norm: 1/rms of each new K row of the tile, one row per thread
+    // with k_norm: 1/rms of each new K row of the tile, one row per thread;
+    // the tasks' own loads below are issued first, so the two overlap
     __shared__ float kinv_s[kKT];
-    if (has_new && a.k_norm) {
-        if (tid < kKT) {
-            const int p = t0 + tid;
-            kinv_s[tid] = fresh(p, page[tid / kPage])
-                              ? row_inv_rms<HD>(a.k_new + ((size_t)(p - a.pos0) * v.n_kv_heads + kvh) * HD, a.rms_eps)
-                              : 0.0f;
-        }
-        __syncthreads();
-    }
     if (has_new) {
         constexpr int HALF = HD / 2;
         constexpr int CPR = HD / 8;
@@ -400,13 +402,32 @@ __global__ __launch_bounds__(kThreads) void prefill_stage_kernel(StageArgs a) {
                 const float *src = (kv ? a.v_new : a.k_new) + (row * v.n_kv_heads + kvh) * HD;
                 xl[t] = *reinterpret_cast<const v4f *>(src + 4 * c);
                 xu[t] = *reinterpret_cast<const v4f *>(src + HALF + 4 * c);
-                if (!kv && a.k_norm) {
-                    xl[t] = norm4(xl[t], kinv_s[r], *reinterpret_cast<const v4f *>(a.k_norm + 4 * c));
-                    xu[t] = norm4(xu[t], kinv_s[r], *reinterpret_cast<const v4f *>(a.k_norm + HALF + 4 * c));
-                }
                 if (!kv && rot) {
                     cs[t] = *reinterpret_cast<const v4f *>(a.cos_t + row * HALF + 4 * c);
                     sn[t] = *reinterpret_cast<const v4f *>(a.sin_t + row * HALF + 4 * c);
+                }
+            }
+        }
+        if (a.k_norm) {
+            // every task of a thread has the same columns: its weights once
+            const int cw = tid % CPR;
+            const v4f wlo = *reinterpret_cast<const v4f *>(a.k_norm + 4 * cw);
+            const v4f whi = *reinterpret_cast<const v4f *>(a.k_norm + HALF + 4 * cw);
+            if (tid < kKT) {
+                const int p = t0 + tid;
+                kinv_s[tid] = fresh(p, page[tid / kPage])
+                                  ? row_inv_rms<HD>(a.k_new + ((size_t)(p - a.pos0) * v.n_kv_heads + kvh) * HD,
+                                                    a.rms_eps)
+                                  : 0.0f;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < TPT; t++) {
+                const int task = tid + kThreads * t;
+                const int r = task / (2 * CPR), kv = (task / CPR) & 1;
+                if (mine[t] && !kv) {
+                    xl[t] = norm4(xl[t], kinv_s[r], wlo);
+                    xu[t] = norm4(xu[t], kinv_s[r], whi);
                 }
             }
         }
