@@ -527,13 +527,25 @@ def decode_curve(args, nat, hip):
     return points
 
 
+def bench_lib():
+    """libtqbench.so (tailorquantkernel_amd/bench/tq_bench.h): the measurement
+    kernels that are not part of the attention library."""
+    lib = C.CDLL(os.path.join(ROOT, "tailorquantkernel_amd", "libtqbench.so"))
+    vp, i, sz = C.c_void_p, C.c_int, C.c_size_t
+    for name, res, argt in (("tq_hip_floor_scratch_bytes", sz, [i, i]), ("tq_hip_floor_out_bytes", sz, [i, i]),
+                            ("tq_hip_floor_step", i, [vp, sz, i, i, i, vp, vp, vp])):
+        f = getattr(lib, name)
+        f.restype, f.argtypes = res, argt
+    return lib
+
+
 def step_floor(nat, hip, stream, bufs, nbytes, n_heads, reps, n_splits=32):
     """The floor of this step's shape on this GPU, measured the same way (a
     HIP graph of one launch per layer buffer, the same buffers): the launch
     alone, the read of the layer's KV bytes by n_heads x n_splits work-groups,
     and that read plus the split-K combine chain with no attention math
     (tq_hip_floor_step)."""
-    lib = nat.load()
+    lib = bench_lib()
     scratch = nat.DeviceBuffer(lib.tq_hip_floor_scratch_bytes(n_heads, n_splits))
     zeros = np.zeros(n_heads * 64, np.int32)   # held until the copy has read it
     nat.check(lib.tq_hip_memcpy_h2d(scratch.ptr, zeros.ctypes.data, zeros.nbytes, None), "zero counters")
@@ -575,6 +587,9 @@ def bench_decode_8b(args, nat, hip):
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": r["steps"],
+        "steps_requested": args.steps,
+        "steps_note": (f"at least {MIN_TIMED} launches are timed whatever --steps asks (whole replays of the "
+                       f"{layers}-launch graph): steps is the count timed, steps_requested the count asked"),
         "warmup": args.warmup,
         "ms_per_step": ms,
         "higher_is_better": True,

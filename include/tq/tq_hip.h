@@ -6,9 +6,24 @@
  *
  * Two kinds of entry point:
  *   - synchronous ones take HOST buffers, copy them in, run, copy results out
- *     and return with the results valid (the boundary of attention_layer);
+ *     and return with the results valid (the boundary of attention_layer).
+ *     A call that waits on completion flags returns as soon as its outputs are
+ *     visible in host memory, which may be before the cache's stream has
+ *     drained (the kernel's last waves may still be retiring); work enqueued
+ *     next on that stream is still ordered after it.  The host thread spins
+ *     (with a pause hint, not a yield) while it waits;
  *   - *_async ones take DEVICE buffers and a stream (hipStream_t as void*,
  *     NULL = the cache's own stream) and only enqueue work.
+ *
+ * Environment variables named TQ_HIP_* are for tests and plan sweeps only:
+ * each forces one launch plan or code path for A/B comparisons, and
+ * production callers leave them unset.  Results stay within the documented
+ * tolerances under every setting.  Decode: TQ_HIP_DECODE_WG_TARGET,
+ * TQ_HIP_DECODE_MAX_SPLITS, TQ_HIP_DECODE_SPLIT_CAP, TQ_HIP_DECODE_WAVES,
+ * TQ_HIP_DECODE_KERNEL; prefill: TQ_HIP_PREFILL_DENSE, TQ_HIP_PREFILL_ROWS,
+ * TQ_HIP_PREFILL_FUSED_NORM, TQ_HIP_PREFILL_QUANT_OUT; weight matmuls:
+ * TQ_HIP_GEMV_RW, TQ_HIP_GEMV_GC, TQ_HIP_GEMM_MIN_TOKENS, TQ_HIP_GEMM_SPLIT,
+ * TQ_HIP_GEMM_XS, TQ_HIP_MLP_FUSED.
  *
  * KV storage is an HBM-resident paged cache.  A page holds TQ_HIP_PAGE_TOKENS
  * consecutive positions of one sequence for every kv head, K then V:
@@ -408,21 +423,6 @@ int tq_hip_attention_layer_batch_async(tq_hip_kv *kv, const tq_hip_attn_weights 
  * equals `never`.  Asynchronous on `stream`; the caller times it. */
 size_t tq_hip_membw_sink_bytes(void);
 int tq_hip_membw_read(const void *buf, size_t bytes, void *sink, unsigned int never, void *stream);
-
-/* Measurement helper, no counterpart in the reference: the floor of one
- * split-K decode step on this GPU.  n_heads * n_splits work-groups of 256
- * threads; work-group w reads its 1/(n_heads*n_splits) chunk of buf (bytes,
- * a multiple of 16) with every 16-byte load in flight.  mode 0: the launch
- * alone; 1: the read; 2: the read, then the decode's combine chain with no
- * math — a 520-float partial row stored agent-coherent, an arrival counter per
- * head, and the head's last work-group pulling its n_splits rows and writing
- * their sum to out[head][520].  scratch: tq_hip_floor_scratch_bytes bytes,
- * 256-byte aligned, its first n_heads*256 bytes (the counters) zeroed once;
- * out: tq_hip_floor_out_bytes bytes, 16-byte aligned. */
-size_t tq_hip_floor_scratch_bytes(int n_heads, int n_splits);
-size_t tq_hip_floor_out_bytes(int n_heads, int n_splits);
-int tq_hip_floor_step(const void *buf, size_t bytes, int n_heads, int n_splits, int mode, void *scratch,
-                      void *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -71,9 +71,6 @@ _PROTOS = {
     "tq_hip_prefill_async": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tq_hip_membw_sink_bytes": (_sz, []),
     "tq_hip_membw_read": (_i, [_vp, _sz, _vp, C.c_uint, _vp]),
-    "tq_hip_floor_scratch_bytes": (_sz, [_i, _i]),
-    "tq_hip_floor_out_bytes": (_sz, [_i, _i]),
-    "tq_hip_floor_step": (_i, [_vp, _sz, _i, _i, _i, _vp, _vp, _vp]),
     "tq_hip_decode_step_noalloc": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tq_hip_decode_step_norm_async": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp,
                                           _vp, _vp]),

@@ -96,3 +96,23 @@ def test_missing_library_fails_loudly(tmp_path):
             native.load(str(tmp_path / "libtqhip.so"))
     finally:
         native._lib = saved
+
+
+def test_bench_library_exports_its_header():
+    """libtqbench.so (bench.py's step floor, not part of the attention
+    library) exports what tailorquantkernel_amd/bench/tq_bench.h declares, and
+    the attention library exports none of it."""
+    text = open(os.path.join(ROOT, "tailorquantkernel_amd", "bench", "tq_bench.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = set(re.findall(r"\b(tq_hip_\w*)\s*\(", text))
+    assert names == {"tq_hip_floor_scratch_bytes", "tq_hip_floor_out_bytes", "tq_hip_floor_step"}
+    bench = C.CDLL(os.path.join(ROOT, "tailorquantkernel_amd", "libtqbench.so"))
+    from tailorquantkernel_amd import native
+    attn = native.load()
+    for n in names:
+        assert hasattr(bench, n), n
+        assert not hasattr(attn, n), f"{n} still exported by libtqhip.so"
+    f = bench.tq_hip_floor_step
+    f.restype = C.c_int
+    f.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    assert f(None, 1 << 20, 8, 32, 2, None, None, None) == native.EINVAL
