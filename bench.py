@@ -783,7 +783,8 @@ def bench_prefill_2k(args, nat, hip):
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": tflops / 2500.0, "executed_tflops": 2 * tflops,
                      "traffic": measured_traffic("prefill_8b_2048_pmc.txt"),
-                     "kernel": "append_kernel + prefill_stage_kernel<128> + prefill_kernel<128, 4, 2> (one step)",
+                     "kernel": ("prefill_stage_kernel<128, 4, 2> (fused append) + prefill_block_kernel<128, 4, 2> "
+                                "(one step)"),
                      "kernel_ms": ms},
     }
     host = {"nq": nq, "nkv": nkv, "hd": hd, "n": n, "theta": theta, "q": q, "k": k, "v": v, "gpu_out": first}

@@ -21,7 +21,7 @@
  * tolerances under every setting.  Decode: TQ_HIP_DECODE_WG_TARGET,
  * TQ_HIP_DECODE_MAX_SPLITS, TQ_HIP_DECODE_SPLIT_CAP, TQ_HIP_DECODE_WAVES,
  * TQ_HIP_DECODE_KERNEL; prefill: TQ_HIP_PREFILL_DENSE, TQ_HIP_PREFILL_ROWS,
- * TQ_HIP_PREFILL_FUSED_NORM, TQ_HIP_PREFILL_QUANT_OUT; weight matmuls:
+ * TQ_HIP_PREFILL_WHOLE, TQ_HIP_PREFILL_FUSED_NORM, TQ_HIP_PREFILL_QUANT_OUT; weight matmuls:
  * TQ_HIP_GEMV_RW, TQ_HIP_GEMV_GC, TQ_HIP_GEMM_MIN_TOKENS, TQ_HIP_GEMM_SPLIT,
  * TQ_HIP_GEMM_XS, TQ_HIP_MLP_FUSED.
  *

@@ -21,7 +21,7 @@
 //   fp32 and split into bf16 hi + lo (hi + lo = x to 2^-18 relative).  Every
 //   query block then streams these images instead of re-deriving them.
 //
-// prefill_kernel — work-group of 256 threads (4 waves), one kv head, 64*NJ
+// The attention — per 4 waves, one kv head, 64*NJ
 //   (query, head) rows = QB = 64*NJ/G consecutive query tokens x the G heads
 //   of the group, in row tiles of 16 queries of one head; wave w owns NJ row
 //   tiles.  The block's staged q codes go to registers as bf16 (exact), its
@@ -43,18 +43,25 @@
 //   B operand of the P.V product (keys permuted identically in A and B), so P
 //   never goes through LDS.
 //
-// Balance: under the causal mask the last query block reads every key tile
-// and the first reads one.  Query blocks are paired last with first (p with
-// nb-1-p), so every pair reads about the same number of tiles; a pair's tile
-// sequence (the later block's tiles, then the earlier block's) is cut into nsp
-// equal chunks, one work item each, so all items carry the same work.  An item
-// runs one or two segments (a block and a tile range).  A block covered by
-// several segments is merged by the segment that finishes last, picked by an
-// arrival counter: every other segment writes its partial (o, m, l per row)
-// with agent-coherent 16-byte stores and counts itself on a second counter,
-// which the last one waits on; it merges the partials and its own registers
-// in segment order, so the result does not depend on which work-group
-// finished last.
+// Balance: under the causal mask query block b reads b + 1 key tiles.  Two
+// attention kernels share the per-tile code:
+//
+// prefill_block_kernel — with at least two query blocks per CU (the 2048-
+//   token prefill: 64 blocks x 8 kv heads), one work-group of 8 waves per
+//   (query block, kv head), dealt longest block first, so the CUs pair long
+//   blocks with short ones by themselves.  Its two 4-wave halves cover the
+//   same 128 rows and split the block's key tiles (half h: tiles h, h+2, ...);
+//   half 1 leaves its (o, m, l) in LDS and half 0 merges the two in half
+//   order.  Nothing leaves the work-group but the output rows.
+// prefill_kernel — with fewer blocks, query blocks are paired last with first
+//   (p with nb-1-p), so every pair reads about the same number of tiles, and a
+//   pair's tile sequence (the later block's tiles, then the earlier block's)
+//   is cut into nsp equal chunks, one 4-wave work-group each.  A block covered
+//   by several segments: every segment writes its partial (o, m, l per row)
+//   with agent-coherent 16-byte stores, waits for them and arrives on a
+//   counter; the last to arrive merges the partials and its own registers in
+//   segment order, so the result does not depend on which finished last.  No
+//   work-group waits on another.
 //
 // Grid: one dimension, work-group w serves kv head w % n_kv, so with 8 kv
 // heads each XCD (work-groups go round-robin over the 8 XCDs) works on one
@@ -531,14 +538,311 @@ __host__ __device__ inline int block_tiles(int pos0, int n, int qb, int b) {
     return (pos0 + last + kKT - 1) / kKT;
 }
 
+// Per-row state of one wave's NJ row tiles over a run of key tiles: o and
+// lsum are taken against moff (mrow, or 0 before any key); mrow is the running
+// max; thr the largest score - moff a tile may hold without moving the max
+// (kLazy; -inf before any key, so the first visible key takes the slow path);
+// lsum is this lane's share of the row sum, added over the row's lanes at the
+// end.  The same in the row's four lanes.
+template <int HD, int G, int NJ>
+struct PRows {
+    static constexpr int MT = PShape<HD, G, NJ>::MT;
+    v4f o[MT][NJ];
+    float mrow[NJ], moff[NJ], thr[NJ], lsum[NJ];
+    __device__ __forceinline__ void init() {
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++) o[m][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            mrow[j] = -INFINITY;
+            moff[j] = 0.0f;
+            thr[j] = -INFINITY;
+            lsum[j] = 0.0f;
+        }
+    }
+};
+
+// The score product's B operands of one wave's rows: the q codes of query
+// l16, values 32b + 8lg .. +7, as bf16 (exact), qd * scale * log2(e) per
+// block, and each row's query position.
+template <int HD, int G, int NJ>
+struct PQ {
+    static constexpr int NB = PShape<HD, G, NJ>::NB;
+    v8bf qcb[NJ][NB];
+    float qsc[NJ][NB];
+    int qpos[NJ];
+};
+
+// From the block's staged q image in LDS (codes at qc, scales after them).
+template <int HD, int G, int NJ>
+__device__ __forceinline__ void load_q(const PrefillArgs &a, const unsigned char *qc, int i0, int wave, int lane,
+                                       PQ<HD, G, NJ> &q) {
+    using S = PShape<HD, G, NJ>;
+    constexpr int NB = S::NB;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const float *qd = reinterpret_cast<const float *>(qc + S::RW * S::QCS);
+    const float qscale = a.scale * kLog2e;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int r = (wave * NJ + j) * 16 + l16;
+        const int nt = r >> 4;
+        int qi = i0 + (nt % S::QT) * 16 + l16;
+        qi = qi < a.n ? qi : a.n - 1;
+        q.qpos[j] = a.pos0 + qi;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            q.qsc[j][b] = qd[r * NB + b] * qscale;
+            const unsigned char *c = qc + r * S::QCS + b * kQK + 8 * lg;
+            u32x4 w;
+#pragma unroll
+            for (int i = 0; i < 4; i++) w[i] = bf16_pair((float)(int8_t)c[2 * i], (float)(int8_t)c[2 * i + 1]);
+            q.qcb[j][b] = as_v8bf(w);
+        }
+    }
+}
+
+// The P operands of one tile: P = exp2(S - moff) split into bf16 hi | lo.
+template <int NJ>
+struct PP {
+    u32x4 hi[NJ], lo[NJ];
+};
+
+// One key tile kt (image T in LDS) against the wave's rows, first part:
+// exact scores, the causal mask, the online softmax (o and lsum rescaled when
+// the max moves) and this tile's P.
+template <int HD, int G, int NJ>
+__device__ __forceinline__ void tile_scores(const PrefillArgs &a, const unsigned char *T, int kt, int i0, int lane,
+                                            const PQ<HD, G, NJ> &q, PRows<HD, G, NJ> &st, PP<NJ> &pp) {
+    using S = PShape<HD, G, NJ>;
+    using I = TileImg<HD>;
+    constexpr int NB = S::NB;
+    const int lg = lane >> 4;
+    // S^T - moff for keys [32kt, 32kt+32) x the wave's queries: per block the
+    // exact int32 dot on the matrix cores, then (kd * qd') * dot added in
+    // block order onto -moff
+    v4f s[2][NJ];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+            const v8bf kc = as_v8bf(*reinterpret_cast<const u32x4 *>(T + I::KC_OFF + ((mt * NB + b) * 64 + lane) * 16));
+            const v4f kd = *reinterpret_cast<const v4f *>(T + I::KD_OFF + ((mt * NB + b) * 4 + lg) * 16);
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const v4f d =
+                    __builtin_amdgcn_mfma_f32_16x16x32_bf16(kc, q.qcb[j][b], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    s[mt][j][r] = __builtin_fmaf(d[r], kd[r] * q.qsc[j][b], b == 0 ? -st.moff[j] : s[mt][j][r]);
+            }
+        }
+    }
+
+    // fast path: no row's tile max passes its threshold, and the tile needs
+    // no causal mask (it ends at or before the block's first query); the lane
+    // maxima are taken here, in the block that computes the scores
+    auto max8 = [](const v4f &x, const v4f &y) {
+        return fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])));
+    };
+    const int k0 = kt * kKT;
+    const bool diag = k0 + kKT - 1 > a.pos0 + i0;
+    bool move = false;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) move |= max8(s[0][j], s[1][j]) > st.thr[j];
+    if (diag || __builtin_amdgcn_ballot_w64(move) != 0) {
+        // slow path, for the whole wave: the causal mask, the row max over the
+        // four lanes, the lazy move (only by more than kLazy), o and lsum
+        // rescaled and the tile re-offset
+        if (diag) {
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int kp = k0 + mt * 16 + 4 * lg + r;
+                        s[mt][j][r] = kp > q.qpos[j] ? -INFINITY : s[mt][j][r];
+                    }
+        }
+        bool rescale = false;
+        float corr[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const float mx = xrow_max(max8(s[0][j], s[1][j])) + st.moff[j];
+            const float mnew = mx > st.mrow[j] + kLazy ? mx : st.mrow[j];
+            const float onew = mnew == -INFINITY ? 0.0f : mnew;
+            // nothing is accumulated while mrow is -inf: corr 0, not exp2 of a difference
+            corr[j] = st.mrow[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st.moff[j] - onew);
+            const float delta = st.moff[j] - onew;
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) s[mt][j][r] += delta;
+            rescale |= corr[j] != 1.0f;
+            st.lsum[j] *= corr[j];
+            st.mrow[j] = mnew;
+            st.moff[j] = onew;
+            st.thr[j] = mnew == -INFINITY ? -INFINITY : kLazy;
+        }
+        if (__builtin_amdgcn_ballot_w64(rescale) != 0) {
+#pragma unroll
+            for (int m = 0; m < S::MT; m++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) st.o[m][j] *= corr[j];
+        }
+    }
+    // P = exp2(S - moff) <= 2^kLazy, split into bf16 hi | lo (B operands)
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        float p[8];
+        float ps = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                p[mt * 4 + r] = __builtin_amdgcn_exp2f(s[mt][j][r]);
+                ps += p[mt * 4 + r];
+            }
+        st.lsum[j] += ps;
+        split_bf16(p, pp.hi[j], pp.lo[j]);
+    }
+}
+
+// Second part: O^T += V'^T . P^T with the tile's V' (image T) and its P.
+template <int HD, int G, int NJ>
+__device__ __forceinline__ void tile_pv(const unsigned char *T, int lane, const PP<NJ> &pp, PRows<HD, G, NJ> &st) {
+    using S = PShape<HD, G, NJ>;
+    using I = TileImg<HD>;
+#pragma unroll
+    for (int m = 0; m < S::MT; m++) {
+        const v8bf ahi = as_v8bf(*reinterpret_cast<const u32x4 *>(T + I::VH_OFF + (m * 64 + lane) * 16));
+        const v8bf alo = as_v8bf(*reinterpret_cast<const u32x4 *>(T + I::VL_OFF + (m * 64 + lane) * 16));
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            st.o[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, as_v8bf(pp.hi[j]), st.o[m][j], 0, 0, 0);
+            st.o[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, as_v8bf(pp.lo[j]), st.o[m][j], 0, 0, 0);
+            st.o[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, as_v8bf(pp.hi[j]), st.o[m][j], 0, 0, 0);
+        }
+    }
+}
+
+// Both parts of one tile.
+template <int HD, int G, int NJ>
+__device__ __forceinline__ void tile_update(const PrefillArgs &a, const unsigned char *T, int kt, int i0, int lane,
+                                            const PQ<HD, G, NJ> &q, PRows<HD, G, NJ> &st) {
+    PP<NJ> pp;
+    tile_scores<HD, G, NJ>(a, T, kt, i0, lane, q, st, pp);
+    tile_pv<HD, G, NJ>(T, lane, pp, st);
+}
+
+// Normalise and store the wave's rows: lane holds columns 16m + 4lg .. +3 of
+// query l16.  Either fp32 rows into out, or (out_xs) each row quantized as
+// quantize_row_q8 straight into the split layout the output GEMM reads.
+template <int HD, int G, int NJ>
+__device__ __forceinline__ void store_rows(const PrefillArgs &a, int kvh, int i0, int wave, int lane,
+                                           const PRows<HD, G, NJ> &st, const float (&lrow)[NJ]) {
+    using S = PShape<HD, G, NJ>;
+    const int l16 = lane & 15, lg = lane >> 4;
+    if (a.out_xs) {
+        // block b of a head is columns 32b..32b+31, tiles m = 2b (codes 0-15)
+        // and 2b+1 (codes 16-31), 8 values in each of the 4 lanes of the
+        // query (lanes l16 + 16 lg); the absmax as quantize8x4 takes it (|x|,
+        // NaN and -0 as 0, an exact max), then the same scale, inverse and
+        // codes as a separate quantize launch over the stored rows
+        const size_t nrows = (size_t)a.n, cols = (size_t)a.n_q_heads * HD;
+        float *xd = reinterpret_cast<float *>(a.out_xs + nrows * cols);
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const float inv = 1.0f / lrow[j];
+            const int nt = wave * NJ + j;
+            const int g = nt / S::QT;
+            const int qi = i0 + (nt % S::QT) * 16 + l16;
+#pragma unroll
+            for (int b = 0; b < HD / kQK; b++) {
+                const v4f x0 = st.o[2 * b][j] * inv, x1 = st.o[2 * b + 1][j] * inv;
+                float m = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float a0 = x0[i] < 0.0f ? -x0[i] : x0[i];
+                    const float a1 = x1[i] < 0.0f ? -x1[i] : x1[i];
+                    m = fmaxf(m, a0 > 0.0f ? a0 : 0.0f);
+                    m = fmaxf(m, a1 > 0.0f ? a1 : 0.0f);
+                }
+                m = fmaxf(m, __shfl_xor(m, 16));
+                m = fmaxf(m, __shfl_xor(m, 32));
+                const float d = quant_scale(m);
+                const float qinv = quant_inverse(d);
+                uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    w0 |= quant_code(x0[i], qinv) << (8 * i);
+                    w1 |= quant_code(x1[i], qinv) << (8 * i);
+                }
+                if (qi < a.n) {
+                    const size_t gb = (size_t)(kvh * G + g) * (HD / kQK) + b;
+                    *reinterpret_cast<uint32_t *>(a.out_xs + ((2 * gb) * nrows + qi) * 16 + 4 * lg) = w0;
+                    *reinterpret_cast<uint32_t *>(a.out_xs + ((2 * gb + 1) * nrows + qi) * 16 + 4 * lg) = w1;
+                    if (lg == 0) xd[gb * nrows + qi] = d;
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const float inv = 1.0f / lrow[j];
+        const int nt = wave * NJ + j;
+        const int g = nt / S::QT;
+        const int qi = i0 + (nt % S::QT) * 16 + l16;
+        if (qi < a.n) {
+            float *orow = a.out + ((size_t)qi * a.n_q_heads + (size_t)kvh * G + g) * HD;
+#pragma unroll
+            for (int m = 0; m < S::MT; m++) *reinterpret_cast<v4f *>(orow + m * 16 + 4 * lg) = st.o[m][j] * inv;
+        }
+    }
+}
+
+// Merge the partial (ms, ls, os) into the running (M, L, acc), in order.
+template <int MT>
+__device__ __forceinline__ void merge_part(float &M, float &L, v4f (&acc)[MT], float ms, float ls, const v4f (&os)[MT]) {
+    const float Mn = fmaxf(M, ms);
+    const float fo = __builtin_amdgcn_exp2f(M - Mn);   // 0 while M is -inf
+    const float fs = __builtin_amdgcn_exp2f(ms - Mn);  // 0 for a partial with no key
+#pragma unroll
+    for (int m = 0; m < MT; m++) acc[m] = acc[m] * fo + os[m] * fs;
+    L = L * fo + ls * fs;
+    M = Mn;
+}
+
+// Copy of key tile kt of img into an LDS buffer by the 256 threads of one
+// 4-wave group (thread t's copy r is chunk t + 256 r; the partial last round:
+// the first REM threads, whole waves).
+template <int HD>
+__device__ __forceinline__ void fetch_tile(const unsigned char *img, int kt, unsigned char *buf, int gtid, int gwave) {
+    using I = TileImg<HD>;
+    const unsigned char *src = img + (size_t)kt * I::BYTES;
+    const int wu = __builtin_amdgcn_readfirstlane(gwave);
+#pragma unroll
+    for (int r = 0; r < I::ROUNDS; r++) dma16(src + 16 * (gtid + kThreads * r), buf + 16 * (kThreads * r + 64 * wu));
+    if (I::REM > 0 && 64 * wu < I::REM)
+        dma16(src + 16 * (gtid + kThreads * I::ROUNDS), buf + 16 * (kThreads * I::ROUNDS + 64 * wu));
+}
+// Copies of one tile a wave of the group issues.
+template <int HD>
+__device__ __forceinline__ bool tile_has_rem(int gwave) {
+    using I = TileImg<HD>;
+    return I::REM > 0 && 64 * gwave < I::REM;
+}
+
 // One segment: query block blk against key tiles [kt_begin, kt_end), the
-// segment sp of the nsp that cover the block.
+// segment sp of the nsp that cover the block (4-wave work-group).
 template <int HD, int G, int NJ>
 __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, int blk, int kt_begin, int kt_end,
                                                 int sp, int nsp, unsigned char *tile0, unsigned char *tile1) {
     using S = PShape<HD, G, NJ>;
     using I = TileImg<HD>;
-    constexpr int NB = S::NB;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -547,22 +851,9 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
     const int i0 = blk * S::QB;
     const unsigned char *img = a.img + (size_t)kvh * a.n_tiles * I::BYTES;
 
-    // copy of tile kt into an LDS buffer: thread t's copy r is chunk t + 256 r
-    // (the partial last round: the first REM threads, whole waves)
-    auto fetch = [&](unsigned char *buf, int kt) {
-        const unsigned char *src = img + (size_t)kt * I::BYTES;
-        const int wu = __builtin_amdgcn_readfirstlane(wave);
-#pragma unroll
-        for (int r = 0; r < I::ROUNDS; r++)
-            dma16(src + 16 * (tid + kThreads * r), buf + 16 * (kThreads * r + 64 * wu));
-        if (I::REM > 0 && 64 * wu < I::REM)
-            dma16(src + 16 * (tid + kThreads * I::ROUNDS), buf + 16 * (kThreads * I::ROUNDS + 64 * wu));
-    };
     // ---- the block's staged q rows (prefill_stage_kernel) into tile1, then
     //      the first key tile into tile0; waiting for all but this wave's
     //      copies of the tile leaves only the tile in flight
-    unsigned char *qc = tile1;
-    float *qd = reinterpret_cast<float *>(tile1 + S::RW * S::QCS);
     {
         constexpr int QCH = S::Q_BYTES / 16;
         const unsigned char *src = a.qimg + ((size_t)kvh * a.qblocks + blk) * S::Q_BYTES;
@@ -570,56 +861,19 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
         for (int c0 = 64 * wu; c0 < QCH; c0 += kThreads)
             if (c0 + lane < QCH) dma16(src + 16 * (c0 + lane), tile1 + 16 * c0);
     }
-    fetch(tile0, kt_begin);
-    if (I::REM > 0 && 64 * wave < I::REM)
+    fetch_tile<HD>(img, kt_begin, tile0, tid, wave);
+    if (tile_has_rem<HD>(wave))
         wait_vm<I::ROUNDS + 1>();
     else
         wait_vm<I::ROUNDS>();
     __syncthreads();
 
-    // ---- per-lane B operands: the q codes of query l16, values 32b + 8lg ..
-    //      +7, as bf16 (exact), and qd * scale * log2(e) per block
-    v8bf qcb[NJ][NB];
-    float qsc[NJ][NB];
-    int qpos[NJ];
-    const float qscale = a.scale * kLog2e;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int r = (wave * NJ + j) * 16 + l16;
-        const int nt = r >> 4;
-        int qi = i0 + (nt % S::QT) * 16 + l16;
-        qi = qi < a.n ? qi : a.n - 1;
-        qpos[j] = a.pos0 + qi;
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-            qsc[j][b] = qd[r * NB + b] * qscale;
-            const unsigned char *c = qc + r * S::QCS + b * kQK + 8 * lg;
-            u32x4 w;
-#pragma unroll
-            for (int i = 0; i < 4; i++) w[i] = bf16_pair((float)(int8_t)c[2 * i], (float)(int8_t)c[2 * i + 1]);
-            qcb[j][b] = as_v8bf(w);
-        }
-    }
+    PQ<HD, G, NJ> q;
+    load_q<HD, G, NJ>(a, tile1, i0, wave, lane, q);
+    PRows<HD, G, NJ> st;
+    st.init();
 
-    // ---- the key loop
-    v4f o[S::MT][NJ];
-#pragma unroll
-    for (int m = 0; m < S::MT; m++)
-#pragma unroll
-        for (int j = 0; j < NJ; j++) o[m][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    // per row (the same in the row's four lanes): mrow the running max, moff
-    // the offset o and lsum are taken against (mrow, or 0 before any key),
-    // thr the largest score - moff a tile may hold without moving the max
-    // (kLazy; -inf before any key, so the first visible key takes the slow path)
-    float mrow[NJ], moff[NJ], thr[NJ], lsum[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        mrow[j] = -INFINITY;
-        moff[j] = 0.0f;
-        thr[j] = -INFINITY;
-        lsum[j] = 0.0f;
-    }
-
+    // ---- the key loop: two LDS buffers, one tile ahead, one barrier per tile
     for (int kt = kt_begin; kt < kt_end; kt++) {
         const bool odd = (kt - kt_begin) & 1;
         unsigned char *T = odd ? tile1 : tile0;
@@ -628,228 +882,49 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
         // staging) for the next copy
         asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
         __syncthreads();
-        if (kt + 1 < kt_end) fetch(odd ? tile0 : tile1, kt + 1);
-
-        // S^T - moff for keys [32kt, 32kt+32) x the wave's queries: per block
-        // the exact int32 dot on the matrix cores, then (kd * qd') * dot added
-        // in block order onto -moff
-        v4f s[2][NJ];
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                const v8bf kc = as_v8bf(*reinterpret_cast<const u32x4 *>(T + I::KC_OFF + ((mt * NB + b) * 64 + lane) * 16));
-                const v4f kd = *reinterpret_cast<const v4f *>(T + I::KD_OFF + ((mt * NB + b) * 4 + lg) * 16);
-#pragma unroll
-                for (int j = 0; j < NJ; j++) {
-                    const v4f d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kc, qcb[j][b], v4f{0.0f, 0.0f, 0.0f, 0.0f},
-                                                                          0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        s[mt][j][r] = __builtin_fmaf(d[r], kd[r] * qsc[j][b], b == 0 ? -moff[j] : s[mt][j][r]);
-                }
-            }
-        }
-
-        // fast path: no row's tile max passes its threshold, and the tile needs
-        // no causal mask (it ends at or before the block's first query); the
-        // lane maxima are taken here, in the block that computes the scores
-        auto max8 = [](const v4f &x, const v4f &y) {
-            return fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])));
-        };
-        const int k0 = kt * kKT;
-        const bool diag = k0 + kKT - 1 > a.pos0 + i0;
-        bool move = false;
-#pragma unroll
-        for (int j = 0; j < NJ; j++) move |= max8(s[0][j], s[1][j]) > thr[j];
-        if (diag || __builtin_amdgcn_ballot_w64(move) != 0) {
-            // slow path, for the whole wave: the causal mask, the row max over
-            // the four lanes, the lazy move (only by more than kLazy), o and
-            // lsum rescaled and the tile re-offset
-            if (diag) {
-#pragma unroll
-                for (int j = 0; j < NJ; j++)
-#pragma unroll
-                    for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            const int kp = k0 + mt * 16 + 4 * lg + r;
-                            s[mt][j][r] = kp > qpos[j] ? -INFINITY : s[mt][j][r];
-                        }
-            }
-            bool rescale = false;
-            float corr[NJ];
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                const float mx = xrow_max(max8(s[0][j], s[1][j])) + moff[j];
-                const float mnew = mx > mrow[j] + kLazy ? mx : mrow[j];
-                const float onew = mnew == -INFINITY ? 0.0f : mnew;
-                // nothing is accumulated while mrow is -inf: corr 0, not exp2 of a difference
-                corr[j] = mrow[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(moff[j] - onew);
-                const float delta = moff[j] - onew;
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) s[mt][j][r] += delta;
-                rescale |= corr[j] != 1.0f;
-                lsum[j] *= corr[j];
-                mrow[j] = mnew;
-                moff[j] = onew;
-                thr[j] = mnew == -INFINITY ? -INFINITY : kLazy;
-            }
-            if (__builtin_amdgcn_ballot_w64(rescale) != 0) {
-#pragma unroll
-                for (int m = 0; m < S::MT; m++)
-#pragma unroll
-                    for (int j = 0; j < NJ; j++) o[m][j] *= corr[j];
-            }
-        }
-        // P = exp2(S - moff) <= 2^kLazy, split into bf16 hi | lo (B operands)
-        u32x4 phi[NJ], plo[NJ];
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            float p[8];
-            float ps = 0.0f;
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    p[mt * 4 + r] = __builtin_amdgcn_exp2f(s[mt][j][r]);
-                    ps += p[mt * 4 + r];
-                }
-            lsum[j] += ps;
-            split_bf16(p, phi[j], plo[j]);
-        }
-
-        // O^T += V'^T . P^T
-#pragma unroll
-        for (int m = 0; m < S::MT; m++) {
-            const v8bf ahi = as_v8bf(*reinterpret_cast<const u32x4 *>(T + I::VH_OFF + (m * 64 + lane) * 16));
-            const v8bf alo = as_v8bf(*reinterpret_cast<const u32x4 *>(T + I::VL_OFF + (m * 64 + lane) * 16));
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                o[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, as_v8bf(phi[j]), o[m][j], 0, 0, 0);
-                o[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi, as_v8bf(plo[j]), o[m][j], 0, 0, 0);
-                o[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, as_v8bf(phi[j]), o[m][j], 0, 0, 0);
-            }
-        }
+        if (kt + 1 < kt_end) fetch_tile<HD>(img, kt + 1, odd ? tile0 : tile1, tid, wave);
+        tile_update<HD, G, NJ>(a, T, kt, i0, lane, q, st);
     }
 
-    // ---- normalise and store: lane holds columns 16m + 4lg .. +3 of query l16
     float lrow[NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; j++) lrow[j] = xrow_sum(lsum[j]);
-    auto store_out = [&]() {
-        if (a.out_xs) {
-            // quantize_row_q8 of each row: block b of a head is columns
-            // 32b..32b+31, tiles m = 2b (codes 0-15) and 2b+1 (codes 16-31),
-            // 8 values in each of the 4 lanes of the query (lanes l16 + 16 lg);
-            // the absmax as quantize8x4 takes it (|x|, NaN and -0 as 0, an
-            // exact max), then the same scale, inverse and codes as a
-            // separate quantize launch over the stored rows
-            const size_t nrows = (size_t)a.n, cols = (size_t)a.n_q_heads * HD;
-            float *xd = reinterpret_cast<float *>(a.out_xs + nrows * cols);
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                const float inv = 1.0f / lrow[j];
-                const int nt = wave * NJ + j;
-                const int g = nt / S::QT;
-                const int qi = i0 + (nt % S::QT) * 16 + l16;
-#pragma unroll
-                for (int b = 0; b < HD / kQK; b++) {
-                    const v4f x0 = o[2 * b][j] * inv, x1 = o[2 * b + 1][j] * inv;
-                    float m = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float a0 = x0[i] < 0.0f ? -x0[i] : x0[i];
-                        const float a1 = x1[i] < 0.0f ? -x1[i] : x1[i];
-                        m = fmaxf(m, a0 > 0.0f ? a0 : 0.0f);
-                        m = fmaxf(m, a1 > 0.0f ? a1 : 0.0f);
-                    }
-                    m = fmaxf(m, __shfl_xor(m, 16));
-                    m = fmaxf(m, __shfl_xor(m, 32));
-                    const float d = quant_scale(m);
-                    const float qinv = quant_inverse(d);
-                    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        w0 |= quant_code(x0[i], qinv) << (8 * i);
-                        w1 |= quant_code(x1[i], qinv) << (8 * i);
-                    }
-                    if (qi < a.n) {
-                        const size_t gb = (size_t)(kvh * G + g) * (HD / kQK) + b;
-                        *reinterpret_cast<uint32_t *>(a.out_xs + ((2 * gb) * nrows + qi) * 16 + 4 * lg) = w0;
-                        *reinterpret_cast<uint32_t *>(a.out_xs + ((2 * gb + 1) * nrows + qi) * 16 + 4 * lg) = w1;
-                        if (lg == 0) xd[gb * nrows + qi] = d;
-                    }
-                }
-            }
-            return;
-        }
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const float inv = 1.0f / lrow[j];
-            const int nt = wave * NJ + j;
-            const int g = nt / S::QT;
-            const int qi = i0 + (nt % S::QT) * 16 + l16;
-            if (qi < a.n) {
-                float *orow = a.out + ((size_t)qi * a.n_q_heads + (size_t)kvh * G + g) * HD;
-#pragma unroll
-                for (int m = 0; m < S::MT; m++)
-                    *reinterpret_cast<v4f *>(orow + m * 16 + 4 * lg) = o[m][j] * inv;
-            }
-        }
-    };
+    for (int j = 0; j < NJ; j++) lrow[j] = xrow_sum(st.lsum[j]);
     if (nsp == 1) {
-        store_out();
+        store_rows<HD, G, NJ>(a, kvh, i0, wave, lane, st, lrow);
         return;
     }
 
-    // ---- split: the arrival counter first; only the splits that are not the
-    //      last to arrive write their partial rows [RW][HD + 4] (o
-    //      unnormalised, m, l) and then count themselves on a second counter
+    // ---- split: every segment writes its partial rows [RW][HD + 4] (o
+    //      unnormalised, m, l) with agent-coherent stores, waits for them,
+    //      then arrives; the last to arrive merges all of them in segment
+    //      order (its own from registers) and puts the counter back to 0.
+    //      Nothing waits on another work-group.
     constexpr int PS = HD + 4;
     const size_t pblock = ((size_t)kvh * a.qblocks + blk) * a.nsp;
     const __amdgpu_buffer_rsrc_t prs =
         __builtin_amdgcn_make_buffer_rsrc(a.partials + pblock * S::RW * PS, 0, nsp * S::RW * PS * 4, 0x00020000);
     int *counter = a.counters + ((size_t)kvh * a.qblocks + blk) * kCounterStrideP;
-    int *ready = counter + kCounterStrideP / 2;   // a line of its own
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int r = (wave * NJ + j) * 16 + l16;
+        const int base = (sp * S::RW + r) * PS;
+#pragma unroll
+        for (int m = 0; m < S::MT; m++)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, st.o[m][j]), prs,
+                                                   (base + m * 16 + 4 * lg) * 4, 0, kCoherentP);
+        if (lg == 0) {
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(st.mrow[j]), prs, (base + HD) * 4, 0, kCoherentP);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lrow[j]), prs, (base + HD + 1) * 4, 0, kCoherentP);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // this thread's partial is at the point of coherence
     int *flag = reinterpret_cast<int *>(tile0);
-    __syncthreads();   // every wave is done with the tile buffers
+    __syncthreads();                 // every thread's partial; every wave done with the tile buffers
     if (tid == 0) *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsp - 1;
     __syncthreads();
-    if (!*flag) {
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const int r = (wave * NJ + j) * 16 + l16;
-            const int base = (sp * S::RW + r) * PS;
-#pragma unroll
-            for (int m = 0; m < S::MT; m++)
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[m][j]), prs,
-                                                       (base + m * 16 + 4 * lg) * 4, 0, kCoherentP);
-            if (lg == 0) {
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(mrow[j]), prs, (base + HD) * 4, 0, kCoherentP);
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lrow[j]), prs, (base + HD + 1) * 4, 0,
-                                                      kCoherentP);
-            }
-        }
-        __builtin_amdgcn_s_waitcnt(0);   // this thread's partial is at the point of coherence
-        __syncthreads();
-        if (tid == 0) __hip_atomic_fetch_add(ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
-    }
-    // the last to arrive waits for the other nsp - 1 partials: their splits
-    // have arrived, so they are running, and they finish without waiting on
-    // anything; then both counters go back to 0 for the next launch
-    if (tid == 0) {
-        while (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != nsp - 1)
-            __builtin_amdgcn_s_sleep(1);
-        __hip_atomic_store(ready, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
+    if (!*flag) return;
+    if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-    // ---- the last split merges all of them in split order (its own from registers)
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const int r = (wave * NJ + j) * 16 + l16;
@@ -862,10 +937,10 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
             float ms, ls;
             v4f os[S::MT];
             if (s2 == sp) {
-                ms = mrow[j];
+                ms = st.mrow[j];
                 ls = lrow[j];
 #pragma unroll
-                for (int m = 0; m < S::MT; m++) os[m] = o[m][j];
+                for (int m = 0; m < S::MT; m++) os[m] = st.o[m][j];
             } else {
                 ms = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, (base + HD) * 4, 0, kCoherentP));
                 ls = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, (base + HD + 1) * 4, 0, kCoherentP));
@@ -874,25 +949,19 @@ __device__ __forceinline__ void prefill_segment(const PrefillArgs &a, int kvh, i
                     os[m] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
                                                         prs, (base + m * 16 + 4 * lg) * 4, 0, kCoherentP));
             }
-            const float Mn = fmaxf(M, ms);
-            const float fo = __builtin_amdgcn_exp2f(M - Mn);   // 0 while M is -inf
-            const float fs = __builtin_amdgcn_exp2f(ms - Mn);
-#pragma unroll
-            for (int m = 0; m < S::MT; m++) acc[m] = acc[m] * fo + os[m] * fs;
-            L = L * fo + ls * fs;
-            M = Mn;
+            merge_part<S::MT>(M, L, acc, ms, ls, os);
         }
 #pragma unroll
-        for (int m = 0; m < S::MT; m++) o[m][j] = acc[m];
+        for (int m = 0; m < S::MT; m++) st.o[m][j] = acc[m];
         lrow[j] = L;
     }
-    store_out();
+    store_rows<HD, G, NJ>(a, kvh, i0, wave, lane, st, lrow);
 }
 
 template <int HD, int G, int NJ>
 __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
-    using S = PShape<HD, G, NJ>;
     using I = TileImg<HD>;
+    using S = PShape<HD, G, NJ>;
     __shared__ __attribute__((aligned(16))) unsigned char tile0[I::BYTES];
     __shared__ __attribute__((aligned(16))) unsigned char tile1[I::BYTES];
     const int kvh = (int)blockIdx.x % a.n_kv;
@@ -913,6 +982,118 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     }
 }
 
+// Whole query blocks: one work-group of 8 waves per (query block, kv head),
+// longest block first.  The two 4-wave halves cover the same 128 rows and
+// split the block's key tiles, half h taking tiles h, h + 2, h + 4, ...; they
+// step together (one barrier per pair of tiles, each half with its own two
+// LDS buffers, one tile ahead), then half 1 leaves its (o, m, l) in LDS and
+// half 0 merges the two in half order and stores the rows.  No partial leaves
+// the work-group and no work-group waits on another.
+template <int HD, int G, int NJ>
+__global__ __launch_bounds__(2 * kThreads, 1) void prefill_block_kernel(PrefillArgs a) {
+    using S = PShape<HD, G, NJ>;
+    using I = TileImg<HD>;
+    constexpr int MT = S::MT;
+    // tile buffers: half 0 uses 0, 1; half 1 uses 2, 3
+    __shared__ __attribute__((aligned(16))) unsigned char tiles[4][I::BYTES];
+    static_assert(4 * 64 * (MT * NJ * 16 + NJ * 8) <= 4 * I::BYTES, "half 1's rows fit the tile buffers");
+    const int kvh = (int)blockIdx.x % a.n_kv;
+    const int blk = a.qblocks - 1 - (int)blockIdx.x / a.n_kv;
+    const int tid = threadIdx.x;
+    const int half = __builtin_amdgcn_readfirstlane(tid >> 8);
+    const int htid = tid & (kThreads - 1);
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);   // wave within the half
+    const int i0 = blk * S::QB;
+    const unsigned char *img = a.img + (size_t)kvh * a.n_tiles * I::BYTES;
+    const int nt = block_tiles(a.pos0, a.n, S::QB, blk);
+    const int mine = (nt - half + 1) / 2;   // tiles of this half
+    const int steps = (nt + 1) / 2;         // half 0 has the most
+
+    // buffer of this half's step s
+    auto buf = [&](int st_) -> unsigned char * { return tiles[2 * half + (st_ & 1)]; };
+    // ---- the block's staged q rows into buffer 1 (half 0's second; all 8
+    //      waves copy), then each half's first tile into its first buffer;
+    //      waiting for all but this wave's copies of its tile leaves only the
+    //      tile in flight
+    {
+        constexpr int QCH = S::Q_BYTES / 16;
+        const unsigned char *src = a.qimg + ((size_t)kvh * a.qblocks + blk) * S::Q_BYTES;
+        const int wu = __builtin_amdgcn_readfirstlane(tid >> 6);
+        for (int c0 = 64 * wu; c0 < QCH; c0 += 2 * kThreads)
+            if (c0 + lane < QCH) dma16(src + 16 * (c0 + lane), tiles[1] + 16 * c0);
+    }
+    if (mine > 0) {
+        fetch_tile<HD>(img, half, buf(0), htid, wave);
+        if (tile_has_rem<HD>(wave))
+            wait_vm<I::ROUNDS + 1>();
+        else
+            wait_vm<I::ROUNDS>();
+    } else {
+        wait_vm<0>();
+    }
+    __syncthreads();
+
+    PQ<HD, G, NJ> q;
+    load_q<HD, G, NJ>(a, tiles[1], i0, wave, lane, q);
+    PRows<HD, G, NJ> st;
+    st.init();
+
+    // Both halves step together, one barrier per step, each tile's scores
+    // and P.V in its step.  (Running half 1 one part behind, so that each
+    // SIMD's two waves would meet matrix products with vector work, measured
+    // slower: 256 registers, and no overlap gained.)
+    for (int s = 0; s < steps; s++) {
+        // this thread's copies of its half's tile have landed; the barrier
+        // makes every thread's visible and frees the other buffers (the
+        // previous step's tiles, or the q staging) for the next copies
+        asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+        __syncthreads();
+        if (s + 1 < mine) fetch_tile<HD>(img, 2 * (s + 1) + half, buf(s + 1), htid, wave);
+        if (s < mine) tile_update<HD, G, NJ>(a, buf(s), 2 * s + half, i0, lane, q, st);
+    }
+
+    float lrow[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) lrow[j] = xrow_sum(st.lsum[j]);
+    // half 1's rows, lane by lane (the waves of both halves hold the same
+    // rows and columns in the same lanes), into the free tile buffers
+    v4f *ob = reinterpret_cast<v4f *>(&tiles[0][0]);              // [wave][MT][NJ][64]
+    float *mb = reinterpret_cast<float *>(ob + 4 * MT * NJ * 64);  // [wave][NJ][64] x (m, l)
+    __syncthreads();   // every wave is done with the tile buffers
+    if (half == 1) {
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++) ob[((wave * MT + m) * NJ + j) * 64 + lane] = st.o[m][j];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            mb[((wave * NJ + j) * 64 + lane) * 2] = st.mrow[j];
+            mb[((wave * NJ + j) * 64 + lane) * 2 + 1] = lrow[j];
+        }
+    }
+    __syncthreads();
+    if (half == 1) return;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        float M = -INFINITY, L = 0.0f;
+        v4f acc[MT], os[MT];
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            acc[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            os[m] = st.o[m][j];
+        }
+        merge_part<MT>(M, L, acc, st.mrow[j], lrow[j], os);
+#pragma unroll
+        for (int m = 0; m < MT; m++) os[m] = ob[((wave * MT + m) * NJ + j) * 64 + lane];
+        merge_part<MT>(M, L, acc, mb[((wave * NJ + j) * 64 + lane) * 2], mb[((wave * NJ + j) * 64 + lane) * 2 + 1], os);
+#pragma unroll
+        for (int m = 0; m < MT; m++) st.o[m][j] = acc[m];
+        lrow[j] = L;
+    }
+    store_rows<HD, G, NJ>(a, kvh, i0, wave, lane, st, lrow);
+}
+
 // Rows per work-group: 128 (two row tiles per wave) by default;
 // TQ_HIP_PREFILL_ROWS=64 selects one row tile per wave where G allows.
 int prefill_rows(int g) {
@@ -927,17 +1108,36 @@ int prefill_rows(int g) {
 // Query tokens per work-group for a shape (the kernel's QB).
 int prefill_qb(int g) { return 64 * (prefill_rows(g) == 128 ? 2 : 1) / g; }
 
-// Chunk plan: nsp chunks per block pair, the count that minimises the time of
-// the item waves (items of ceil(tp/nsp) tiles each, kItemOverheadTiles extra,
-// resident work-groups at once per wave).
+// With at least two query blocks per CU, every (query block, kv head) is one
+// work-group of prefill_block_kernel (no partials): dealt longest first, the
+// blocks pair up on the CUs by themselves.  With fewer, query blocks are
+// paired last with first and cut into nsp chunks, the count that minimises
+// the time of the item waves (items of ceil(tp/nsp) tiles each,
+// kItemOverheadTiles extra, resident work-groups at once per wave), run by
+// prefill_kernel with split partials.
+constexpr int kCUs = 256;                // compute units of an MI355X
+// TQ_HIP_PREFILL_WHOLE=1|0 forces the whole-block kernel or the paired split
+// one (tests of both at any size); read on every call.  -1: the plan decides.
+int prefill_whole_env() {
+    const char *s = getenv("TQ_HIP_PREFILL_WHOLE");
+    return (s && *s) ? (s[0] == '1' ? 1 : 0) : -1;
+}
 struct PrefillPlan {
     int qblocks, nsp, rows, items;
+    bool whole;                          // prefill_block_kernel
 };
 PrefillPlan plan_prefill(int hd, int g, int n_kv_heads, int pos0, int n) {
     PrefillPlan p;
     const int qb = prefill_qb(g);
     p.rows = 64 * (prefill_rows(g) == 128 ? 2 : 1);
     p.qblocks = (n + qb - 1) / qb;
+    const int forced = prefill_whole_env();
+    p.whole = forced >= 0 ? forced == 1 : (long)p.qblocks * n_kv_heads >= 2L * kCUs;
+    if (p.whole) {
+        p.nsp = 1;
+        p.items = p.qblocks;
+        return p;
+    }
     const int pairs = (p.qblocks + 1) / 2;
     int tp_max = 0;
     for (int q = 0; q < pairs; q++) {
@@ -972,7 +1172,7 @@ size_t qimg_offset(int head_dim, int n_kv_heads, int kend) {
 
 // The staging launch (key tiles and q blocks), then the attention.
 template <int HD, int G, int NJ>
-hipError_t launch_hd_g(const TqPrefillArgs &t, const PrefillArgs &a, hipStream_t s) {
+hipError_t launch_hd_g(const TqPrefillArgs &t, const PrefillArgs &a, bool whole, hipStream_t s) {
     StageArgs st;
     st.view = t.view;
     st.seq = t.seq;
@@ -998,19 +1198,24 @@ hipError_t launch_hd_g(const TqPrefillArgs &t, const PrefillArgs &a, hipStream_t
                        0, s, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int items = (a.qblocks + 1) / 2 * a.nsp;
-    hipLaunchKernelGGL((prefill_kernel<HD, G, NJ>), dim3(items * t.n_kv_heads), dim3(kThreads), 0, s, a);
+    if (whole) {
+        hipLaunchKernelGGL((prefill_block_kernel<HD, G, NJ>), dim3(a.qblocks * t.n_kv_heads), dim3(2 * kThreads), 0,
+                           s, a);
+    } else {
+        const int items = (a.qblocks + 1) / 2 * a.nsp;
+        hipLaunchKernelGGL((prefill_kernel<HD, G, NJ>), dim3(items * t.n_kv_heads), dim3(kThreads), 0, s, a);
+    }
     return hipGetLastError();
 }
 
 template <int HD>
-hipError_t launch_hd(const TqPrefillArgs &t, const PrefillArgs &a, int g, hipStream_t s) {
+hipError_t launch_hd(const TqPrefillArgs &t, const PrefillArgs &a, int g, bool whole, hipStream_t s) {
     const bool wide = prefill_rows(g) == 128;
     switch (g) {
-        case 1: return wide ? launch_hd_g<HD, 1, 2>(t, a, s) : launch_hd_g<HD, 1, 1>(t, a, s);
-        case 2: return wide ? launch_hd_g<HD, 2, 2>(t, a, s) : launch_hd_g<HD, 2, 1>(t, a, s);
-        case 4: return wide ? launch_hd_g<HD, 4, 2>(t, a, s) : launch_hd_g<HD, 4, 1>(t, a, s);
-        case 8: return launch_hd_g<HD, 8, 2>(t, a, s);
+        case 1: return wide ? launch_hd_g<HD, 1, 2>(t, a, whole, s) : launch_hd_g<HD, 1, 1>(t, a, whole, s);
+        case 2: return wide ? launch_hd_g<HD, 2, 2>(t, a, whole, s) : launch_hd_g<HD, 2, 1>(t, a, whole, s);
+        case 4: return wide ? launch_hd_g<HD, 4, 2>(t, a, whole, s) : launch_hd_g<HD, 4, 1>(t, a, whole, s);
+        case 8: return launch_hd_g<HD, 8, 2>(t, a, whole, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -1026,6 +1231,11 @@ bool tq_prefill_mfma_supported(int head_dim, int group, int kend) {
 void tq_prefill_scratch(int head_dim, int group, int n_kv_heads, int pos0, int n, size_t *partial_bytes,
                         size_t *counter_ints) {
     const PrefillPlan p = plan_prefill(head_dim, group, n_kv_heads, pos0, n);
+    if (p.whole || p.nsp == 1) {
+        *partial_bytes = 0;
+        *counter_ints = 0;
+        return;
+    }
     *partial_bytes = (size_t)n_kv_heads * p.qblocks * p.nsp * p.rows * (head_dim + 4) * sizeof(float);
     *counter_ints = (size_t)n_kv_heads * p.qblocks * kCounterStrideP;
 }
@@ -1056,5 +1266,5 @@ hipError_t tq_launch_prefill(const TqPrefillArgs &t, hipStream_t s) {
     a.partials = t.partials;
     a.counters = t.counters;
     if (p.nsp > 1 && (!t.partials || !t.counters)) return hipErrorInvalidValue;
-    return t.head_dim == 64 ? launch_hd<64>(t, a, g, s) : launch_hd<128>(t, a, g, s);
+    return t.head_dim == 64 ? launch_hd<64>(t, a, g, p.whole, s) : launch_hd<128>(t, a, g, p.whole, s);
 }

@@ -543,6 +543,22 @@ PREFILL_SHAPES = [
 def test_prefill(nat, oracle, shape):
     """attention_layer_batch semantics: n tokens stored then attending
     causally; equal to n sequential oracle steps."""
+    check_prefill(nat, oracle, shape)
+
+
+@pytest.mark.parametrize("whole", ["1", "0"])
+@pytest.mark.parametrize("shape", PREFILL_SHAPES[:8])
+def test_prefill_both_plans(nat, oracle, shape, whole, monkeypatch):
+    """The dense shapes through each of the two attention kernels, forced:
+    whole query blocks (one 8-wave work-group per block, its two halves merged
+    in LDS) and the paired, split blocks (partials merged by the last
+    segment).  Both against the oracle's sequential steps, cache bytes
+    bit-exact."""
+    monkeypatch.setenv("TQ_HIP_PREFILL_WHOLE", whole)
+    check_prefill(nat, oracle, shape)
+
+
+def check_prefill(nat, oracle, shape):
     nq, nkv, hd, T, theta, pos0, n = shape
     nb = hd // QK
     kc, vc = blocks(nkv * T * nb), blocks(nkv * T * nb)
