@@ -19,20 +19,12 @@ namespace {
 
 using namespace tq;
 
-__global__ __launch_bounds__(512) void append_kernel(PagedView view, const int32_t *__restrict__ seq_of,
-                                                     const int32_t *__restrict__ pos_of,
-                                                     const float *__restrict__ k,
-                                                     const float *__restrict__ v,
-                                                     const float *__restrict__ cos_t,
-                                                     const float *__restrict__ sin_t, int hd,
-                                                     int seq_const, int pos0) {
-    const int row = blockIdx.x, kvh = blockIdx.y;
-    const int seq = seq_of ? seq_of[row] : seq_const;
-    const int pos = pos_of ? pos_of[row] : pos0 + row;
-    if (pos < 0) return;
-    const int phys = phys_page(view, seq, pos / kPage);
-    if (phys < 0) return;
-
+// One value per thread of row `row`, kv head kvh: K (after RoPE) then V,
+// quantized by 32-lane groups into the cache at position pos.
+__device__ __forceinline__ void append_row(const PagedView &view, int phys, int pos, int row, int kvh,
+                                           const float *__restrict__ k, const float *__restrict__ v,
+                                           const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+                                           int hd) {
     const int e = threadIdx.x;
     const bool is_v = e >= hd;
     const int col = is_v ? e - hd : e;
@@ -48,6 +40,30 @@ __global__ __launch_bounds__(512) void append_kernel(PagedView view, const int32
     unsigned char *dst = head_run_ptr(view, phys, kvh) + (is_v ? view.kv_chunk : 0) +
                          (size_t)(pos % kPage) * view.row_bytes + (size_t)(col >> 5) * kBlockBytes;
     quantize_store32(x, dst);
+}
+
+__global__ __launch_bounds__(512) void append_kernel(PagedView view, const int32_t *__restrict__ seq_of,
+                                                     const int32_t *__restrict__ pos_of,
+                                                     const float *__restrict__ k,
+                                                     const float *__restrict__ v,
+                                                     const float *__restrict__ cos_t,
+                                                     const float *__restrict__ sin_t, int hd,
+                                                     int seq_const, int pos0, unsigned *done,
+                                                     unsigned done_seq) {
+    const int row = blockIdx.x, kvh = blockIdx.y;
+    const int seq = seq_of ? seq_of[row] : seq_const;
+    const int pos = pos_of ? pos_of[row] : pos0 + row;
+    const int phys = pos < 0 ? -1 : phys_page(view, seq, pos / kPage);
+    if (phys >= 0) append_row(view, phys, pos, row, kvh, k, v, cos_t, sin_t, hd);
+    if (done) {
+        // completion flag of (row, kv head) for a host that waits on memory: the
+        // inputs are read and every store of the work-group is acknowledged
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_store(done + (size_t)row * view.n_kv_heads + kvh, done_seq, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+    }
 }
 
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -137,11 +153,12 @@ __global__ __launch_bounds__(kThreads) void append_run_kernel(PagedView view, in
 hipError_t tq_launch_append(const PagedView &view, int n_rows, const int32_t *seq,
                             const int32_t *pos, int seq_const, int pos0, const float *k,
                             const float *v, const float *c, const float *sn, int hd,
-                            hipStream_t s) {
+                            hipStream_t s, unsigned *done, unsigned done_seq) {
     if (n_rows <= 0) return hipSuccess;
     // a run of one sequence with 16-byte aligned inputs: a work-group per page
+    // (completion flags: one work-group per row)
     const bool aligned = (((uintptr_t)k | (uintptr_t)v | (uintptr_t)c | (uintptr_t)sn) & 15) == 0;
-    if (!seq && !pos && aligned && (hd == 64 || hd == 128 || hd == 256) && pos0 >= 0) {
+    if (!done && !seq && !pos && aligned && (hd == 64 || hd == 128 || hd == 256) && pos0 >= 0) {
         const int pages = (pos0 + n_rows - 1) / kPage - pos0 / kPage + 1;
         const dim3 grid(pages, view.n_kv_heads);
         switch (hd) {
@@ -152,6 +169,6 @@ hipError_t tq_launch_append(const PagedView &view, int n_rows, const int32_t *se
         return hipGetLastError();
     }
     hipLaunchKernelGGL(append_kernel, dim3(n_rows, view.n_kv_heads), dim3(2 * hd), 0, s, view, seq,
-                       pos, k, v, c, sn, hd, seq_const, pos0);
+                       pos, k, v, c, sn, hd, seq_const, pos0, done, done_seq);
     return hipGetLastError();
 }

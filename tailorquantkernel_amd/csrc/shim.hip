@@ -881,10 +881,19 @@ int tq_hip_kv_append(tq_hip_kv *kv, int seq, int pos, const float *k, const floa
     pack(kv, os, sin_t, tb);
     rc = inputs_at(kv, st.used, true, &S);
     if (rc != TQ_HIP_OK) return rc;
+    // the host waits on the work-groups' completion flags (raised once the
+    // inputs are read and the rows stored), not on the stream: later work on
+    // kv's stream is ordered after the append either way
+    DoneFlags d = next_done(kv);
+    const bool flags = d.flags && D.n_kv_heads <= kDoneFlags;
     TQ_TRY(tq_launch_append(kv->view, 1, nullptr, nullptr, seq, pos, (const float *)(S + ok_),
                             (const float *)(S + ov), cos_t ? (const float *)(S + oc) : nullptr,
-                            cos_t ? (const float *)(S + os) : nullptr, D.head_dim, s));
-    return herr(hipStreamSynchronize(s));
+                            cos_t ? (const float *)(S + os) : nullptr, D.head_dim, s, flags ? d.flags : nullptr,
+                            d.seq));
+    if (!flags) return herr(hipStreamSynchronize(s));
+    d.count = D.n_kv_heads;
+    d.armed = true;
+    return wait_done(kv, d);
 }
 
 // ---- decode ----------------------------------------------------------------------

@@ -293,10 +293,12 @@ size_t tq_gemm_partial_floats(int rows, int cols, int n_cap);
 hipError_t tq_launch_rmsnorm_rows(const float *x, const float *w, float *out, int n_rows, int n, float eps,
                                   hipStream_t s);
 // seq null: every row goes to seq_const; pos null: row r goes to pos0 + r.
+// done non-null: each (row, kv head) work-group raises done[row * n_kv + kvh] =
+// done_seq at system scope once its inputs are read and its stores acknowledged.
 hipError_t tq_launch_append(const tq::PagedView &view, int n_rows, const int32_t *seq,
                             const int32_t *pos, int seq_const, int pos0, const float *k,
                             const float *v, const float *c, const float *sn, int hd,
-                            hipStream_t s);
+                            hipStream_t s, unsigned *done = nullptr, unsigned done_seq = 0);
 // Tokens per sub-chunk of the decode kernel for a head_dim.
 int tq_decode_tsub(int head_dim);
 // Upper bounds of n_splits (for a head_dim and group size) and of
