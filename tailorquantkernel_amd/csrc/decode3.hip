@@ -105,7 +105,8 @@ struct Smem3 {
     using L = L3<HD, G>;
     unsigned char newrow[2 * L::ROW];        // step mode: the new token's K, V
     int pages[kMaxSplitPages3];              // physical page of each page of the split
-    int qlen[kSortQ];                        // the batch's lengths, for the longest-first order
+    int qlen[kSortQ];                        // the batch's lengths and sequences, for the
+    int qseq[kSortQ];                        // longest-first order
     int qsel;
     float wts[G * kMaxSplits3];              // combine weights
     int last;
@@ -253,11 +254,20 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
     // short ones fill the gaps at the end (longest-processing-time order).
     // Each query's result does not depend on the order.
     int qi = blockIdx.z;
+    // (the query's raw length and sequence, when the ranking below reads them)
+    bool ranked = false;
+    int len_rk = 0, seq_rk = 0;
     if (a.n_q > 1) {
         if (!a.len_of) {
             qi = a.n_q - 1 - (int)blockIdx.z;   // query i attends pos0 + i + 1 keys
         } else if (a.n_q <= kSortQ) {
-            for (int i = tid; i < a.n_q; i += kThreads) sm.qlen[i] = a.len_of[i];
+            // the batch's lengths (and sequences) through LDS, ranked by one
+            // thread per query; the chosen query's length and sequence are
+            // then read from LDS, not loaded again
+            for (int i = tid; i < a.n_q; i += kThreads) {
+                sm.qlen[i] = a.len_of[i];
+                sm.qseq[i] = a.seq_of ? a.seq_of[i] : 0;
+            }
             __syncthreads();
             for (int i = tid; i < a.n_q; i += kThreads) {
                 const int li = sm.qlen[i];
@@ -270,9 +280,14 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
             }
             __syncthreads();
             qi = sm.qsel;
+            ranked = true;
         }
     }
     qi = __builtin_amdgcn_readfirstlane(qi);
+    if (ranked) {
+        len_rk = __builtin_amdgcn_readfirstlane(sm.qlen[qi]);
+        seq_rk = __builtin_amdgcn_readfirstlane(sm.qseq[qi]);
+    }
     const int t_begin = split * a.split_tokens;
     const int split_end = t_begin + a.split_tokens;
     const PagedView &view = a.view;
@@ -284,8 +299,8 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
     // Uniform inputs: issued first as unconditional scalar loads (a dummy
     // address when absent), used only after the copies below are issued, so
     // the copies do not wait for them.
-    const int len_raw = *(a.len_of ? a.len_of + qi : reinterpret_cast<const int32_t *>(a.q));
-    const int seq_raw = *(a.seq_of ? a.seq_of + qi : reinterpret_cast<const int32_t *>(a.q));
+    const int len_raw = ranked ? len_rk : *(a.len_of ? a.len_of + qi : reinterpret_cast<const int32_t *>(a.q));
+    const int seq_raw = ranked ? seq_rk : *(a.seq_of ? a.seq_of + qi : reinterpret_cast<const int32_t *>(a.q));
 
     // ---- 1. this wave's copy of the inputs it quantizes, into the tail-free
     //      front of its second slot: q rows of the group | cos | sin | new K | new V
