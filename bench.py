@@ -548,7 +548,7 @@ def step_floor(nat, hip, stream, bufs, nbytes, n_heads, reps, n_splits=32):
     lib = bench_lib()
     scratch = nat.DeviceBuffer(lib.tq_hip_floor_scratch_bytes(n_heads, n_splits))
     zeros = np.zeros(n_heads * 64, np.int32)   # held until the copy has read it
-    nat.check(lib.tq_hip_memcpy_h2d(scratch.ptr, zeros.ctypes.data, zeros.nbytes, None), "zero counters")
+    nat.check(nat.load().tq_hip_memcpy_h2d(scratch.ptr, zeros.ctypes.data, zeros.nbytes, None), "zero counters")
     out = nat.DeviceBuffer(lib.tq_hip_floor_out_bytes(n_heads, n_splits))
     res = {}
     for mode, key in ((0, "launch_us"), (1, "read_us"), (2, "read_combine_us")):
