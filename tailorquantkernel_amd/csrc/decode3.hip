@@ -264,9 +264,13 @@ __global__ __launch_bounds__(64 * W) void decode3_kernel(TqDecodeArgs a) {
             // the batch's lengths (and sequences) through LDS, ranked by one
             // thread per query; the chosen query's length and sequence are
             // then read from LDS, not loaded again
+            // both loads issued before either is waited for (a missing
+            // sequence array reads the lengths again and stores 0)
             for (int i = tid; i < a.n_q; i += kThreads) {
-                sm.qlen[i] = a.len_of[i];
-                sm.qseq[i] = a.seq_of ? a.seq_of[i] : 0;
+                const int li = a.len_of[i];
+                const int si = (a.seq_of ? a.seq_of : a.len_of)[i];
+                sm.qlen[i] = li;
+                sm.qseq[i] = a.seq_of ? si : 0;
             }
             __syncthreads();
             for (int i = tid; i < a.n_q; i += kThreads) {
