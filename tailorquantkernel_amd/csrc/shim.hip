@@ -5,6 +5,7 @@
 // TQ_HIP_EHIP_BASE - hipError_t.
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include <algorithm>
 #include <mutex>
@@ -329,15 +330,30 @@ DoneFlags next_done(tq_hip_kv *kv) {
 
 // Until every armed flag holds the call's value, or the stream has drained
 // (flags a query never raises, e.g. one with nothing to attend) or failed.
+// The stream is asked only once the flags are late (kLateUs after the wait
+// began, then every kLateUs): hipStreamQuery costs about as much as the call
+// it would check, and asked every few hundred spins it landed inside calls
+// whose flags come 6-9 us after launch (store_kv_device 9 -> 20 us).
+constexpr double kLateUs = 25.0;
+double now_us() {
+    timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return (double)t.tv_sec * 1e6 + (double)t.tv_nsec * 1e-3;
+}
 int wait_done(tq_hip_kv *kv, const DoneFlags &d) {
+    double ask_at = now_us() + kLateUs;
     for (unsigned it = 1;; it++) {
         bool all = true;
         for (int i = 0; i < d.count && all; i++) all = __atomic_load_n(d.flags + i, __ATOMIC_ACQUIRE) == d.seq;
         if (all) return TQ_HIP_OK;
         __builtin_ia32_pause();   // a spin-wait hint to the core, not a yield
-        if ((it & 255u) == 0) {
-            const hipError_t e = hipStreamQuery(kv->stream);
-            if (e != hipErrorNotReady) return herr(e);
+        if ((it & 63u) == 0) {
+            const double t = now_us();
+            if (t >= ask_at) {
+                const hipError_t e = hipStreamQuery(kv->stream);
+                if (e != hipErrorNotReady) return herr(e);
+                ask_at = t + kLateUs;
+            }
         }
     }
 }
