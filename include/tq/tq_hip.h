@@ -11,7 +11,9 @@
  *     visible in host memory, which may be before the cache's stream has
  *     drained (the kernel's last waves may still be retiring); work enqueued
  *     next on that stream is still ordered after it.  The host thread spins
- *     (with a pause hint, not a yield) while it waits;
+ *     (with a pause hint, not a yield) while it waits, and asks the stream
+ *     for its status only once the flags are 25 us late, so that a device
+ *     error still ends the wait;
  *   - *_async ones take DEVICE buffers and a stream (hipStream_t as void*,
  *     NULL = the cache's own stream) and only enqueue work.
  *
